@@ -1,0 +1,286 @@
+"""Benchmark of the MI355X oracle path; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
+                    [--no-configs] [--no-cpu] [--copy-calibration MIB]
+
+Headline: BASELINE config 2 (per-channel bias + GELU-tanh, bf16 NCHW ->
+NHWC [128,256,56,56]); a step is one oracle_forward over one batch.  Inputs
+are resident in HBM before timing starts.  R rotating input/output sets
+(together >= 1 GiB, four times the 256 MB Infinity Cache) are each captured
+in a hipGraph; step k replays graph k % R, so no step reads its inputs from
+the cache a previous step left warm.  Exactly K steps are timed between two
+device synchronisations (wall clock) and, on the launch stream, between two
+hipEvents (kernel time).
+
+value   = algorithmic bytes per step / (wall ms per step)   [GB/s]
+roofline.achieved = algorithmic bytes / (event time / K)    [GB/s]
+cpu_baseline = the CPU oracle (oracle/hipo_ref.c, OpenMP) on the same
+               workload on the host cores.
+configs = every BASELINE config timed through oracle_harness.bench_oracle
+          (hipGraph replay, cache flush between replays, min of 5 rounds),
+          with the eager repro on the host CPU beside it.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "better-benchmark_amd"
+for _p in (str(PKG), str(ROOT)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+CANONICAL = PKG / "repros" / "canonical"
+HEADLINE = "pointwise_bias_gelu_tanh_nhwc"
+ALL_CONFIGS = [
+    ("1", "mean_lastdim_f32"),
+    ("2", "pointwise_bias_gelu_tanh_nhwc"),
+    ("3", "amax_sum_scaled_masked_softmax"),
+    ("4a", "var_mean_residual_layernorm"),
+    ("4b", "mean_rmsnorm"),
+    ("5", "var_mean_batchnorm_train_relu"),
+]
+WORKLOAD = {
+    "mean_lastdim_f32": "config1 row mean fp32 [8192,4096]",
+    "pointwise_bias_gelu_tanh_nhwc": "config2 bias+gelu_tanh bf16 NCHW->NHWC [128,256,56,56]",
+    "amax_sum_scaled_masked_softmax": "config3 scaled causal-masked softmax bf16 [384,1024,1024]",
+    "var_mean_residual_layernorm": "config4a residual-add LayerNorm bf16 [16384,4096]",
+    "mean_rmsnorm": "config4b RMSNorm bf16 [16384,4096]",
+    "var_mean_batchnorm_train_relu": "config5 BatchNorm-train fwd+ReLU fp32 [128,256,56,56]",
+}
+DTYPE = {
+    "mean_lastdim_f32": "f32", "pointwise_bias_gelu_tanh_nhwc": "bf16",
+    "amax_sum_scaled_masked_softmax": "bf16", "var_mean_residual_layernorm": "bf16",
+    "mean_rmsnorm": "bf16", "var_mean_batchnorm_train_relu": "f32",
+}
+METRIC = "achieved HBM GB/s and % of 8 TB/s SOL per kernel; µs vs host-CPU eager"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _baseline_point(rid):
+    from repro_harness import load_shape_configs
+    cfgs = load_shape_configs(str(CANONICAL / rid / "repro.py"))
+    label, cfg = next(iter(cfgs.items()))
+    return label, cfg
+
+
+def _cpu_oracle_call(rid, cpu_inputs, threads):
+    import oracle as ref
+    if rid == "mean_lastdim_f32":
+        return lambda: ref.row_mean(cpu_inputs[0], threads=threads)
+    if rid == "pointwise_bias_gelu_tanh_nhwc":
+        return lambda: ref.bias_gelu_nchw_to_nhwc(*cpu_inputs, threads=threads)
+    if rid == "amax_sum_scaled_masked_softmax":
+        return lambda: ref.scaled_masked_softmax(cpu_inputs[0], cpu_inputs[1], 0.125, threads=threads)
+    if rid == "var_mean_residual_layernorm":
+        return lambda: ref.residual_layernorm(*cpu_inputs, 1e-5, threads=threads)
+    if rid == "mean_rmsnorm":
+        return lambda: ref.rmsnorm(*cpu_inputs, 1e-5, threads=threads)
+    return lambda: ref.batchnorm_train(*cpu_inputs, momentum=0.1, eps=1e-5, threads=threads)
+
+
+def cpu_baseline(rid, cpu_inputs, nbytes, budget_s: float = 10.0) -> dict:
+    """CPU oracle on the host cores: min over repeated full-workload runs
+    within ~budget_s of wall time (at least 2 runs)."""
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    fn = _cpu_oracle_call(rid, cpu_inputs, threads)
+    fn()  # warm (page-in, thread pool)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    best = min(times)
+    return {"value": round(nbytes / best / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"full {WORKLOAD[rid]} workload, min of {len(times)} runs "
+                      f"({best * 1e3:.1f} ms each) of oracle/hipo_ref.c, OpenMP",
+            "us": round(best * 1e6, 1)}
+
+
+def headline(rid, steps, warmup, want_cpu):
+    import torch
+    import oracle_harness as oh
+    from byte_accounting import HBM_PEAK_BYTES_PER_S
+    from repro_harness import make_inputs_from_config
+
+    dev = torch.device("cuda:0")
+    label, cfg = _baseline_point(rid)
+    mod, fn, d = oh._load_oracle_module(CANONICAL / rid)
+    instance = oh.get_repro_instance(d)
+    oh._seed_input_generation(1)
+    cpu_inputs = make_inputs_from_config(cfg, device="cpu")
+    nbytes = oh.effective_bytes(instance, cpu_inputs)
+    impl, info = oh.resolve_oracle(fn, [t.to("meta") if isinstance(t, torch.Tensor) else t
+                                        for t in cpu_inputs])
+    per_set = sum(t.numel() * t.element_size() for t in cpu_inputs if isinstance(t, torch.Tensor))
+    per_set += nbytes  # outputs are of the same order
+    sets = max(2, math.ceil((1 << 30) / max(per_set, 1)))
+    sets = min(sets, 16)
+    log(f"{rid}: {label}, {nbytes} algorithmic bytes/step, {sets} rotating sets")
+
+    input_sets = []
+    for s in range(sets):
+        input_sets.append([t.to(dev) if isinstance(t, torch.Tensor) else t for t in cpu_inputs])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    graphs = []
+    for s in range(sets):
+        for _ in range(2):
+            impl(input_sets[s])
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            impl(input_sets[s])
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for k in range(warmup):
+        graphs[k % sets].replay()
+    torch.cuda.synchronize()
+
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    with oh._gpu_exclusive_lock(f"bench:{rid}"):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        for k in range(steps):
+            graphs[k % sets].replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    event_s = ev0.elapsed_time(ev1) / 1e3
+    ms_per_step = wall / steps * 1e3
+    kernel_s = event_s / steps
+    peak = HBM_PEAK_BYTES_PER_S["MI355X"]
+    achieved = nbytes / kernel_s
+    result = {
+        "ms_per_step": round(ms_per_step, 4),
+        "value": round(nbytes / (wall / steps) / 1e9, 1),
+        "nbytes": nbytes,
+        "label": label,
+        "dispatch": info and {"matched": info["matched"], "tuned_on": info["tuned_hardware"]},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved / 1e9, 1),
+            "peak": peak / 1e9,
+            "unit": "GB/s",
+            "frac": round(achieved / peak, 4),
+            "traffic": None,
+            "kernel_us": round(kernel_s * 1e6, 2),
+        },
+        "rotating_sets": sets,
+    }
+    del graphs, input_sets
+    torch.cuda.synchronize()
+    if want_cpu:
+        log("cpu baseline (CPU oracle)")
+        result["cpu_baseline"] = cpu_baseline(rid, cpu_inputs, nbytes)
+    return result
+
+
+def per_config(want_cpu):
+    import torch
+    import oracle_harness as oh
+    from repro_harness import make_inputs_from_config
+    out = []
+    for tag, rid in ALL_CONFIGS:
+        label, cfg = _baseline_point(rid)
+        log(f"config {tag}: {rid}")
+        mod, fn, d = oh._load_oracle_module(CANONICAL / rid)
+        oh._seed_input_generation(1)
+        inputs = make_inputs_from_config(cfg, device="cuda")
+        r = oh.bench_oracle(fn, oh.get_repro_instance(d), inputs, f"{rid}_{label}",
+                            warmup=10, rep=100, rounds=5, compare_compile=False,
+                            cpu_eager=want_cpu)
+        entry = {"config": tag, "repro": rid, "status": r.get("status"),
+                 "us": r.get("oracle_us"), "median_us": r.get("oracle_median_us"),
+                 "bytes": r.get("bytes"), "gbps": r.get("gbps"), "sol_frac": r.get("sol_frac")}
+        gate = r.get("numerics_gate")
+        if gate is not None:
+            entry["numerics_gate_pass"] = gate.get("pass")
+        for k in ("cpu_eager_us", "cpu_threads", "cpu_model"):
+            if k in r:
+                entry[k] = r[k]
+        out.append(entry)
+        del inputs
+        torch.cuda.empty_cache()
+    return out
+
+
+def copy_calibration(mib: int, reps: int = 20) -> None:
+    """A plain device copy of known size, for scaling rocprof byte counters."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4, "reps": reps}))
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default=HEADLINE, help="repro id of the headline workload")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config table")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py runs on one GPU only: this build has no multi-GPU path "
+              "(each MI355X box here has one GPU). Use --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs the ROCm device", file=sys.stderr)
+        return 2
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return 0
+    import hip_oracles
+    hip_oracles.load_library()
+
+    rid = args.config
+    h = headline(rid, args.steps, args.warmup, not args.no_cpu)
+    line = {
+        "metric": METRIC,
+        "value": h["value"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": h["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DTYPE[rid],
+        "data": "synthetic (seeded N(mu, sigma) inputs of the BASELINE config)",
+        "config": {"workload": WORKLOAD[rid], "repro": rid, "point": h["label"],
+                   "bytes_per_step": h["nbytes"], "rotating_sets": h["rotating_sets"],
+                   "parallelism": "single-gpu"},
+        "roofline": h["roofline"],
+        "cpu_baseline": h.get("cpu_baseline"),
+    }
+    if not args.no_configs:
+        line["configs"] = per_config(not args.no_cpu)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

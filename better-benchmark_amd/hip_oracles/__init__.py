@@ -1,0 +1,258 @@
+"""MI355X (gfx950) kernel library for better-benchmark's oracle API.
+
+`libhip_oracles.so` (built by hip_oracles/build.py from csrc/*.hip) exports
+the C ABI declared in include/hip_oracles.h.  This module opens it with
+ctypes and wraps each entry point in a torch-facing function that checks
+the operands on the host, allocates outputs with torch, and launches on
+torch's current HIP stream (so calls are capturable by torch.cuda.graph).
+
+There is no fallback: if the library is missing or a tensor is not on a
+ROCm device, the wrappers raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import threading
+from pathlib import Path
+
+import torch  # imported before the .so so the process has one HIP runtime
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libhip_oracles.so"
+HEADER_PATH = PKG_DIR.parents[1] / "include" / "hip_oracles.h"
+ABI_VERSION = 1
+
+_c_i64 = ctypes.c_int64
+_c_ptr = ctypes.c_void_p
+_c_f32 = ctypes.c_float
+
+# Signatures of every exported symbol (mirrors include/hip_oracles.h).
+_SIGNATURES = {
+    "hipo_abi_version": (ctypes.c_int, []),
+    "hipo_last_error": (ctypes.c_char_p, []),
+    "hipo_row_mean_f32": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr]),
+    "hipo_bias_gelu_nchw_to_nhwc_bf16": (
+        ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr]),
+    "hipo_scaled_masked_softmax_bf16": (
+        ctypes.c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _c_ptr]),
+    "hipo_residual_layernorm_bf16": (
+        ctypes.c_int,
+        [_c_ptr] * 8 + [_c_i64, _c_i64, _c_f32, _c_ptr]),
+    "hipo_rmsnorm_bf16": (
+        ctypes.c_int, [_c_ptr] * 4 + [_c_i64, _c_i64, _c_f32, _c_ptr]),
+    "hipo_batchnorm_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
+    "hipo_batchnorm_train_fwd_f32": (
+        ctypes.c_int,
+        [_c_ptr] * 8 + [_c_i64, _c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int,
+                        _c_ptr, ctypes.c_size_t, _c_ptr]),
+}
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+class HipOraclesUnavailable(RuntimeError):
+    """libhip_oracles.so is missing or unusable."""
+
+
+def header_symbols(header: Path = HEADER_PATH) -> list[str]:
+    """Names of the functions include/hip_oracles.h declares."""
+    text = header.read_text()
+    return sorted(set(re.findall(r"\b(hipo_[a-z0-9_]+)\s*\(", text)))
+
+
+def load_library(path: str | Path | None = None):
+    """Open (once) and return the ctypes handle; raises if unavailable."""
+    global _lib
+    with _lib_lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise HipOraclesUnavailable(
+                f"{p} not found: build it with "
+                f"`python better-benchmark_amd/hip_oracles/build.py` "
+                f"(or __graft_entry__.build())")
+        lib = ctypes.CDLL(str(p))
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        got = lib.hipo_abi_version()
+        if got != ABI_VERSION:
+            raise HipOraclesUnavailable(
+                f"{p}: ABI version {got}, expected {ABI_VERSION}")
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = _lib.hipo_last_error().decode(errors="replace") if _lib else ""
+        raise RuntimeError(f"hip_oracles.{what} failed (code {rc}): {msg}")
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _require_rocm(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        _require(isinstance(t, torch.Tensor), "expected tensors")
+        _require(t.device.type == "cuda",
+                 f"hip_oracles runs on the ROCm device only, got a {t.device} tensor")
+        _require(t.device == dev, "all operands must be on one device")
+    _require(torch.version.hip is not None, "torch is not a ROCm build")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# Op wrappers
+# ---------------------------------------------------------------------------
+
+def row_mean(x: torch.Tensor) -> torch.Tensor:
+    """fp32 mean over the last dim of a 2-D fp32 tensor -> [rows]."""
+    lib = load_library()
+    dev = _require_rocm(x)
+    _require(x.dtype == torch.float32 and x.dim() == 2, "row_mean: x must be 2-D fp32")
+    _require(x.stride(1) == 1 or x.shape[1] <= 1, "row_mean: last dim must be contiguous")
+    rows, cols = x.shape
+    out = torch.empty(rows, dtype=torch.float32, device=dev)
+    row_stride = x.stride(0) if rows > 1 else cols
+    with torch.cuda.device(dev):
+        _check(lib.hipo_row_mean_f32(_ptr(x), _ptr(out), rows, cols,
+                                     max(row_stride, cols), _stream(dev)),
+               "row_mean")
+    return out
+
+
+def bias_gelu_nchw_to_nhwc(x: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """gelu_tanh(x + bias[None,:,None,None]) written channels-last (bf16)."""
+    lib = load_library()
+    dev = _require_rocm(x, bias)
+    _require(x.dtype == torch.bfloat16 and bias.dtype == torch.bfloat16,
+             "bias_gelu: bf16 operands required")
+    _require(x.dim() == 4 and x.is_contiguous(), "bias_gelu: x must be contiguous NCHW")
+    n, c, h, w = x.shape
+    _require(bias.shape == (c,) and bias.is_contiguous(), "bias_gelu: bias must be [C]")
+    out = torch.empty((n, c, h, w), dtype=torch.bfloat16, device=dev,
+                      memory_format=torch.channels_last)
+    with torch.cuda.device(dev):
+        _check(lib.hipo_bias_gelu_nchw_to_nhwc_bf16(_ptr(x), _ptr(bias), _ptr(out),
+                                                    n, c, h * w, _stream(dev)),
+               "bias_gelu_nchw_to_nhwc")
+    return out
+
+
+def scaled_masked_softmax(x: torch.Tensor, mask: torch.Tensor, scale: float) -> torch.Tensor:
+    """softmax(x * scale + mask, -1) for bf16 x [B, Q, K], mask [Q, K]."""
+    lib = load_library()
+    dev = _require_rocm(x, mask)
+    _require(x.dtype == torch.bfloat16 and mask.dtype == torch.bfloat16,
+             "masked_softmax: bf16 operands required")
+    _require(x.dim() == 3 and x.is_contiguous(), "masked_softmax: x must be contiguous [B,Q,K]")
+    b, q, k = x.shape
+    _require(mask.dim() == 2 and tuple(mask.shape) == (q, k) and mask.stride(1) == 1,
+             "masked_softmax: mask must be [Q, K] with unit inner stride")
+    mstride = mask.stride(0) if q > 1 else k
+    out = torch.empty_like(x)
+    with torch.cuda.device(dev):
+        _check(lib.hipo_scaled_masked_softmax_bf16(_ptr(x), _ptr(mask), _ptr(out),
+                                                   b, q, k, max(mstride, k),
+                                                   float(scale), _stream(dev)),
+               "scaled_masked_softmax")
+    return out
+
+
+def residual_layernorm(x, residual, gamma, beta, eps: float):
+    """(h, y, mean, rstd) of LayerNorm(x + residual) over the last dim."""
+    lib = load_library()
+    dev = _require_rocm(x, residual, gamma, beta)
+    for t in (x, residual, gamma, beta):
+        _require(t.dtype == torch.bfloat16 and t.is_contiguous(),
+                 "residual_layernorm: contiguous bf16 operands required")
+    _require(x.dim() == 2 and residual.shape == x.shape, "residual_layernorm: x, residual [R, C]")
+    rows, cols = x.shape
+    _require(gamma.shape == (cols,) and beta.shape == (cols,), "residual_layernorm: gamma/beta [C]")
+    h = torch.empty_like(x)
+    y = torch.empty_like(x)
+    mean = torch.empty(rows, dtype=torch.float32, device=dev)
+    rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib.hipo_residual_layernorm_bf16(
+            _ptr(x), _ptr(residual), _ptr(gamma), _ptr(beta), _ptr(h), _ptr(y),
+            _ptr(mean), _ptr(rstd), rows, cols, float(eps), _stream(dev)),
+            "residual_layernorm")
+    return h, y, mean, rstd
+
+
+def rmsnorm(x, gamma, eps: float):
+    """(y, rstd) of RMSNorm(x) over the last dim."""
+    lib = load_library()
+    dev = _require_rocm(x, gamma)
+    for t in (x, gamma):
+        _require(t.dtype == torch.bfloat16 and t.is_contiguous(),
+                 "rmsnorm: contiguous bf16 operands required")
+    _require(x.dim() == 2, "rmsnorm: x must be [R, C]")
+    rows, cols = x.shape
+    _require(gamma.shape == (cols,), "rmsnorm: gamma must be [C]")
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib.hipo_rmsnorm_bf16(_ptr(x), _ptr(gamma), _ptr(y), _ptr(rstd),
+                                     rows, cols, float(eps), _stream(dev)),
+               "rmsnorm")
+    return y, rstd
+
+
+def batchnorm_workspace_bytes(n: int, c: int, hw: int) -> int:
+    return int(load_library().hipo_batchnorm_workspace_bytes(n, c, hw))
+
+
+def batchnorm_train(x, gamma, beta, running_mean, running_var, *, momentum: float,
+                    eps: float, relu: bool = True, workspace: torch.Tensor | None = None):
+    """(y, save_mean, save_invstd); running_mean/var are updated in place."""
+    lib = load_library()
+    dev = _require_rocm(x, gamma, beta, running_mean, running_var)
+    _require(x.dim() == 4 and x.dtype == torch.float32 and x.is_contiguous(),
+             "batchnorm: x must be contiguous NCHW fp32")
+    n, c, h, w = x.shape
+    for t in (gamma, beta, running_mean, running_var):
+        _require(t.dtype == torch.float32 and t.shape == (c,) and t.is_contiguous(),
+                 "batchnorm: gamma/beta/running stats must be contiguous fp32 [C]")
+    need = int(lib.hipo_batchnorm_workspace_bytes(n, c, h * w))
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    _require(workspace.device == dev and workspace.numel() * workspace.element_size() >= need,
+             "batchnorm: workspace too small")
+    y = torch.empty_like(x)
+    save_mean = torch.empty(c, dtype=torch.float32, device=dev)
+    save_invstd = torch.empty(c, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib.hipo_batchnorm_train_fwd_f32(
+            _ptr(x), _ptr(gamma), _ptr(beta), _ptr(running_mean), _ptr(running_var),
+            _ptr(y), _ptr(save_mean), _ptr(save_invstd), n, c, h * w,
+            float(momentum), float(eps), 1 if relu else 0,
+            _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(dev)),
+            "batchnorm_train")
+    return y, save_mean, save_invstd
+
+
+__all__ = [
+    "HipOraclesUnavailable", "LIB_PATH", "load_library", "header_symbols",
+    "row_mean", "bias_gelu_nchw_to_nhwc", "scaled_masked_softmax",
+    "residual_layernorm", "rmsnorm", "batchnorm_workspace_bytes", "batchnorm_train",
+]

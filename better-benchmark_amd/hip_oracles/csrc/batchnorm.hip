@@ -1,0 +1,314 @@
+// BatchNorm training forward, fp32 NCHW: per-channel statistics over
+// (N, H, W), normalisation + affine (+ ReLU), running-stat update.
+//
+// Split-K structure (two launches on the caller's stream):
+//   1. bn_partial_stats: grid (S, C).  Workgroup (s, c) reduces the planes
+//      n in [s*N/S, (s+1)*N/S) of channel c to a Welford triple
+//      (count, mean, M2) and writes it to the workspace.  Inside the
+//      workgroup each thread reduces its slice of every plane exactly
+//      (two-pass over registers) and merges it into a running triple with
+//      Chan's formula; threads then merge across the wave with DPP and
+//      across waves through LDS.
+//   2. bn_normalize: grid (S, C).  Every workgroup of channel c merges the S
+//      triples of that channel (Chan, fp64, fixed order), derives
+//      mean / invstd, and writes y = relu?(x * alpha + beta') for its planes
+//      with alpha = invstd * gamma, beta' = beta - mean * alpha.  Workgroup
+//      (0, c) also writes save_mean / save_invstd and updates the running
+//      statistics (unbiased variance, count / (count - 1)).
+// This version reads x twice (once per launch).
+#include "hipo_common.h"
+
+namespace hipo {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWavesPerBlock = kThreads / kWave;
+
+struct Welford {
+  float n;
+  float mean;
+  float m2;
+};
+
+// max(v, 0) that keeps NaN (torch.relu propagates NaN; fmaxf would not).
+__device__ __forceinline__ float relu_f32(float v) { return v < 0.f ? 0.f : v; }
+
+// Chan et al. pairwise merge of two Welford triples.
+__device__ __forceinline__ Welford merge(Welford a, Welford b) {
+  const float n = a.n + b.n;
+  if (n == 0.f) return a;
+  const float wb = b.n / n;
+  const float d = b.mean - a.mean;
+  Welford r;
+  r.n = n;
+  r.mean = __builtin_fmaf(d, wb, a.mean);
+  r.m2 = a.m2 + b.m2 + d * d * a.n * wb;
+  return r;
+}
+
+template <int Ctrl>
+__device__ __forceinline__ Welford dpp_w(Welford w) {
+  return Welford{dpp<Ctrl>(w.n), dpp<Ctrl>(w.mean), dpp<Ctrl>(w.m2)};
+}
+
+__device__ __forceinline__ Welford lane_w(Welford w, int lane) {
+  return Welford{
+      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w.n), lane)),
+      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w.mean), lane)),
+      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w.m2), lane))};
+}
+
+// Whole-wave merge (all 64 lanes active); every lane gets the result.
+// Each step merges triples over disjoint lane sets.
+__device__ __forceinline__ Welford wave_welford(Welford w) {
+  w = merge(w, dpp_w<kDppQuadXor1>(w));
+  w = merge(w, dpp_w<kDppQuadXor2>(w));
+  w = merge(w, dpp_w<kDppRowRor4>(w));
+  w = merge(w, dpp_w<kDppRowRor8>(w));
+  return merge(merge(lane_w(w, 0), lane_w(w, 16)),
+               merge(lane_w(w, 32), lane_w(w, 48)));
+}
+
+// Exact statistics of up to 4*U values held by one thread, merged into acc.
+template <int U>
+__device__ __forceinline__ void absorb(Welford& acc, const float4 (&v)[U],
+                                       const bool (&ok)[U]) {
+  float cnt = 0.f, s = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (ok[u]) {
+      cnt += 4.f;
+      s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+    }
+  }
+  if (cnt == 0.f) return;
+  const float m = s / cnt;
+  float q = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (ok[u]) {
+      const float a = v[u].x - m, b = v[u].y - m, c = v[u].z - m, d = v[u].w - m;
+      q += (a * a + b * b) + (c * c + d * d);
+    }
+  }
+  acc = merge(acc, Welford{cnt, m, q});
+}
+
+// Planes handled by split s of S over N planes.
+__device__ __forceinline__ void split_range(int64_t N, int64_t S, int64_t s,
+                                            int64_t& n0, int64_t& n1) {
+  n0 = (N * s) / S;
+  n1 = (N * (s + 1)) / S;
+}
+
+__global__ __launch_bounds__(kThreads) void bn_partial_stats_vec(
+    const float* __restrict__ x, float* __restrict__ ws, int64_t N, int64_t C,
+    int64_t HW, int64_t S) {
+  constexpr int U = 4;
+  const int64_t s = blockIdx.x;
+  const int64_t c = blockIdx.y;
+  int64_t n0, n1;
+  split_range(N, S, s, n0, n1);
+  const int64_t hw4 = HW / 4;
+  Welford acc{0.f, 0.f, 0.f};
+  for (int64_t n = n0; n < n1; ++n) {
+    const float4* plane = reinterpret_cast<const float4*>(x + (n * C + c) * HW);
+    for (int64_t base = 0; base < hw4; base += kThreads * U) {
+      float4 v[U];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = base + u * kThreads + threadIdx.x;
+        ok[u] = i < hw4;
+        v[u] = ok[u] ? plane[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      absorb<U>(acc, v, ok);
+    }
+  }
+  acc = wave_welford(acc);
+  __shared__ Welford part[kWavesPerBlock];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Welford t = merge(merge(part[0], part[1]), merge(part[2], part[3]));
+    float* dst = ws + (c * S + s) * 3;
+    dst[0] = t.n;
+    dst[1] = t.mean;
+    dst[2] = t.m2;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void bn_partial_stats_scalar(
+    const float* __restrict__ x, float* __restrict__ ws, int64_t N, int64_t C,
+    int64_t HW, int64_t S) {
+  const int64_t s = blockIdx.x;
+  const int64_t c = blockIdx.y;
+  int64_t n0, n1;
+  split_range(N, S, s, n0, n1);
+  Welford acc{0.f, 0.f, 0.f};
+  for (int64_t n = n0; n < n1; ++n) {
+    const float* plane = x + (n * C + c) * HW;
+    for (int64_t i = threadIdx.x; i < HW; i += kThreads) {
+      acc = merge(acc, Welford{1.f, plane[i], 0.f});
+    }
+  }
+  acc = wave_welford(acc);
+  __shared__ Welford part[kWavesPerBlock];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Welford t = merge(merge(part[0], part[1]), merge(part[2], part[3]));
+    float* dst = ws + (c * S + s) * 3;
+    dst[0] = t.n;
+    dst[1] = t.mean;
+    dst[2] = t.m2;
+  }
+}
+
+// Merge the S partial triples of channel c in fp64, fixed order.
+__device__ void channel_stats(const float* __restrict__ ws, int64_t c,
+                              int64_t S, double& mean, double& m2,
+                              double& count) {
+  double n = 0.0, mu = 0.0, q = 0.0;
+  for (int64_t s = 0; s < S; ++s) {
+    const float* p = ws + (c * S + s) * 3;
+    const double nb = p[0], mb = p[1], qb = p[2];
+    const double nn = n + nb;
+    if (nn == 0.0) continue;
+    const double d = mb - mu;
+    mu += d * (nb / nn);
+    q += qb + d * d * n * (nb / nn);
+    n = nn;
+  }
+  mean = mu;
+  m2 = q;
+  count = n;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void bn_normalize(
+    const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float* __restrict__ running_mean,
+    float* __restrict__ running_var, float* __restrict__ y,
+    float* __restrict__ save_mean, float* __restrict__ save_invstd,
+    const float* __restrict__ ws, int64_t N, int64_t C, int64_t HW, int64_t S,
+    float momentum, float eps, int relu) {
+  const int64_t s = blockIdx.x;
+  const int64_t c = blockIdx.y;
+  __shared__ float coef[2];
+  if (threadIdx.x == 0) {
+    double mean, m2, count;
+    channel_stats(ws, c, S, mean, m2, count);
+    const float meanf = static_cast<float>(mean);
+    const float var = static_cast<float>(m2 / count);
+    const float invstd = 1.0f / __builtin_sqrtf(var + eps);
+    const float alpha = invstd * gamma[c];
+    coef[0] = alpha;
+    coef[1] = beta[c] - meanf * alpha;
+    if (s == 0) {
+      save_mean[c] = meanf;
+      save_invstd[c] = invstd;
+      const double unbiased = count > 1.0 ? m2 / (count - 1.0)
+                                          : __builtin_nan("");
+      const double mom = momentum;
+      running_mean[c] = static_cast<float>(mom * mean +
+                                           (1.0 - mom) * running_mean[c]);
+      running_var[c] = static_cast<float>(mom * unbiased +
+                                          (1.0 - mom) * running_var[c]);
+    }
+  }
+  __syncthreads();
+  const float alpha = coef[0];
+  const float shift = coef[1];
+  int64_t n0, n1;
+  split_range(N, S, s, n0, n1);
+  for (int64_t n = n0; n < n1; ++n) {
+    const int64_t off = (n * C + c) * HW;
+    if (VEC) {
+      const float4* src = reinterpret_cast<const float4*>(x + off);
+      float4* dst = reinterpret_cast<float4*>(y + off);
+      for (int64_t i = threadIdx.x; i < HW / 4; i += kThreads) {
+        float4 v = src[i];
+        v.x = __builtin_fmaf(v.x, alpha, shift);
+        v.y = __builtin_fmaf(v.y, alpha, shift);
+        v.z = __builtin_fmaf(v.z, alpha, shift);
+        v.w = __builtin_fmaf(v.w, alpha, shift);
+        if (relu) {
+          v.x = relu_f32(v.x);
+          v.y = relu_f32(v.y);
+          v.z = relu_f32(v.z);
+          v.w = relu_f32(v.w);
+        }
+        dst[i] = v;
+      }
+    } else {
+      for (int64_t i = threadIdx.x; i < HW; i += kThreads) {
+        float v = __builtin_fmaf(x[off + i], alpha, shift);
+        if (relu) v = relu_f32(v);
+        y[off + i] = v;
+      }
+    }
+  }
+}
+
+// Number of plane splits per channel for the split-K launches.
+int64_t num_splits(int64_t n, int64_t c) {
+  const int64_t target_blocks = 4096;
+  int64_t s = (target_blocks + c - 1) / c;
+  if (s > n) s = n;
+  if (s < 1) s = 1;
+  return s;
+}
+
+}  // namespace
+}  // namespace hipo
+
+extern "C" size_t hipo_batchnorm_workspace_bytes(int64_t n, int64_t c,
+                                                 int64_t hw) {
+  if (n <= 0 || c <= 0 || hw <= 0) return 0;
+  const int64_t s = hipo::num_splits(n, c);
+  return static_cast<size_t>(c * s * 3) * sizeof(float);
+}
+
+extern "C" int hipo_batchnorm_train_fwd_f32(
+    const float* x, const float* gamma, const float* beta, float* running_mean,
+    float* running_var, float* y, float* save_mean, float* save_invstd,
+    int64_t n, int64_t c, int64_t hw, float momentum, float eps, int relu,
+    void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  HIPO_REQUIRE(n > 0 && c > 0 && hw > 0, "batchnorm: sizes must be positive");
+  HIPO_REQUIRE(x && gamma && beta && running_mean && running_var && y &&
+                   save_mean && save_invstd && workspace,
+               "batchnorm: null pointer");
+  const size_t need = hipo_batchnorm_workspace_bytes(n, c, hw);
+  HIPO_REQUIRE(workspace_bytes >= need,
+               "batchnorm: workspace %zu bytes < required %zu", workspace_bytes,
+               need);
+  HIPO_REQUIRE(c <= 65535, "batchnorm: too many channels");
+  const int64_t S = num_splits(n, c);
+  const dim3 grid(static_cast<unsigned>(S), static_cast<unsigned>(c));
+  float* ws = static_cast<float*>(workspace);
+  const bool vec = hw % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(y) % 16 == 0;
+  if (vec) {
+    bn_partial_stats_vec<<<grid, dim3(kThreads), 0, stream>>>(x, ws, n, c, hw, S);
+  } else {
+    bn_partial_stats_scalar<<<grid, dim3(kThreads), 0, stream>>>(x, ws, n, c, hw,
+                                                                 S);
+  }
+  int rc = check_launch("batchnorm_train_fwd_f32 (stats)");
+  if (rc) return rc;
+  if (vec) {
+    bn_normalize<true><<<grid, dim3(kThreads), 0, stream>>>(
+        x, gamma, beta, running_mean, running_var, y, save_mean, save_invstd,
+        ws, n, c, hw, S, momentum, eps, relu);
+  } else {
+    bn_normalize<false><<<grid, dim3(kThreads), 0, stream>>>(
+        x, gamma, beta, running_mean, running_var, y, save_mean, save_invstd,
+        ws, n, c, hw, S, momentum, eps, relu);
+  }
+  return check_launch("batchnorm_train_fwd_f32 (normalize)");
+}

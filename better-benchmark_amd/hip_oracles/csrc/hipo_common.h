@@ -1,0 +1,119 @@
+// Shared device helpers and host-side error plumbing for libhip_oracles.
+//
+// Written for gfx950 (CDNA4): wave64, 16-byte global loads/stores, DPP
+// cross-lane reductions, hardware bf16 conversion (v_cvt_pk_bf16_f32).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "hip_oracles.h"
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting (thread-local message; see hipo_last_error()).
+// ---------------------------------------------------------------------------
+namespace hipo {
+
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// Properties of the current device, cached per device on first use.
+struct DeviceInfo {
+  int device;
+  int cu_count;          // multiProcessorCount
+  int max_threads_per_cu;
+  size_t lds_per_block;  // sharedMemPerBlock
+};
+const DeviceInfo* device_info();
+
+// Map the result of a kernel launch onto the ABI's return convention.
+int check_launch(const char* what);
+
+}  // namespace hipo
+
+#define HIPO_REQUIRE(cond, ...)          \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::hipo::set_error(__VA_ARGS__);    \
+      return HIPO_EINVAL;                \
+    }                                    \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Device helpers.
+// ---------------------------------------------------------------------------
+namespace hipo {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+// bf16 bits held in the low / high half of a 32-bit word -> fp32 (exact).
+__device__ __forceinline__ float bf16lo(uint32_t w) {
+  return __uint_as_float(w << 16);
+}
+__device__ __forceinline__ float bf16hi(uint32_t w) {
+  return __uint_as_float(w & 0xffff0000u);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Two fp32 -> one word of two bf16 (round to nearest even, NaN stays NaN):
+// a single v_cvt_pk_bf16_f32 on gfx950.  `lo` lands in bits 0..15.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  float2_t v = {lo, hi};
+  bf16x2_t b = __builtin_convertvector(v, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, b);
+}
+
+// fp32 -> fp32 value rounded through bf16 (what an eager bf16 op stores).
+__device__ __forceinline__ float round_bf16(float v) {
+  return bf16lo(pack_bf16x2(v, 0.0f));
+}
+
+// DPP controls (GFX9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;  // row_ror:4
+constexpr int kDppRowRor8 = 0x128;  // row_ror:8
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(
+      0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+
+// Full-wave sum; every lane receives the same value.  All 64 lanes must be
+// active.  Order is fixed (DPP butterflies within each 16-lane row, then
+// (row0 + row1) + (row2 + row3)), so results are deterministic.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<kDppQuadXor1>(v);
+  v += dpp<kDppQuadXor2>(v);
+  v += dpp<kDppRowRor4>(v);
+  v += dpp<kDppRowRor8>(v);
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+
+// Full-wave max; every lane receives the same value (all lanes active).
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp<kDppRowRor4>(v));
+  v = fmaxf(v, dpp<kDppRowRor8>(v));
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+}  // namespace hipo

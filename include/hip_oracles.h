@@ -1,0 +1,152 @@
+/*
+ * hip_oracles.h -- C ABI of libhip_oracles.so, the MI355X (gfx950) kernel
+ * library behind the gfx950 oracle registrations.
+ *
+ * In better-benchmark an oracle is `oracle_forward(inputs, **cfg)` in a
+ * canonical repro's oracle.py, registered with `@oracle_impl(...)`
+ * (reference: oracle_harness.py:468-549); its body launches Triton kernels.
+ * Each entry point below replaces one such body: the Python oracle
+ * allocates the outputs with torch, then calls here with raw device pointers,
+ * sizes and the caller's HIP stream.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers.  bf16 tensors are passed as uint16_t*
+ *     (raw bfloat16 bit patterns).  Tensors are dense and row-major
+ *     (contiguous) unless a stride argument says otherwise.
+ *   - `stream` is the caller's stream (torch.cuda.current_stream()); every
+ *     launch goes on it.  Calls only enqueue work: no allocation, no
+ *     synchronisation, no host<->device copies, so they are safe under
+ *     hipStreamBeginCapture / torch.cuda.graph.
+ *   - Return 0 on success.  Non-zero is a hipError_t from the launch, or
+ *     HIPO_EINVAL (argument check failed before anything was launched).
+ *     hipo_last_error() then holds a message (per calling thread).
+ *   - Re-entrant.  The only global state is a per-device cache of device
+ *     properties, filled on first use.
+ */
+#ifndef HIP_ORACLES_H_
+#define HIP_ORACLES_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HIPO_ABI_VERSION 1
+#define HIPO_EINVAL 1000
+
+/* ABI version of the loaded library (HIPO_ABI_VERSION at build time). */
+int hipo_abi_version(void);
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* hipo_last_error(void);
+
+/*
+ * Row mean: out[r] = mean(x[r, 0:cols]) in fp32.
+ * x is [rows, cols] with row stride `row_stride` elements (>= cols).
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/mean_c9e1a8113328/oracle.py:95 (_spatial_mean_row_kernel,
+ * same file :45) for the row-reduction form `x.mean(dim=-1)`.
+ */
+int hipo_row_mean_f32(const float* x, float* out, int64_t rows, int64_t cols,
+                      int64_t row_stride, hipStream_t stream);
+
+/*
+ * Channel bias + GELU(tanh) + NCHW -> NHWC:
+ *   t = x[n,c,hw] + bias[c];  y = 0.5 t (1 + tanh(sqrt(2/pi) (t + 0.044715 t^3)))
+ *   out[n,hw,c] = bf16(y)     (fp32 arithmetic, one rounding to bf16)
+ * x is contiguous NCHW [n, c, hw]; out is the same logical tensor stored
+ * channels-last (physical [n, hw, c]).
+ * Replaces the Triton bodies of oracle_forward in
+ * repros/canonical/pointwise_2d969ac9ad59/oracle.py:47 (tanh GELU) and
+ * repros/canonical/pointwise_021e90d9c17d/oracle.py:58 (permute + clone),
+ * fused into one pass.
+ */
+int hipo_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x, const uint16_t* bias,
+                                     uint16_t* out, int64_t n, int64_t c,
+                                     int64_t hw, hipStream_t stream);
+
+/*
+ * Scaled, additively masked softmax over the last dim (bf16 in/out):
+ *   s[b,q,k] = bf16(bf16(x[b,q,k] * scale) + mask[q,k])
+ *   out[b,q,:] = bf16(softmax_fp32(s[b,q,:]))
+ * x/out are [batch, q, k] contiguous; mask is [q, k] with row stride
+ * `mask_row_stride` elements, broadcast over batch.
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/amax_sum_20ccc18dda60/oracle.py:63
+ * (_broadcast_add_softmax_kernel, same file :12).
+ */
+int hipo_scaled_masked_softmax_bf16(const uint16_t* x, const uint16_t* mask,
+                                    uint16_t* out, int64_t batch, int64_t q,
+                                    int64_t k, int64_t mask_row_stride,
+                                    float scale, hipStream_t stream);
+
+/*
+ * Residual add + LayerNorm forward over the last dim (bf16 in/out):
+ *   h = bf16(x + residual);  mean, var = fp32 stats of h (population var)
+ *   rstd = 1/sqrt(var + eps);  y = bf16((h - mean) * rstd * gamma + beta)
+ * x, residual, h, y are [rows, cols] contiguous; gamma, beta are [cols];
+ * mean, rstd are fp32 [rows].
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/var_mean_80e7ff4dee7f/oracle.py:122
+ * (_residual_layernorm_kernel, same file :51).
+ */
+int hipo_residual_layernorm_bf16(const uint16_t* x, const uint16_t* residual,
+                                 const uint16_t* gamma, const uint16_t* beta,
+                                 uint16_t* h, uint16_t* y, float* mean,
+                                 float* rstd, int64_t rows, int64_t cols,
+                                 float eps, hipStream_t stream);
+
+/*
+ * RMSNorm forward over the last dim (bf16 in/out):
+ *   rstd = 1/sqrt(mean(x^2) + eps)   (fp32)
+ *   y = bf16(x * rstd * gamma)       (fp32 arithmetic, one rounding)
+ * x, y are [rows, cols] contiguous; gamma is [cols]; rstd is fp32 [rows].
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/mean_4462ce967d63/oracle.py:65.
+ */
+int hipo_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma, uint16_t* y,
+                      float* rstd, int64_t rows, int64_t cols, float eps,
+                      hipStream_t stream);
+
+/*
+ * Bytes of device workspace hipo_batchnorm_train_fwd_f32 needs for this
+ * shape (0 if the shape is unsupported).
+ */
+size_t hipo_batchnorm_workspace_bytes(int64_t n, int64_t c, int64_t hw);
+
+/*
+ * BatchNorm training forward over dims (0, 2, 3) of NCHW fp32, fused with
+ * the affine transform, an optional ReLU and the running-stat update:
+ *   mean[c], var[c] = population stats of x[:, c, :]   (correction 0)
+ *   save_mean = mean;  save_invstd = 1/sqrt(var + eps)
+ *   y = relu?((x - mean) * save_invstd * gamma + beta)
+ *   running_mean = (1 - momentum) running_mean + momentum mean
+ *   running_var  = (1 - momentum) running_var
+ *                  + momentum var * count / (count - 1)     (in place)
+ * x, y are contiguous [n, c, hw]; gamma, beta, running_*, save_* are [c].
+ * `workspace` is caller-allocated device memory of at least
+ * hipo_batchnorm_workspace_bytes(n, c, hw) bytes; its contents on entry do
+ * not matter.
+ * Replaces the Triton bodies of oracle_forward in
+ * repros/canonical/var_mean_mean_19ffdb35cc67/oracle.py:167 (one CTA per
+ * channel) and repros/canonical/var_mean_ceb5c315290a/oracle.py:238
+ * (split-K sum/sum-of-squares, then an epilogue that re-reads x).
+ */
+int hipo_batchnorm_train_fwd_f32(const float* x, const float* gamma,
+                                 const float* beta, float* running_mean,
+                                 float* running_var, float* y,
+                                 float* save_mean, float* save_invstd,
+                                 int64_t n, int64_t c, int64_t hw,
+                                 float momentum, float eps, int relu,
+                                 void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* HIP_ORACLES_H_ */

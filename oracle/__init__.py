@@ -1,0 +1,146 @@
+"""CPU oracle for the six HIP kernels -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this package, and only as the checker (or as the timed CPU baseline),
+never as the thing shipped: the product path (hip_oracles) has no CPU
+fallback and fails loudly without its HIP library.
+
+The arithmetic lives in oracle/hipo_ref.c (compiled by oracle/build.py);
+this module passes torch CPU tensors to it through ctypes.  Each function
+restates the eager semantics of one repro module; see hipo_ref.c for the
+reference files it follows.  How each function is pinned (closed forms,
+brute force, ATen eager, golden fixtures) is in tests/test_oracle_pins.py.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "_build" / "libhipo_ref.so"
+
+_lib = None
+
+_i64 = ctypes.c_int64
+_p = ctypes.c_void_p
+_f = ctypes.c_float
+_i = ctypes.c_int
+
+_SIGS = {
+    "ref_abi_version": (_i, []),
+    "ref_max_threads": (_i, []),
+    "ref_row_mean_f32": (None, [_p, _p, _i64, _i64, _i]),
+    "ref_bias_gelu_nchw_to_nhwc_bf16": (None, [_p, _p, _p, _i64, _i64, _i64, _i, _i]),
+    "ref_scaled_masked_softmax_bf16": (None, [_p, _p, _p, _i64, _i64, _i64, _i64, _f, _i]),
+    "ref_residual_layernorm_bf16": (None, [_p] * 8 + [_i64, _i64, _f, _i]),
+    "ref_rmsnorm_bf16": (None, [_p] * 4 + [_i64, _i64, _f, _i]),
+    "ref_batchnorm_train_f32": (None, [_p] * 8 + [_i64, _i64, _i64, _f, _f, _i, _i]),
+}
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            from oracle.build import build
+            build()
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def default_threads() -> int:
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    return max(1, min(os.cpu_count() or 1, 16))
+
+
+def _cpu(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    assert t.dtype == dtype, f"expected {dtype}, got {t.dtype}"
+    return t.detach().to("cpu").contiguous()
+
+
+def _th(threads):
+    return default_threads() if threads is None else int(threads)
+
+
+def row_mean(x: torch.Tensor, threads=None) -> torch.Tensor:
+    x = _cpu(x, torch.float32)
+    rows, cols = x.shape
+    out = torch.empty(rows, dtype=torch.float32)
+    load().ref_row_mean_f32(x.data_ptr(), out.data_ptr(), rows, cols, _th(threads))
+    return out
+
+
+def bias_gelu_nchw_to_nhwc(x, bias, *, round_t: bool = False, threads=None):
+    x = _cpu(x, torch.bfloat16)
+    bias = _cpu(bias, torch.bfloat16)
+    n, c, h, w = x.shape
+    out = torch.empty((n, c, h, w), dtype=torch.bfloat16, memory_format=torch.channels_last)
+    load().ref_bias_gelu_nchw_to_nhwc_bf16(x.data_ptr(), bias.data_ptr(), out.data_ptr(),
+                                           n, c, h * w, 1 if round_t else 0, _th(threads))
+    return out
+
+
+def scaled_masked_softmax(x, mask, scale: float, threads=None):
+    x = _cpu(x, torch.bfloat16)
+    mask = _cpu(mask, torch.bfloat16)
+    b, q, k = x.shape
+    assert tuple(mask.shape) == (q, k)
+    out = torch.empty_like(x)
+    load().ref_scaled_masked_softmax_bf16(x.data_ptr(), mask.data_ptr(), out.data_ptr(),
+                                          b, q, k, k, float(scale), _th(threads))
+    return out
+
+
+def residual_layernorm(x, residual, gamma, beta, eps: float, threads=None):
+    x, residual = _cpu(x, torch.bfloat16), _cpu(residual, torch.bfloat16)
+    gamma, beta = _cpu(gamma, torch.bfloat16), _cpu(beta, torch.bfloat16)
+    rows, cols = x.shape
+    h, y = torch.empty_like(x), torch.empty_like(x)
+    mean = torch.empty(rows, dtype=torch.float32)
+    rstd = torch.empty(rows, dtype=torch.float32)
+    load().ref_residual_layernorm_bf16(
+        x.data_ptr(), residual.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
+        h.data_ptr(), y.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+        rows, cols, float(eps), _th(threads))
+    return h, y, mean, rstd
+
+
+def rmsnorm(x, gamma, eps: float, threads=None):
+    x, gamma = _cpu(x, torch.bfloat16), _cpu(gamma, torch.bfloat16)
+    rows, cols = x.shape
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, dtype=torch.float32)
+    load().ref_rmsnorm_bf16(x.data_ptr(), gamma.data_ptr(), y.data_ptr(), rstd.data_ptr(),
+                            rows, cols, float(eps), _th(threads))
+    return y, rstd
+
+
+def batchnorm_train(x, gamma, beta, running_mean, running_var, *, momentum: float,
+                    eps: float, relu: bool = True, threads=None):
+    """Returns (y, save_mean, save_invstd, running_mean', running_var').
+
+    The running statistics are updated on CPU copies, which are returned.
+    """
+    x = _cpu(x, torch.float32)
+    gamma, beta = _cpu(gamma, torch.float32), _cpu(beta, torch.float32)
+    rm = _cpu(running_mean, torch.float32).clone()
+    rv = _cpu(running_var, torch.float32).clone()
+    n, c, h, w = x.shape
+    y = torch.empty_like(x)
+    sm = torch.empty(c, dtype=torch.float32)
+    si = torch.empty(c, dtype=torch.float32)
+    load().ref_batchnorm_train_f32(
+        x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), rm.data_ptr(), rv.data_ptr(),
+        y.data_ptr(), sm.data_ptr(), si.data_ptr(), n, c, h * w,
+        float(momentum), float(eps), 1 if relu else 0, _th(threads))
+    return y, sm, si, rm, rv

@@ -1,0 +1,245 @@
+/*
+ * CPU restatement of the six oracle patterns -- TEST INFRASTRUCTURE ONLY.
+ *
+ * This file is the checker, never the product: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ * The product path is libhip_oracles.so and has no CPU fallback.
+ *
+ * Semantics follow the eager PyTorch graphs of the build's repro modules,
+ * which restate the reference's canonical repros:
+ *   row mean            repros/canonical/mean_c9e1a8113328/repro.py:26
+ *   bias + GELU(tanh)   repros/canonical/pointwise_2d969ac9ad59/repro.py:23-36
+ *   NCHW -> NHWC        repros/canonical/pointwise_021e90d9c17d/repro.py:26-28
+ *   masked softmax      repros/canonical/amax_sum_192a3a5bd7ff/repro.py:23-44
+ *   residual LayerNorm  repros/canonical/var_mean_80e7ff4dee7f/repro.py:23-39
+ *   RMSNorm             repros/canonical/mean_4462ce967d63/repro.py:23-38
+ *   BatchNorm train     repros/canonical/var_mean_mean_19ffdb35cc67/repro.py:23-54
+ * (paths relative to the reference tree).  Every rounding that the eager
+ * graph performs on a bf16 tensor is reproduced (float arithmetic, then
+ * round-to-nearest-even to bf16); reductions and transcendental functions
+ * are evaluated in double, so the restatement is at least as accurate as
+ * eager fp32.  Results are returned as float / bf16 bits like the kernels.
+ *
+ * Build: oracle/build.py (gcc -O2 -fopenmp, no fast-math).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static inline float bf16_to_f32(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, sizeof f);
+  return f;
+}
+
+/* Round-to-nearest-even fp32 -> bf16; NaN stays a (quiet) NaN. */
+static inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, sizeof u);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static inline float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+int ref_abi_version(void) { return 1; }
+
+int ref_max_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* out[r] = mean(x[r, :]) ; fp64 accumulation. */
+void ref_row_mean_f32(const float* x, float* out, int64_t rows, int64_t cols,
+                      int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* p = x + r * cols;
+    double s = 0.0;
+    for (int64_t j = 0; j < cols; ++j) s += p[j];
+    out[r] = (float)(s / (double)cols);
+  }
+}
+
+static inline double gelu_tanh(double t) {
+  const double k = 0.7978845608028654; /* sqrt(2/pi) */
+  return 0.5 * t * (1.0 + tanh(k * (t + 0.044715 * t * t * t)));
+}
+
+/*
+ * out (NHWC, bf16 bits) = bf16(gelu_tanh(t)), t = x[n,c,hw] + bias[c].
+ * round_t != 0 rounds t to bf16 first (what eager's bf16 add stores).
+ */
+void ref_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x, const uint16_t* bias,
+                                     uint16_t* out, int64_t n, int64_t c,
+                                     int64_t hw, int round_t, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static) collapse(2)
+  for (int64_t i = 0; i < n; ++i) {
+    for (int64_t p = 0; p < hw; ++p) {
+      uint16_t* o = out + (i * hw + p) * c;
+      for (int64_t ch = 0; ch < c; ++ch) {
+        float t = bf16_to_f32(x[(i * c + ch) * hw + p]) + bf16_to_f32(bias[ch]);
+        if (round_t) t = round_bf16(t);
+        o[ch] = f32_to_bf16((float)gelu_tanh((double)t));
+      }
+    }
+  }
+}
+
+/*
+ * s = bf16(bf16(x * scale) + mask[q, :]); out = bf16(softmax(s)) with the
+ * max, exp and sum in fp64.  x/out [batch, q, k]; mask row stride in
+ * elements.
+ */
+void ref_scaled_masked_softmax_bf16(const uint16_t* x, const uint16_t* mask,
+                                    uint16_t* out, int64_t batch, int64_t q,
+                                    int64_t k, int64_t mask_stride, float scale,
+                                    int threads) {
+  const int64_t rows = batch * q;
+  if (k <= 0) return;
+#pragma omp parallel num_threads(threads)
+  {
+    double* s = (double*)malloc(sizeof(double) * (size_t)k); /* per thread */
+#pragma omp for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+      const uint16_t* xr = x + r * k;
+      const uint16_t* mr = mask + (r % q) * mask_stride;
+      double m = -INFINITY;
+      for (int64_t j = 0; j < k; ++j) {
+        const float a = round_bf16(bf16_to_f32(xr[j]) * scale);
+        const float v = round_bf16(a + bf16_to_f32(mr[j]));
+        s[j] = v;
+        if (isnan(v) || isnan(m)) {
+          m = NAN; /* amax propagates NaN */
+        } else if (v > m) {
+          m = v;
+        }
+      }
+      double sum = 0.0;
+      for (int64_t j = 0; j < k; ++j) {
+        s[j] = exp(s[j] - m);
+        sum += s[j];
+      }
+      uint16_t* o = out + r * k;
+      for (int64_t j = 0; j < k; ++j) o[j] = f32_to_bf16((float)(s[j] / sum));
+    }
+    free(s);
+  }
+}
+
+/*
+ * h = bf16(x + residual); mean, var (population) of h in fp64;
+ * rstd = 1/sqrt(var + eps); y = bf16((h - mean) * rstd * gamma + beta).
+ */
+void ref_residual_layernorm_bf16(const uint16_t* x, const uint16_t* res,
+                                 const uint16_t* gamma, const uint16_t* beta,
+                                 uint16_t* h, uint16_t* y, float* mean_out,
+                                 float* rstd_out, int64_t rows, int64_t cols,
+                                 float eps, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t base = r * cols;
+    double s = 0.0;
+    for (int64_t j = 0; j < cols; ++j) {
+      const uint16_t hb = f32_to_bf16(bf16_to_f32(x[base + j]) + bf16_to_f32(res[base + j]));
+      h[base + j] = hb;
+      s += bf16_to_f32(hb);
+    }
+    const double mean = s / (double)cols;
+    double q = 0.0;
+    for (int64_t j = 0; j < cols; ++j) {
+      const double d = bf16_to_f32(h[base + j]) - mean;
+      q += d * d;
+    }
+    const double rstd = 1.0 / sqrt(q / (double)cols + (double)eps);
+    for (int64_t j = 0; j < cols; ++j) {
+      const double v = (bf16_to_f32(h[base + j]) - mean) * rstd *
+                           bf16_to_f32(gamma[j]) + bf16_to_f32(beta[j]);
+      y[base + j] = f32_to_bf16((float)v);
+    }
+    mean_out[r] = (float)mean;
+    rstd_out[r] = (float)rstd;
+  }
+}
+
+/* rstd = 1/sqrt(mean(x^2) + eps); y = bf16(x * rstd * gamma). */
+void ref_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma, uint16_t* y,
+                      float* rstd_out, int64_t rows, int64_t cols, float eps,
+                      int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t base = r * cols;
+    double q = 0.0;
+    for (int64_t j = 0; j < cols; ++j) {
+      const double v = bf16_to_f32(x[base + j]);
+      q += v * v;
+    }
+    const double rstd = 1.0 / sqrt(q / (double)cols + (double)eps);
+    for (int64_t j = 0; j < cols; ++j) {
+      const double v = bf16_to_f32(x[base + j]) * rstd * bf16_to_f32(gamma[j]);
+      y[base + j] = f32_to_bf16((float)v);
+    }
+    rstd_out[r] = (float)rstd;
+  }
+}
+
+/*
+ * BatchNorm training forward over (N, H, W) of NCHW fp32, fp64 statistics:
+ *   save_mean = mean; save_invstd = 1/sqrt(var + eps)   (var: correction 0)
+ *   y = relu?((x - mean) * invstd * gamma + beta)
+ *   running_mean = (1 - m) running_mean + m mean
+ *   running_var  = (1 - m) running_var  + m var * cnt / (cnt - 1)
+ */
+void ref_batchnorm_train_f32(const float* x, const float* gamma,
+                             const float* beta, float* running_mean,
+                             float* running_var, float* y, float* save_mean,
+                             float* save_invstd, int64_t n, int64_t c,
+                             int64_t hw, float momentum, float eps, int relu,
+                             int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t ch = 0; ch < c; ++ch) {
+    const double cnt = (double)n * (double)hw;
+    double s = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+      const float* p = x + (i * c + ch) * hw;
+      for (int64_t j = 0; j < hw; ++j) s += p[j];
+    }
+    const double mean = s / cnt;
+    double q = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+      const float* p = x + (i * c + ch) * hw;
+      for (int64_t j = 0; j < hw; ++j) {
+        const double d = p[j] - mean;
+        q += d * d;
+      }
+    }
+    const double var = q / cnt;
+    const double invstd = 1.0 / sqrt(var + (double)eps);
+    const double g = gamma[ch], b = beta[ch];
+    for (int64_t i = 0; i < n; ++i) {
+      const float* p = x + (i * c + ch) * hw;
+      float* o = y + (i * c + ch) * hw;
+      for (int64_t j = 0; j < hw; ++j) {
+        double v = (p[j] - mean) * invstd * g + b;
+        if (relu && !(v > 0.0)) v = isnan(v) ? v : 0.0;
+        o[j] = (float)v;
+      }
+    }
+    save_mean[ch] = (float)mean;
+    save_invstd[ch] = (float)invstd;
+    const double mom = momentum;
+    const double unbiased = cnt > 1.0 ? q / (cnt - 1.0) : NAN;
+    running_mean[ch] = (float)(mom * mean + (1.0 - mom) * running_mean[ch]);
+    running_var[ch] = (float)(mom * unbiased + (1.0 - mom) * running_var[ch]);
+  }
+}

@@ -1,0 +1,305 @@
+"""GPU parity: every HIP kernel against the CPU oracle and the eager repro.
+
+Inputs are generated on the CPU (seed 1, the harness's oracle seed) and
+copied to the device, so all three see identical data.  Tolerances (from
+the BASELINE north star):
+  fp32 outputs (means, rstd, BN y / stats / running stats): rtol = atol = 1e-5
+  bf16 outputs (fp32 accumulation inside):                  rtol = atol = 1.6e-2
+Integer/index work: none on this path.
+"""
+import importlib.util
+import math
+
+import pytest
+import torch
+
+from conftest import CANONICAL, REPRO_IDS
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_TOL = 1.6e-2
+
+
+def _tol(t):
+    return BF16_TOL if t.dtype == torch.bfloat16 else F32_TOL
+
+
+def assert_close(got, want, tol, what):
+    g = got.detach().float().cpu()
+    w = want.detach().float().cpu()
+    assert g.shape == w.shape, f"{what}: shape {tuple(g.shape)} != {tuple(w.shape)}"
+    ok = torch.allclose(g, w, rtol=tol, atol=tol, equal_nan=True)
+    if not ok:
+        d = (g - w).abs().nan_to_num(0)
+        idx = int(d.argmax())
+        pytest.fail(f"{what}: max |diff| {d.max().item():.3e} at flat {idx} "
+                    f"(got {g.flatten()[idx].item()}, want {w.flatten()[idx].item()}), tol {tol}")
+
+
+def _load(rid):
+    import oracle_harness
+    mod, fn, d = oracle_harness._load_oracle_module(CANONICAL / rid)
+    return fn, oracle_harness.get_repro_instance(d)
+
+
+def _points(rid):
+    from repro_harness import load_shape_configs
+    return load_shape_configs(str(CANONICAL / rid / "repro.py"))
+
+
+def _oracle_outputs(rid, cpu_inputs):
+    import oracle as ref
+    if rid == "mean_lastdim_f32":
+        return [ref.row_mean(cpu_inputs[0])]
+    if rid == "pointwise_bias_gelu_tanh_nhwc":
+        return [ref.bias_gelu_nchw_to_nhwc(*cpu_inputs)]
+    if rid == "amax_sum_scaled_masked_softmax":
+        return [ref.scaled_masked_softmax(cpu_inputs[0], cpu_inputs[1], 0.125)]
+    if rid == "var_mean_residual_layernorm":
+        return list(ref.residual_layernorm(*cpu_inputs, 1e-5))
+    if rid == "mean_rmsnorm":
+        return list(ref.rmsnorm(*cpu_inputs, 1e-5))
+    return list(ref.batchnorm_train(*cpu_inputs, momentum=0.1, eps=1e-5, relu=True))
+
+
+@pytest.mark.parametrize("rid", REPRO_IDS)
+def test_all_points_vs_oracle_and_eager(rid, rocm_device):
+    """Each shapes.json point (BASELINE size first, then ragged ones)."""
+    from oracle_harness import _normalize_outputs, resolve_oracle
+    from repro_harness import make_inputs_from_config
+    fn, inst = _load(rid)
+    for label, cfg in _points(rid).items():
+        print(f"[{rid}] point {label}", flush=True)
+        torch.manual_seed(1)
+        cpu_in = make_inputs_from_config(cfg, device="cpu")
+        dev_in = [t.to(rocm_device) for t in cpu_in]
+        impl, info = resolve_oracle(fn, dev_in)
+        assert info["current_hardware"] != "unknown"
+        got = _normalize_outputs(impl(dev_in))
+        torch.cuda.synchronize()
+        want = _oracle_outputs(rid, cpu_in)
+        assert len(got) == len(want)
+        for i, (g, w) in enumerate(zip(got, want)):
+            assert g.dtype == w.dtype, f"{label} out{i} dtype"
+            assert g.stride() == w.stride(), f"{label} out{i} strides {g.stride()} vs {w.stride()}"
+            assert_close(g, w, _tol(w), f"{rid}/{label} out{i} vs oracle")
+        with torch.no_grad():
+            eager = _normalize_outputs(inst(*[t.clone() for t in cpu_in]))
+        for i, (g, e) in enumerate(zip(got, eager)):
+            assert_close(g, e, _tol(e), f"{rid}/{label} out{i} vs eager")
+        del cpu_in, dev_in, got, want, eager
+
+
+# ---------------------------------------------------------------------------
+# Edge cases and closed forms
+# ---------------------------------------------------------------------------
+
+def test_row_mean_edges(rocm_device):
+    import hip_oracles
+    import oracle as ref
+    x = torch.full((5, 4096), 3.25)
+    assert torch.equal(hip_oracles.row_mean(x.to(rocm_device)).cpu(), torch.full((5,), 3.25))
+    # single column, single row, NaN propagation
+    x = torch.randn(9, 1)
+    assert_close(hip_oracles.row_mean(x.to(rocm_device)), x[:, 0], F32_TOL, "cols=1")
+    x = torch.randn(1, 12345)
+    assert_close(hip_oracles.row_mean(x.to(rocm_device)), ref.row_mean(x), F32_TOL, "rows=1")
+    x = torch.randn(4, 256)
+    x[2, 17] = float("nan")
+    out = hip_oracles.row_mean(x.to(rocm_device)).cpu()
+    assert math.isnan(out[2].item()) and not torch.isnan(out[[0, 1, 3]]).any()
+    # strided rows (a column slice): scalar path
+    base = torch.randn(64, 1031)
+    view = base.to(rocm_device)[:, 3:1003]
+    assert_close(hip_oracles.row_mean(view), ref.row_mean(base[:, 3:1003].contiguous()),
+                 F32_TOL, "strided")
+    # exact small integers: sum is exact, so the mean is exact
+    x = torch.randint(-8, 8, (33, 4096)).float()
+    assert torch.equal(hip_oracles.row_mean(x.to(rocm_device)).cpu(), x.sum(1) / 4096)
+
+
+def test_bias_gelu_edges(rocm_device):
+    import hip_oracles
+    import oracle as ref
+    bf = torch.bfloat16
+    # gelu(0) = 0; gelu(t) -> t for large t, -> 0 for very negative t
+    x = torch.zeros(1, 8, 8, 8, dtype=bf)
+    b = torch.zeros(8, dtype=bf)
+    assert torch.equal(hip_oracles.bias_gelu_nchw_to_nhwc(x.to(rocm_device), b.to(rocm_device)).cpu(), x)
+    x = torch.tensor([20.0, -20.0, 1e30, -1e30, float("inf"), float("-inf"), 0.5, -0.5]).to(bf)
+    x = x.view(1, 1, 1, 8).repeat(1, 8, 1, 1).contiguous()
+    out = hip_oracles.bias_gelu_nchw_to_nhwc(x.to(rocm_device), torch.zeros(8, dtype=bf, device=rocm_device)).cpu()
+    want = torch.nn.functional.gelu(x.float(), approximate="tanh").to(bf)
+    assert_close(out[..., :4], want[..., :4], BF16_TOL, "gelu large |t|")
+    assert out[0, 0, 0, 4].item() == float("inf") and math.isnan(out[0, 0, 0, 5].float().item())
+    assert_close(out[..., 6:], want[..., 6:], BF16_TOL, "gelu +-0.5")
+    # shapes off the vector path (C % 8, HW % 8) and partial channel groups
+    for shape in [(2, 5, 3, 3), (1, 264, 2, 4), (3, 16, 1, 8)]:
+        g = torch.Generator().manual_seed(sum(shape))
+        x = torch.randn(shape, generator=g).to(bf)
+        b = (0.1 * torch.randn(shape[1], generator=g)).to(bf)
+        got = hip_oracles.bias_gelu_nchw_to_nhwc(x.to(rocm_device), b.to(rocm_device))
+        assert got.is_contiguous(memory_format=torch.channels_last)
+        assert_close(got, ref.bias_gelu_nchw_to_nhwc(x, b), BF16_TOL, f"gelu {shape}")
+
+
+def test_softmax_closed_forms(rocm_device):
+    import hip_oracles
+    import oracle as ref
+    bf = torch.bfloat16
+    q = k = 1024
+    mask = torch.triu(torch.full((q, k), float("-inf")), 1).to(bf)
+    x = torch.full((2, q, k), 0.75, dtype=bf)
+    out = hip_oracles.scaled_masked_softmax(x.to(rocm_device), mask.to(rocm_device), 0.125).cpu().float()
+    rows = torch.arange(q).view(q, 1)
+    cols = torch.arange(k).view(1, k)
+    want = torch.where(cols <= rows, 1.0 / (rows + 1).float(), torch.zeros(()))
+    want = want.to(bf).float().expand(2, q, k)
+    assert_close(out, want, BF16_TOL, "uniform causal row -> 1/(q+1)")
+    assert (out.masked_select((cols > rows).expand(2, q, k)) == 0).all(), "masked entries must be exactly 0"
+    # fully masked row -> NaN everywhere (as eager)
+    full = torch.full((4, 64), float("-inf")).to(bf)
+    x = torch.randn(1, 4, 64).to(bf)
+    out = hip_oracles.scaled_masked_softmax(x.to(rocm_device), full.to(rocm_device), 0.125).cpu()
+    assert torch.isnan(out.float()).all()
+    # generic scale (rounded product), K off the vector path and K > 4096
+    for (b_, q_, k_), scale in [((2, 8, 4096), 0.3), ((1, 3, 5000), 0.125), ((2, 5, 77), 1.7)]:
+        g = torch.Generator().manual_seed(k_)
+        x = (3 * torch.randn(b_, q_, k_, generator=g)).to(bf)
+        m = torch.triu(torch.full((q_, k_), float("-inf")), 1).to(bf)
+        got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), m.to(rocm_device), scale)
+        assert_close(got, ref.scaled_masked_softmax(x, m, scale), BF16_TOL, f"softmax {k_} {scale}")
+    # rows sum to 1 (bf16 outputs, fp32 sum)
+    x = torch.randn(4, 128, 1024).to(bf)
+    got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), mask[:128].contiguous().to(rocm_device), 0.125)
+    assert_close(got.float().sum(-1), torch.ones(4, 128), 1e-2, "row sums")
+
+
+def test_norm_closed_forms(rocm_device):
+    import hip_oracles
+    bf = torch.bfloat16
+    eps = 1e-5
+    x = torch.full((3, 4096), 1.5, dtype=bf)
+    r = torch.full((3, 4096), 0.5, dtype=bf)
+    gamma = torch.randn(4096).to(bf)
+    beta = torch.randn(4096).to(bf)
+    h, y, mean, rstd = hip_oracles.residual_layernorm(*(t.to(rocm_device) for t in (x, r, gamma, beta)), eps)
+    assert torch.equal(h.cpu(), torch.full((3, 4096), 2.0, dtype=bf))
+    assert torch.equal(mean.cpu(), torch.full((3,), 2.0))
+    assert_close(rstd, torch.full((3,), 1 / math.sqrt(eps)), F32_TOL * 1 / math.sqrt(eps), "rstd=1/sqrt(eps)")
+    assert torch.equal(y.cpu(), beta.expand(3, 4096)), "constant row -> y = beta"
+    z = torch.zeros(2, 1024, dtype=bf)
+    y, rstd = hip_oracles.rmsnorm(z.to(rocm_device), gamma[:1024].contiguous().to(rocm_device), eps)
+    assert torch.equal(y.cpu(), z) and torch.allclose(rstd.cpu(), torch.full((2,), 1 / math.sqrt(eps)))
+
+
+def test_norm_shapes_off_vector_path(rocm_device):
+    import hip_oracles
+    import oracle as ref
+    bf = torch.bfloat16
+    for rows, cols in [(7, 100), (5, 8192 + 8), (64, 4096), (3, 8)]:
+        g = torch.Generator().manual_seed(rows * cols)
+        x = torch.randn(rows, cols, generator=g).to(bf)
+        r = torch.randn(rows, cols, generator=g).to(bf)
+        gm = (1 + 0.1 * torch.randn(cols, generator=g)).to(bf)
+        bt = (0.1 * torch.randn(cols, generator=g)).to(bf)
+        got = hip_oracles.residual_layernorm(*(t.to(rocm_device) for t in (x, r, gm, bt)), 1e-5)
+        want = ref.residual_layernorm(x, r, gm, bt, 1e-5)
+        for name, a, w in zip(("h", "y", "mean", "rstd"), got, want):
+            assert_close(a, w, _tol(w), f"ln {rows}x{cols} {name}")
+        got = hip_oracles.rmsnorm(x.to(rocm_device), gm.to(rocm_device), 1e-5)
+        want = ref.rmsnorm(x, gm, 1e-5)
+        for name, a, w in zip(("y", "rstd"), got, want):
+            assert_close(a, w, _tol(w), f"rms {rows}x{cols} {name}")
+
+
+def test_batchnorm_closed_forms_and_edges(rocm_device):
+    import hip_oracles
+    import oracle as ref
+    c = 6
+    x = torch.randn(5, c, 7, 9) * 3
+    x[:, 2] = 4.0  # constant channel
+    gamma = 1 + 0.1 * torch.randn(c)
+    beta = 0.1 * torch.randn(c)
+    beta[2] = -0.25
+    rm, rv = torch.zeros(c), torch.ones(c)
+    rm_d, rv_d = rm.to(rocm_device), rv.to(rocm_device)
+    y, sm, si = hip_oracles.batchnorm_train(x.to(rocm_device), gamma.to(rocm_device),
+                                            beta.to(rocm_device), rm_d, rv_d,
+                                            momentum=0.1, eps=1e-5, relu=True)
+    assert sm.cpu()[2].item() == 4.0
+    assert (y.cpu()[:, 2] == 0).all(), "constant channel, negative beta -> relu(beta) = 0"
+    assert abs(rm_d.cpu()[2].item() - 0.4) < 1e-6 and abs(rv_d.cpu()[2].item() - 0.9) < 1e-6
+    want = ref.batchnorm_train(x, gamma, beta, rm, rv, momentum=0.1, eps=1e-5, relu=True)
+    for name, a, w in zip(("y", "mean", "invstd", "rm", "rv"), (y, sm, si, rm_d, rv_d), want):
+        assert_close(a, w, F32_TOL, f"bn {name}")
+    # no ReLU, NaN propagation through y of its channel only
+    x = torch.randn(3, 4, 8, 8)
+    x[1, 3, 2, 2] = float("nan")
+    rm_d, rv_d = torch.zeros(4, device=rocm_device), torch.ones(4, device=rocm_device)
+    y, sm, si = hip_oracles.batchnorm_train(x.to(rocm_device), torch.ones(4, device=rocm_device),
+                                            torch.zeros(4, device=rocm_device), rm_d, rv_d,
+                                            momentum=0.1, eps=1e-5, relu=False)
+    y = y.cpu()
+    assert torch.isnan(y[:, 3]).all() and not torch.isnan(y[:, :3]).any()
+    assert (y[:, :3] < 0).any(), "relu=False keeps negatives"
+
+
+def test_graph_capture_replays_match_eager(rocm_device):
+    """Each oracle is captured in a hipGraph and replayed several times with
+    eager work in between; every replay must equal the eager call."""
+    from oracle_harness import _normalize_outputs, resolve_oracle
+    from repro_harness import make_inputs_from_config
+    for rid in REPRO_IDS:
+        fn, _ = _load(rid)
+        label, cfg = list(_points(rid).items())[1]  # a small point
+        torch.manual_seed(1)
+        dev_in = make_inputs_from_config(cfg, device=rocm_device)
+        impl, _ = resolve_oracle(fn, dev_in)
+        snapshot = [t.clone() for t in dev_in]
+        eager = [t.clone() for t in _normalize_outputs(impl(dev_in))]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            captured = _normalize_outputs(impl(dev_in))
+        for rep in range(3):
+            for t, s in zip(dev_in, snapshot):
+                t.copy_(s)  # BN updates running stats in place
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            _ = torch.randn(1000, device=rocm_device).sum().item()  # eager work between
+            for i, (a, e) in enumerate(zip(captured, eager)):
+                assert torch.equal(a, e) or torch.allclose(a.float(), e.float(), atol=0, rtol=0,
+                                                           equal_nan=True), \
+                    f"{rid} replay {rep} out{i} differs from eager"
+
+
+def test_deterministic(rocm_device):
+    import hip_oracles
+    x = torch.randn(128, 256, 14, 14, device=rocm_device) * 2 + 0.5
+    w = torch.ones(256, device=rocm_device)
+    b = torch.zeros(256, device=rocm_device)
+    outs = []
+    for _ in range(2):
+        rm, rv = torch.zeros(256, device=rocm_device), torch.ones(256, device=rocm_device)
+        outs.append(hip_oracles.batchnorm_train(x, w, b, rm, rv, momentum=0.1, eps=1e-5))
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
+
+
+def test_wrappers_reject_bad_operands(rocm_device):
+    import hip_oracles
+    with pytest.raises(ValueError):
+        hip_oracles.row_mean(torch.randn(4, 4))  # CPU tensor: no fallback
+    with pytest.raises(ValueError):
+        hip_oracles.row_mean(torch.randn(4, 4, device=rocm_device).half())
+    with pytest.raises(ValueError):
+        hip_oracles.scaled_masked_softmax(torch.randn(2, 4, 8, device=rocm_device).bfloat16(),
+                                          torch.zeros(4, 9, device=rocm_device).bfloat16(), 1.0)
+    x = torch.randn(2, 4, 3, 3, device=rocm_device)
+    ones = torch.ones(4, device=rocm_device)
+    with pytest.raises(ValueError):
+        hip_oracles.batchnorm_train(x, ones, ones, ones.clone(), ones.clone(), momentum=0.1,
+                                    eps=1e-5, workspace=torch.empty(1, dtype=torch.uint8,
+                                                                    device=rocm_device))
