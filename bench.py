@@ -4,21 +4,26 @@
                     [--no-configs] [--no-cpu] [--copy-calibration MIB]
 
 Headline: BASELINE config 2 (per-channel bias + GELU-tanh, bf16 NCHW ->
-NHWC [128,256,56,56]); a step is one oracle_forward over one batch.  Inputs
-are resident in HBM before timing starts.  R rotating input/output sets
-(together >= 1 GiB, four times the 256 MB Infinity Cache) are each captured
-in a hipGraph; step k replays graph k % R, so no step reads its inputs from
-the cache a previous step left warm.  Exactly K steps are timed between two
-device synchronisations (wall clock) and, on the launch stream, between two
-hipEvents (kernel time).
+NHWC [128,256,56,56]); a step is one oracle_forward over one batch of
+inputs already resident in HBM.
 
-value   = algorithmic bytes per step / (wall ms per step)   [GB/s]
-roofline.achieved = algorithmic bytes / (event time / K)    [GB/s]
-cpu_baseline = the CPU oracle (oracle/hipo_ref.c, OpenMP) on the same
-               workload on the host cores.
-configs = every BASELINE config timed through oracle_harness.bench_oracle
-          (hipGraph replay, cache flush between replays, min of 5 rounds),
-          with the eager repro on the host CPU beside it.
+Steady-state timing: R rotating input sets (together >= 1 GiB, four times
+the 256 MB Infinity Cache) and one output buffer per step slot.  L steps
+(cycling through the sets) are captured in one hipGraph, so consecutive
+kernels run back to back as in a real pipeline (a separate graph per step
+would add the ~8 us idle gap a ROCm graph launch costs); no step finds its
+inputs in a cache a previous step warmed.  Exactly K steps are timed
+between two device synchronisations (wall clock) and, on the launch
+stream, between two hipEvents (device time).
+
+value             = algorithmic bytes per step / (wall time per step)   [GB/s]
+roofline.achieved = algorithmic bytes / (device time per step)          [GB/s]
+cpu_baseline      = the CPU oracle (oracle/hipo_ref.c, OpenMP) on the same
+                    workload on the host cores.
+configs           = every BASELINE config: the same steady-state loop, plus
+                    oracle_harness.bench_oracle (single launch after a cache
+                    flush, fp64 numerics gate) with the eager repro timed
+                    on the host CPU beside it.
 """
 from __future__ import annotations
 
@@ -60,6 +65,7 @@ DTYPE = {
     "mean_rmsnorm": "bf16", "var_mean_batchnorm_train_relu": "f32",
 }
 METRIC = "achieved HBM GB/s and % of 8 TB/s SOL per kernel; µs vs host-CPU eager"
+PEAK_GBPS = 8000.0
 
 
 def log(msg: str) -> None:
@@ -69,8 +75,7 @@ def log(msg: str) -> None:
 def _baseline_point(rid):
     from repro_harness import load_shape_configs
     cfgs = load_shape_configs(str(CANONICAL / rid / "repro.py"))
-    label, cfg = next(iter(cfgs.items()))
-    return label, cfg
+    return next(iter(cfgs.items()))
 
 
 def _cpu_oracle_call(rid, cpu_inputs, threads):
@@ -108,88 +113,80 @@ def cpu_baseline(rid, cpu_inputs, nbytes, budget_s: float = 10.0) -> dict:
             "us": round(best * 1e6, 1)}
 
 
-def headline(rid, steps, warmup, want_cpu):
+def steady_state(rid, steps, warmup):
+    """Back-to-back steps over rotating input sets (see module docstring)."""
     import torch
     import oracle_harness as oh
-    from byte_accounting import HBM_PEAK_BYTES_PER_S
     from repro_harness import make_inputs_from_config
 
     dev = torch.device("cuda:0")
     label, cfg = _baseline_point(rid)
-    mod, fn, d = oh._load_oracle_module(CANONICAL / rid)
+    _, fn, d = oh._load_oracle_module(CANONICAL / rid)
     instance = oh.get_repro_instance(d)
     oh._seed_input_generation(1)
     cpu_inputs = make_inputs_from_config(cfg, device="cpu")
     nbytes = oh.effective_bytes(instance, cpu_inputs)
-    impl, info = oh.resolve_oracle(fn, [t.to("meta") if isinstance(t, torch.Tensor) else t
-                                        for t in cpu_inputs])
-    per_set = sum(t.numel() * t.element_size() for t in cpu_inputs if isinstance(t, torch.Tensor))
-    per_set += nbytes  # outputs are of the same order
-    sets = max(2, math.ceil((1 << 30) / max(per_set, 1)))
-    sets = min(sets, 16)
-    log(f"{rid}: {label}, {nbytes} algorithmic bytes/step, {sets} rotating sets")
-
-    input_sets = []
+    in_bytes = sum(t.numel() * t.element_size() for t in cpu_inputs if isinstance(t, torch.Tensor))
+    sets = min(16, max(2, math.ceil((1 << 30) / max(in_bytes, 1))))
+    per_graph = sets * max(1, math.ceil(16 / sets))
+    input_sets = [[t.to(dev) if isinstance(t, torch.Tensor) else t for t in cpu_inputs]
+                  for _ in range(sets)]
+    impl, info = oh.resolve_oracle(fn, input_sets[0])
+    log(f"{rid}: {label}, {nbytes} algorithmic bytes/step, {sets} input sets, "
+        f"{per_graph} steps per graph")
     for s in range(sets):
-        input_sets.append([t.to(dev) if isinstance(t, torch.Tensor) else t for t in cpu_inputs])
+        impl(input_sets[s])
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    graphs = []
+    keep = []  # every captured step keeps its own output buffers
+    cycle = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cycle):
+        for k in range(per_graph):
+            keep.append(impl(input_sets[k % sets]))
+    singles = []
     for s in range(sets):
-        for _ in range(2):
-            impl(input_sets[s])
-        torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            impl(input_sets[s])
-        graphs.append(g)
-    torch.cuda.synchronize()
-    for k in range(warmup):
-        graphs[k % sets].replay()
+            keep.append(impl(input_sets[s]))
+        singles.append(g)
     torch.cuda.synchronize()
 
+    def run(n):
+        full, rem = divmod(n, per_graph)
+        for _ in range(full):
+            cycle.replay()
+        for k in range(rem):
+            singles[k % sets].replay()
+
+    run(warmup)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     with oh._gpu_exclusive_lock(f"bench:{rid}"):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         ev0.record(stream)
-        for k in range(steps):
-            graphs[k % sets].replay()
+        run(steps)
         ev1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-    event_s = ev0.elapsed_time(ev1) / 1e3
-    ms_per_step = wall / steps * 1e3
-    kernel_s = event_s / steps
-    peak = HBM_PEAK_BYTES_PER_S["MI355X"]
-    achieved = nbytes / kernel_s
-    result = {
-        "ms_per_step": round(ms_per_step, 4),
-        "value": round(nbytes / (wall / steps) / 1e9, 1),
-        "nbytes": nbytes,
-        "label": label,
+    device_s = ev0.elapsed_time(ev1) / 1e3 / steps
+    wall_s = wall / steps
+    out = {
+        "label": label, "nbytes": nbytes, "sets": sets, "steps_per_graph": per_graph,
         "dispatch": info and {"matched": info["matched"], "tuned_on": info["tuned_hardware"]},
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved / 1e9, 1),
-            "peak": peak / 1e9,
-            "unit": "GB/s",
-            "frac": round(achieved / peak, 4),
-            "traffic": None,
-            "kernel_us": round(kernel_s * 1e6, 2),
-        },
-        "rotating_sets": sets,
+        "ms_per_step": round(wall_s * 1e3, 4),
+        "device_us_per_step": round(device_s * 1e6, 2),
+        "value": round(nbytes / wall_s / 1e9, 1),
+        "achieved": round(nbytes / device_s / 1e9, 1),
     }
-    del graphs, input_sets
+    del cycle, singles, keep, input_sets
     torch.cuda.synchronize()
-    if want_cpu:
-        log("cpu baseline (CPU oracle)")
-        result["cpu_baseline"] = cpu_baseline(rid, cpu_inputs, nbytes)
-    return result
+    torch.cuda.empty_cache()
+    return out, cpu_inputs
 
 
-def per_config(want_cpu):
+def per_config(want_cpu, steady_steps=64):
     import torch
     import oracle_harness as oh
     from repro_harness import make_inputs_from_config
@@ -197,15 +194,20 @@ def per_config(want_cpu):
     for tag, rid in ALL_CONFIGS:
         label, cfg = _baseline_point(rid)
         log(f"config {tag}: {rid}")
-        mod, fn, d = oh._load_oracle_module(CANONICAL / rid)
+        ss, _ = steady_state(rid, steady_steps, 8)
+        _, fn, d = oh._load_oracle_module(CANONICAL / rid)
         oh._seed_input_generation(1)
         inputs = make_inputs_from_config(cfg, device="cuda")
         r = oh.bench_oracle(fn, oh.get_repro_instance(d), inputs, f"{rid}_{label}",
                             warmup=10, rep=100, rounds=5, compare_compile=False,
                             cpu_eager=want_cpu)
         entry = {"config": tag, "repro": rid, "status": r.get("status"),
+                 "bytes": r.get("bytes"),
+                 "steady_us": ss["device_us_per_step"], "steady_gbps": ss["achieved"],
+                 "steady_sol_frac": round(ss["achieved"] / PEAK_GBPS, 4),
                  "us": r.get("oracle_us"), "median_us": r.get("oracle_median_us"),
-                 "bytes": r.get("bytes"), "gbps": r.get("gbps"), "sol_frac": r.get("sol_frac")}
+                 "graph_us": r.get("oracle_graph_us"),
+                 "gbps": r.get("gbps"), "sol_frac": r.get("sol_frac")}
         gate = r.get("numerics_gate")
         if gate is not None:
             entry["numerics_gate_pass"] = gate.get("pass")
@@ -231,10 +233,11 @@ def copy_calibration(mib: int, reps: int = 20) -> None:
 
 
 def main(argv=None) -> int:
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--config", default=HEADLINE, help="repro id of the headline workload")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
@@ -256,7 +259,7 @@ def main(argv=None) -> int:
     hip_oracles.load_library()
 
     rid = args.config
-    h = headline(rid, args.steps, args.warmup, not args.no_cpu)
+    h, cpu_inputs = steady_state(rid, args.steps, args.warmup)
     line = {
         "metric": METRIC,
         "value": h["value"],
@@ -271,11 +274,17 @@ def main(argv=None) -> int:
         "dtype": DTYPE[rid],
         "data": "synthetic (seeded N(mu, sigma) inputs of the BASELINE config)",
         "config": {"workload": WORKLOAD[rid], "repro": rid, "point": h["label"],
-                   "bytes_per_step": h["nbytes"], "rotating_sets": h["rotating_sets"],
-                   "parallelism": "single-gpu"},
-        "roofline": h["roofline"],
-        "cpu_baseline": h.get("cpu_baseline"),
+                   "bytes_per_step": h["nbytes"], "input_sets": h["sets"],
+                   "steps_per_graph": h["steps_per_graph"], "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": h["achieved"], "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(h["achieved"] / PEAK_GBPS, 4),
+                     "traffic": None, "kernel_us": h["device_us_per_step"]},
+        "cpu_baseline": None,
     }
+    if not args.no_cpu:
+        log("cpu baseline (CPU oracle)")
+        line["cpu_baseline"] = cpu_baseline(rid, cpu_inputs, h["nbytes"])
+    del cpu_inputs
     if not args.no_configs:
         line["configs"] = per_config(not args.no_cpu)
     print(json.dumps(line), flush=True)

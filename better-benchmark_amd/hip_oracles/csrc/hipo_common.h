@@ -49,6 +49,14 @@ constexpr int kWave = 64;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
+// 16-byte vectors as native clang vectors (the non-temporal load/store
+// builtins accept these, not HIP's struct vector types).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+inline bool aligned16(const void* p) {
+  return reinterpret_cast<uintptr_t>(p) % 16 == 0;
+}
 
 // bf16 bits held in the low / high half of a 32-bit word -> fp32 (exact).
 __device__ __forceinline__ float bf16lo(uint32_t w) {

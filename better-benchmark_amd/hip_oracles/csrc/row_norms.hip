@@ -228,10 +228,6 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_scalar(
   if (lane == 0) rstd_out[row] = rstd;
 }
 
-bool aligned16(const void* p) {
-  return reinterpret_cast<uintptr_t>(p) % 16 == 0;
-}
-
 }  // namespace
 }  // namespace hipo
 

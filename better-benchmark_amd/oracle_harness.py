@@ -640,33 +640,45 @@ class _CacheFlusher:
 
     def __init__(self, nbytes: int, device):
         n = max(nbytes // 4, 1)
-        self.buf = torch.ones(n, dtype=torch.int32, device=device)
-        self.out = torch.empty((), dtype=torch.int64, device=device)
+        self.buf = torch.ones(n, dtype=torch.float32, device=device)
+        self.out = torch.empty((), dtype=torch.float32, device=device)
         self.nbytes = n * 4
 
     def __call__(self):
-        torch.sum(self.buf, dim=0, dtype=torch.int64, out=self.out)
+        torch.sum(self.buf, dim=0, out=self.out)  # one read pass, no cast
 
 
-def _time_graph(graph, warmup, rep, *, flush=None):
-    """(min µs, median µs) of `rep` event-timed replays of `graph`.
+def _time_launches(launch, warmup, rep, *, flush=None):
+    """(min µs, median µs) of `rep` event-timed calls of `launch()`.
 
-    Each replay sits alone between a hipEvent pair on the current stream;
-    `flush()` (if given) runs before each pair, outside it.
+    Each call sits alone between a hipEvent pair on the current stream;
+    `flush()` (if given) runs before each pair, outside it.  The flush keeps
+    the GPU busy while the host enqueues the event pair and the launch, so
+    the pair brackets the device work and not the host's launch latency.
     """
     for _ in range(warmup):
-        graph.replay()
+        launch()
     pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
              for _ in range(rep)]
     for start, end in pairs:
         if flush is not None:
             flush()
         start.record()
-        graph.replay()
+        launch()
         end.record()
     torch.cuda.synchronize()
     times = sorted(s.elapsed_time(e) * 1000.0 for s, e in pairs)
     return times[0], times[len(times) // 2]
+
+
+def _time_graph(graph, warmup, rep, *, flush=None):
+    """(min µs, median µs) of `rep` event-timed replays of a captured graph.
+
+    On ROCm a graph launch leaves the GPU idle for several µs before the
+    first node runs, and that gap falls inside the event pair; bench_oracle
+    therefore also times direct launches (_time_launches).
+    """
+    return _time_launches(graph.replay, warmup, rep, flush=flush)
 
 
 def _meta_copy(inputs):
@@ -828,15 +840,24 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
                 return result
 
     flush = _CacheFlusher(flush_bytes, device) if flush_bytes else None
-    quick, _ = _time_graph(g_oracle, 3, 10, flush=flush)
+
+    def run_oracle():
+        with torch.no_grad():
+            oracle_forward(inputs)
+
+    def run_compiled():
+        with torch.no_grad():
+            compiled(*inputs)
+
+    quick, _ = _time_launches(run_oracle, 3, 10, flush=flush)
     if g_compile is not None:
-        quick = min(quick, _time_graph(g_compile, 3, 10, flush=flush)[0])
+        quick = min(quick, _time_launches(run_compiled, 3, 10, flush=flush)[0])
     if quick < 50:
         rep = max(rep, 500)
     elif quick < 200:
         rep = max(rep, 300)
 
-    best_oracle = best_compile = math.inf
+    best_oracle = best_compile = best_graph = best_compile_graph = math.inf
     medians = []
     with _gpu_exclusive_lock(repro_id, disabled=disable_gpu_lock):
         for _ in range(warmup):
@@ -845,11 +866,15 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
                 g_compile.replay()
         torch.cuda.synchronize()
         for _ in range(rounds):
-            o_min, o_med = _time_graph(g_oracle, warmup, rep, flush=flush)
+            o_min, o_med = _time_launches(run_oracle, warmup, rep, flush=flush)
             best_oracle = min(best_oracle, o_min)
             medians.append(o_med)
+            best_graph = min(best_graph, _time_graph(g_oracle, warmup, rep, flush=flush)[0])
             if g_compile is not None:
-                best_compile = min(best_compile, _time_graph(g_compile, warmup, rep, flush=flush)[0])
+                best_compile = min(best_compile,
+                                   _time_launches(run_compiled, warmup, rep, flush=flush)[0])
+                best_compile_graph = min(best_compile_graph,
+                                         _time_graph(g_compile, warmup, rep, flush=flush)[0])
 
     if g_compile is not None:
         ratio = best_compile / best_oracle if best_oracle > 0 else 0.0
@@ -869,7 +894,9 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
         "repro_id": repro_id,
         "oracle_us": round(best_oracle, 2),
         "oracle_median_us": round(sorted(medians)[len(medians) // 2], 2),
+        "oracle_graph_us": round(best_graph, 2),
         "compile_us": round(best_compile, 2) if g_compile is not None else None,
+        "compile_graph_us": round(best_compile_graph, 2) if g_compile is not None else None,
         "ratio": round(ratio, 3) if ratio is not None else None,
         "status": status,
         "hardware": hw,
@@ -880,7 +907,9 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
         if hw in HBM_PEAK_BYTES_PER_S:
             result["sol_frac"] = round(sol_fraction(nbytes, best_oracle, hw), 4)
             result["sol_peak_gbps"] = HBM_PEAK_BYTES_PER_S[hw] / 1e9
-    result["timing"] = {"method": "hipgraph_replay+hipevent", "rep": rep, "rounds": rounds,
+    result["timing"] = {"method": "hipevent pair per launch, cache-flush read before each",
+                        "graph_method": "hipevent pair per hipGraph replay",
+                        "rep": rep, "rounds": rounds,
                         "flush_bytes": flush.nbytes if flush else 0}
     if compile_error:
         result["compile_error"] = compile_error
@@ -1190,6 +1219,7 @@ def _load_oracle_module(canonical_dir):
             raise FileNotFoundError(f"no oracle.py / oracle_*.py in {d}")
         path = candidates[0]
     spec = importlib.util.spec_from_file_location(f"_oracle_{d.name}", path)
+    reset_oracle_registry(spec.name)  # re-loading must not register twice
     mod = importlib.util.module_from_spec(spec)
     sys.modules[spec.name] = mod
     spec.loader.exec_module(mod)

@@ -80,7 +80,7 @@ def row_mean(x: torch.Tensor, threads=None) -> torch.Tensor:
     return out
 
 
-def bias_gelu_nchw_to_nhwc(x, bias, *, round_t: bool = False, threads=None):
+def bias_gelu_nchw_to_nhwc(x, bias, *, round_t: bool = True, threads=None):
     x = _cpu(x, torch.bfloat16)
     bias = _cpu(bias, torch.bfloat16)
     n, c, h, w = x.shape

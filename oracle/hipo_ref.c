@@ -49,6 +49,36 @@ static inline uint16_t f32_to_bf16(float f) {
 
 static inline float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+/* Round-to-nearest-even fp64 -> bf16 in one step (no intermediate fp32
+ * rounding, which could create a false tie). */
+static inline uint16_t f64_to_bf16(double d) {
+  if (isnan(d)) return 0x7fc0;
+  const uint16_t sign = signbit(d) ? 0x8000 : 0;
+  double a = fabs(d);
+  if (isinf(a)) return sign | 0x7f80;
+  if (a == 0.0) return sign;
+  int e;
+  const double m = frexp(a, &e);               /* a = m * 2^e, m in [0.5, 1) */
+  /* bf16 quantum: 2^(e-8) for normal results, 2^-133 for subnormal ones */
+  int qexp = e - 8;
+  if (qexp < -133) qexp = -133;
+  const double scaled = ldexp(a, -qexp);       /* exact: power-of-two scaling */
+  double q = floor(scaled);
+  const double rem = scaled - q;               /* exact */
+  if (rem > 0.5 || (rem == 0.5 && fmod(q, 2.0) == 1.0)) q += 1.0;
+  (void)m;
+  if (q >= 256.0) {                            /* carry into the next binade */
+    q = 128.0;
+    qexp += 1;
+  }
+  if (q >= 128.0) {
+    const int field = qexp + 7 + 127;
+    if (field >= 255) return sign | 0x7f80;
+    return sign | (uint16_t)(field << 7) | (uint16_t)((int)q & 0x7f);
+  }
+  return sign | (uint16_t)q;                   /* subnormal */
+}
+
 int ref_abi_version(void) { return 1; }
 
 int ref_max_threads(void) {
@@ -90,7 +120,7 @@ void ref_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x, const uint16_t* bias,
       for (int64_t ch = 0; ch < c; ++ch) {
         float t = bf16_to_f32(x[(i * c + ch) * hw + p]) + bf16_to_f32(bias[ch]);
         if (round_t) t = round_bf16(t);
-        o[ch] = f32_to_bf16((float)gelu_tanh((double)t));
+        o[ch] = f64_to_bf16(gelu_tanh((double)t));
       }
     }
   }
@@ -131,7 +161,7 @@ void ref_scaled_masked_softmax_bf16(const uint16_t* x, const uint16_t* mask,
         sum += s[j];
       }
       uint16_t* o = out + r * k;
-      for (int64_t j = 0; j < k; ++j) o[j] = f32_to_bf16((float)(s[j] / sum));
+      for (int64_t j = 0; j < k; ++j) o[j] = f64_to_bf16(s[j] / sum);
     }
     free(s);
   }
@@ -165,7 +195,7 @@ void ref_residual_layernorm_bf16(const uint16_t* x, const uint16_t* res,
     for (int64_t j = 0; j < cols; ++j) {
       const double v = (bf16_to_f32(h[base + j]) - mean) * rstd *
                            bf16_to_f32(gamma[j]) + bf16_to_f32(beta[j]);
-      y[base + j] = f32_to_bf16((float)v);
+      y[base + j] = f64_to_bf16(v);
     }
     mean_out[r] = (float)mean;
     rstd_out[r] = (float)rstd;
@@ -187,7 +217,7 @@ void ref_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma, uint16_t* y,
     const double rstd = 1.0 / sqrt(q / (double)cols + (double)eps);
     for (int64_t j = 0; j < cols; ++j) {
       const double v = bf16_to_f32(x[base + j]) * rstd * bf16_to_f32(gamma[j]);
-      y[base + j] = f32_to_bf16((float)v);
+      y[base + j] = f64_to_bf16(v);
     }
     rstd_out[r] = (float)rstd;
   }

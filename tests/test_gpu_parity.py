@@ -144,6 +144,31 @@ def test_bias_gelu_edges(rocm_device):
         assert_close(got, ref.bias_gelu_nchw_to_nhwc(x, b), BF16_TOL, f"gelu {shape}")
 
 
+def test_bias_gelu_every_bf16_input(rocm_device):
+    """All 65536 bf16 bit patterns as x (bias 0): the kernel's output must
+    equal the oracle's correctly rounded fp64 GELU for every finite input,
+    except in the far negative tail where the tanh form cancels (|y| < 1e-12,
+    compared with a tolerance), and follow the special values."""
+    import hip_oracles
+    import oracle as ref
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    x = bits.view(torch.bfloat16).reshape(4, 8, 64, 32).contiguous()  # NCHW, C = 8
+    b = torch.zeros(8, dtype=torch.bfloat16)
+    got = hip_oracles.bias_gelu_nchw_to_nhwc(x.to(rocm_device), b.to(rocm_device)).cpu()
+    want = ref.bias_gelu_nchw_to_nhwc(x, b)
+    g, w = got.float(), want.float()
+    finite = torch.isfinite(x.float())
+    exact = (got.view(torch.int16) == want.view(torch.int16)) | (torch.isnan(g) & torch.isnan(w))
+    tail = finite & ~exact
+    assert (w[tail].abs() < 1e-12).all() and (g[tail].abs() < 1e-12).all(), \
+        f"{int(tail.sum())} inexact results outside the cancelling tail"
+    assert int(tail.sum()) < 100
+    assert torch.isnan(g[torch.isnan(x.float())]).all()
+    xf = x.float()
+    assert (g[xf == float("inf")] == float("inf")).all()
+    assert torch.isnan(g[xf == float("-inf")]).all()
+
+
 def test_softmax_closed_forms(rocm_device):
     import hip_oracles
     import oracle as ref
