@@ -213,6 +213,7 @@ def memcopy_sol_us(total_bytes: int, *, device="cuda", reps: int = 50) -> float:
     fp32 `add(src, 1, out=dst)` over total_bytes // 8 elements moves
     total_bytes (half read, half written); min over `reps` event-timed runs.
     """
+    from oracle_harness import _gpu_exclusive_lock
     n = max(total_bytes // 8, 1)
     src = torch.empty(n, dtype=torch.float32, device=device).fill_(1.0)
     dst = torch.empty_like(src)
@@ -220,14 +221,15 @@ def memcopy_sol_us(total_bytes: int, *, device="cuda", reps: int = 50) -> float:
         torch.add(src, 1, out=dst)
     torch.cuda.synchronize()
     best = math.inf
-    for _ in range(reps):
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        torch.add(src, 1, out=dst)
-        b.record()
-        b.synchronize()
-        best = min(best, a.elapsed_time(b) * 1000.0)
+    with _gpu_exclusive_lock("memcopy_sol"):
+        for _ in range(reps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            torch.add(src, 1, out=dst)
+            b.record()
+            b.synchronize()
+            best = min(best, a.elapsed_time(b) * 1000.0)
     return best
 
 

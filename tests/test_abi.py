@@ -1,0 +1,102 @@
+"""The C-ABI library loads without a GPU and exports exactly what
+include/hip_oracles.h declares; host-side argument checks fail with
+HIPO_EINVAL and a message before anything is launched (no GPU needed)."""
+import ctypes
+import subprocess
+import sys
+
+import pytest
+
+import hip_oracles
+
+HIPO_EINVAL = 1000
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return hip_oracles.load_library()
+
+
+def test_header_symbols_are_exported(lib):
+    declared = hip_oracles.header_symbols()
+    assert len(declared) >= 9
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/hip_oracles.h but not exported"
+    assert set(declared) == set(hip_oracles._SIGNATURES), "ctypes signatures out of sync"
+
+
+def test_exported_names_match_header():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(hip_oracles.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T hipo_" in line}
+    assert exported == set(hip_oracles.header_symbols())
+
+
+def test_abi_version_and_error_string(lib):
+    assert lib.hipo_abi_version() == hip_oracles.ABI_VERSION == 1
+    assert lib.hipo_last_error() == b""
+
+
+@pytest.mark.parametrize("call,msg", [
+    (lambda l: l.hipo_row_mean_f32(None, None, -1, 4, 4, None), b"negative"),
+    (lambda l: l.hipo_row_mean_f32(None, None, 4, 8, 4, None), b"row_stride"),
+    (lambda l: l.hipo_row_mean_f32(None, None, 4, 8, 8, None), b"null"),
+    (lambda l: l.hipo_bias_gelu_nchw_to_nhwc_bf16(None, None, None, 2, 8, 8, None), b"null"),
+    (lambda l: l.hipo_scaled_masked_softmax_bf16(1, 1, 1, 2, 4, 8, 4, 1.0, None), b"mask_row_stride"),
+    (lambda l: l.hipo_residual_layernorm_bf16(None, None, None, None, None, None, None, None,
+                                              4, 0, 1e-5, None), b"cols"),
+    (lambda l: l.hipo_rmsnorm_bf16(None, None, None, None, -2, 8, 1e-5, None), b"negative"),
+    (lambda l: l.hipo_batchnorm_train_fwd_f32(1, 1, 1, 1, 1, 1, 1, 1, 2, 4, 9, 0.1, 1e-5, 1,
+                                              1, 0, None), b"workspace"),
+    (lambda l: l.hipo_batchnorm_train_fwd_f32(None, 1, 1, 1, 1, 1, 1, 1, 2, 4, 9, 0.1, 1e-5, 1,
+                                              1, 1 << 20, None), b"null"),
+])
+def test_argument_errors_before_launch(lib, call, msg):
+    assert call(lib) == HIPO_EINVAL
+    assert msg in lib.hipo_last_error()
+
+
+def test_empty_inputs_are_no_ops(lib):
+    assert lib.hipo_row_mean_f32(None, None, 0, 16, 16, None) == 0
+    assert lib.hipo_bias_gelu_nchw_to_nhwc_bf16(None, None, None, 0, 8, 8, None) == 0
+    assert lib.hipo_scaled_masked_softmax_bf16(None, None, None, 3, 0, 8, 8, 1.0, None) == 0
+    assert lib.hipo_last_error() == b""
+
+
+def test_batchnorm_workspace_bytes(lib):
+    assert lib.hipo_batchnorm_workspace_bytes(0, 4, 4) == 0
+    n = lib.hipo_batchnorm_workspace_bytes(128, 256, 3136)
+    assert 0 < n < (1 << 24)
+    assert hip_oracles.batchnorm_workspace_bytes(128, 256, 3136) == n
+
+
+def test_error_message_is_per_thread(lib):
+    import threading
+    assert lib.hipo_row_mean_f32(None, None, -1, 4, 4, None) == HIPO_EINVAL
+    seen = []
+    th = threading.Thread(target=lambda: seen.append(lib.hipo_last_error()))
+    th.start()
+    th.join()
+    assert seen == [b""] and b"negative" in lib.hipo_last_error()
+
+
+def test_wrappers_reject_cpu_tensors_without_fallback():
+    import torch
+    with pytest.raises(ValueError, match="ROCm device"):
+        hip_oracles.row_mean(torch.randn(4, 4))
+    with pytest.raises(ValueError):
+        hip_oracles.bias_gelu_nchw_to_nhwc(torch.randn(1, 8, 2, 2).bfloat16(),
+                                           torch.zeros(8).bfloat16())
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(hip_oracles.HipOraclesUnavailable):
+        hip_oracles.load_library(tmp_path / "nope.so")
+
+
+def test_bench_refuses_multi_gpu():
+    import pathlib
+    root = pathlib.Path(__file__).resolve().parents[1]
+    proc = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
+                          capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 2 and "one GPU" in proc.stderr
