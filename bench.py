@@ -72,6 +72,17 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def pmc_traffic(rid):
+    """HBM bytes per launch of the repro's kernel from the committed rocprof
+    counter summary (profiles/pmc_traffic.json), or None."""
+    path = ROOT / "profiles" / "pmc_traffic.json"
+    try:
+        entry = json.loads(path.read_text())["kernels"].get(rid)
+    except (OSError, ValueError, KeyError):
+        return None
+    return int(entry["traffic_bytes"]) if entry else None
+
+
 def _baseline_point(rid):
     from repro_harness import load_shape_configs
     cfgs = load_shape_configs(str(CANONICAL / rid / "repro.py"))
@@ -278,7 +289,7 @@ def main(argv=None) -> int:
                    "steps_per_graph": h["steps_per_graph"], "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": h["achieved"], "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(h["achieved"] / PEAK_GBPS, 4),
-                     "traffic": None, "kernel_us": h["device_us_per_step"]},
+                     "traffic": pmc_traffic(rid), "kernel_us": h["device_us_per_step"]},
         "cpu_baseline": None,
     }
     if not args.no_cpu:

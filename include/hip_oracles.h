@@ -56,8 +56,10 @@ int hipo_row_mean_f32(const float* x, float* out, int64_t rows, int64_t cols,
 
 /*
  * Channel bias + GELU(tanh) + NCHW -> NHWC:
- *   t = x[n,c,hw] + bias[c];  y = 0.5 t (1 + tanh(sqrt(2/pi) (t + 0.044715 t^3)))
- *   out[n,hw,c] = bf16(y)     (fp32 arithmetic, one rounding to bf16)
+ *   t = bf16(x[n,c,hw] + bias[c])       (eager order: the add rounds to bf16)
+ *   y = 0.5 t (1 + tanh(sqrt(2/pi) (t + 0.044715 t^3)))
+ *   out[n,hw,c] = bf16(y)    (correctly rounded: y comes from a 65536-entry
+ *                             table over every bf16 t, computed in double)
  * x is contiguous NCHW [n, c, hw]; out is the same logical tensor stored
  * channels-last (physical [n, hw, c]).
  * Replaces the Triton bodies of oracle_forward in
