@@ -222,9 +222,35 @@ def batchnorm_workspace_bytes(n: int, c: int, hw: int) -> int:
     return int(load_library().hipo_batchnorm_workspace_bytes(n, c, hw))
 
 
+# One zero-filled BatchNorm workspace per device, kept for the process: the
+# single-pass kernel keeps its exchange state (completion count, epoch,
+# tagged slots) there between calls, so it must start zeroed and must not be
+# handed to two calls that can run at the same time.
+_bn_workspaces: dict[int, torch.Tensor] = {}
+_bn_ws_lock = threading.Lock()
+
+
+def batchnorm_cached_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """The device's shared workspace, grown (zero-filled) to at least nbytes."""
+    with _bn_ws_lock:
+        ws = _bn_workspaces.get(dev.index)
+        if ws is None or ws.numel() < nbytes:
+            _require(not torch.cuda.is_current_stream_capturing(),
+                     "batchnorm: the workspace is allocated on first use; call once "
+                     "outside graph capture (or pass workspace=) before capturing")
+            ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=dev)
+            _bn_workspaces[dev.index] = ws
+        return ws
+
+
 def batchnorm_train(x, gamma, beta, running_mean, running_var, *, momentum: float,
                     eps: float, relu: bool = True, workspace: torch.Tensor | None = None):
-    """(y, save_mean, save_invstd); running_mean/var are updated in place."""
+    """(y, save_mean, save_invstd); running_mean/var are updated in place.
+
+    workspace: zero-filled uint8 device memory of at least
+    batchnorm_workspace_bytes(n, c, h*w) bytes, reused unmodified across calls
+    that are ordered on one stream.  Default: the device's shared workspace
+    (callers issuing BatchNorm on several streams at once pass their own)."""
     lib = load_library()
     dev = _require_rocm(x, gamma, beta, running_mean, running_var)
     _require(x.dim() == 4 and x.dtype == torch.float32 and x.is_contiguous(),
@@ -235,7 +261,7 @@ def batchnorm_train(x, gamma, beta, running_mean, running_var, *, momentum: floa
                  "batchnorm: gamma/beta/running stats must be contiguous fp32 [C]")
     need = int(lib.hipo_batchnorm_workspace_bytes(n, c, h * w))
     if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        workspace = batchnorm_cached_workspace(dev, need)
     _require(workspace.device == dev and workspace.numel() * workspace.element_size() >= need,
              "batchnorm: workspace too small")
     y = torch.empty_like(x)
@@ -251,8 +277,19 @@ def batchnorm_train(x, gamma, beta, running_mean, running_var, *, momentum: floa
     return y, save_mean, save_invstd
 
 
+def batchnorm_error_flag(dev: torch.device | None = None) -> int:
+    """Sticky error word of the device's shared BatchNorm workspace: nonzero
+    once an exchange wait of the single-pass kernel has timed out (that
+    channel's outputs are then NaN).  Synchronises the device."""
+    ws = _bn_workspaces.get((dev or torch.device("cuda", torch.cuda.current_device())).index)
+    if ws is None:
+        return 0
+    return int(ws[8:12].view(torch.int32).item())
+
+
 __all__ = [
     "HipOraclesUnavailable", "LIB_PATH", "load_library", "header_symbols",
     "row_mean", "bias_gelu_nchw_to_nhwc", "scaled_masked_softmax",
     "residual_layernorm", "rmsnorm", "batchnorm_workspace_bytes", "batchnorm_train",
+    "batchnorm_cached_workspace", "batchnorm_error_flag",
 ]

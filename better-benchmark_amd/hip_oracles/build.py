@@ -33,6 +33,7 @@ SOURCES = [
     "masked_softmax.hip",
     "row_norms.hip",
     "batchnorm.hip",
+    "batchnorm_fused.hip",
 ]
 
 # Packed-FP32 VALU forms are disabled for all device code (the compiler

@@ -1,6 +1,11 @@
 // BatchNorm training forward, fp32 NCHW: per-channel statistics over
 // (N, H, W), normalisation + affine (+ ReLU), running-stat update.
 //
+// Entry point.  The single-pass persistent kernel (batchnorm_fused.hip)
+// serves every shape it supports; the split-K path below serves the rest
+// (HW not a multiple of 4, unaligned pointers, very large tensors, more
+// than 64 workgroups per channel or 64 rounds).
+//
 // Split-K structure (two launches on the caller's stream):
 //   1. bn_partial_stats: grid (S, C).  Workgroup (s, c) reduces the planes
 //      n in [s*N/S, (s+1)*N/S) of channel c to a Welford triple
@@ -15,8 +20,8 @@
 //      with alpha = invstd * gamma, beta' = beta - mean * alpha.  Workgroup
 //      (0, c) also writes save_mean / save_invstd and updates the running
 //      statistics (unbiased variance, count / (count - 1)).
-// This version reads x twice (once per launch).
-#include "hipo_common.h"
+// This path reads x twice (once per launch).
+#include "welford.h"
 
 namespace hipo {
 namespace {
@@ -24,50 +29,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
 
-struct Welford {
-  float n;
-  float mean;
-  float m2;
-};
-
 // max(v, 0) that keeps NaN (torch.relu propagates NaN; fmaxf would not).
 __device__ __forceinline__ float relu_f32(float v) { return v < 0.f ? 0.f : v; }
-
-// Chan et al. pairwise merge of two Welford triples.
-__device__ __forceinline__ Welford merge(Welford a, Welford b) {
-  const float n = a.n + b.n;
-  if (n == 0.f) return a;
-  const float wb = b.n / n;
-  const float d = b.mean - a.mean;
-  Welford r;
-  r.n = n;
-  r.mean = __builtin_fmaf(d, wb, a.mean);
-  r.m2 = a.m2 + b.m2 + d * d * a.n * wb;
-  return r;
-}
-
-template <int Ctrl>
-__device__ __forceinline__ Welford dpp_w(Welford w) {
-  return Welford{dpp<Ctrl>(w.n), dpp<Ctrl>(w.mean), dpp<Ctrl>(w.m2)};
-}
-
-__device__ __forceinline__ Welford lane_w(Welford w, int lane) {
-  return Welford{
-      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w.n), lane)),
-      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w.mean), lane)),
-      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w.m2), lane))};
-}
-
-// Whole-wave merge (all 64 lanes active); every lane gets the result.
-// Each step merges triples over disjoint lane sets.
-__device__ __forceinline__ Welford wave_welford(Welford w) {
-  w = merge(w, dpp_w<kDppQuadXor1>(w));
-  w = merge(w, dpp_w<kDppQuadXor2>(w));
-  w = merge(w, dpp_w<kDppRowRor4>(w));
-  w = merge(w, dpp_w<kDppRowRor8>(w));
-  return merge(merge(lane_w(w, 0), lane_w(w, 16)),
-               merge(lane_w(w, 32), lane_w(w, 48)));
-}
 
 // Exact statistics of up to 4*U values held by one thread, merged into acc.
 template <int U>
@@ -91,7 +54,7 @@ __device__ __forceinline__ void absorb(Welford& acc, const float4 (&v)[U],
       q += (a * a + b * b) + (c * c + d * d);
     }
   }
-  acc = merge(acc, Welford{cnt, m, q});
+  acc = welford_merge(acc, Welford{cnt, m, q});
 }
 
 // Planes handled by split s of S over N planes.
@@ -131,7 +94,8 @@ __global__ __launch_bounds__(kThreads) void bn_partial_stats_vec(
   if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = acc;
   __syncthreads();
   if (threadIdx.x == 0) {
-    Welford t = merge(merge(part[0], part[1]), merge(part[2], part[3]));
+    Welford t = welford_merge(welford_merge(part[0], part[1]),
+                              welford_merge(part[2], part[3]));
     float* dst = ws + (c * S + s) * 3;
     dst[0] = t.n;
     dst[1] = t.mean;
@@ -150,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void bn_partial_stats_scalar(
   for (int64_t n = n0; n < n1; ++n) {
     const float* plane = x + (n * C + c) * HW;
     for (int64_t i = threadIdx.x; i < HW; i += kThreads) {
-      acc = merge(acc, Welford{1.f, plane[i], 0.f});
+      acc = welford_merge(acc, Welford{1.f, plane[i], 0.f});
     }
   }
   acc = wave_welford(acc);
@@ -159,7 +123,8 @@ __global__ __launch_bounds__(kThreads) void bn_partial_stats_scalar(
   if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = acc;
   __syncthreads();
   if (threadIdx.x == 0) {
-    Welford t = merge(merge(part[0], part[1]), merge(part[2], part[3]));
+    Welford t = welford_merge(welford_merge(part[0], part[1]),
+                              welford_merge(part[2], part[3]));
     float* dst = ws + (c * S + s) * 3;
     dst[0] = t.n;
     dst[1] = t.mean;
@@ -269,7 +234,8 @@ extern "C" size_t hipo_batchnorm_workspace_bytes(int64_t n, int64_t c,
                                                  int64_t hw) {
   if (n <= 0 || c <= 0 || hw <= 0) return 0;
   const int64_t s = hipo::num_splits(n, c);
-  return static_cast<size_t>(c * s * 3) * sizeof(float);
+  return hipo::kBnCtlBytes + hipo::bn_fused_slot_bytes(n, c, hw) +
+         static_cast<size_t>(c * s * 3) * sizeof(float);
 }
 
 extern "C" int hipo_batchnorm_train_fwd_f32(
@@ -287,12 +253,19 @@ extern "C" int hipo_batchnorm_train_fwd_f32(
   HIPO_REQUIRE(workspace_bytes >= need,
                "batchnorm: workspace %zu bytes < required %zu", workspace_bytes,
                need);
+  HIPO_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 8 == 0,
+               "batchnorm: workspace must be 8-byte aligned");
+  const int fused = bn_fused_launch(x, gamma, beta, running_mean, running_var, y,
+                                    save_mean, save_invstd, n, c, hw, momentum,
+                                    eps, relu, workspace, stream);
+  if (fused >= 0) return fused;
+
   HIPO_REQUIRE(c <= 65535, "batchnorm: too many channels");
   const int64_t S = num_splits(n, c);
   const dim3 grid(static_cast<unsigned>(S), static_cast<unsigned>(c));
-  float* ws = static_cast<float*>(workspace);
-  const bool vec = hw % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(y) % 16 == 0;
+  float* ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + kBnCtlBytes +
+                                       bn_fused_slot_bytes(n, c, hw));
+  const bool vec = hw % 4 == 0 && aligned16(x) && aligned16(y);
   if (vec) {
     bn_partial_stats_vec<<<grid, dim3(kThreads), 0, stream>>>(x, ws, n, c, hw, S);
   } else {

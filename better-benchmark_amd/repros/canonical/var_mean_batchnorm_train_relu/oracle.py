@@ -2,10 +2,12 @@
 MI355X oracle for var_mean_batchnorm_train_relu: BatchNorm training forward
 + ReLU, save_mean / save_invstd, running statistics updated in place.
 
-Kernel: hipo_batchnorm_train_fwd_f32 -- split-K Welford partials per
-(channel, plane range) merged with Chan's formula, then the fused
-normalise + affine + ReLU epilogue and the running-stat update (unbiased
-variance).  Algorithmic bytes: 4 N C H W (read) + 4 N C H W (write) + O(C).
+Kernel: hipo_batchnorm_train_fwd_f32 -- one persistent launch that reads x
+once: each workgroup holds its slab of a channel in registers, the slabs'
+Welford partials are exchanged between workgroups (tagged atomic words) and
+merged with Chan's formula in fp64, then the same registers are normalised
+(affine + ReLU) and stored; running statistics use the unbiased variance.
+Algorithmic bytes: 4 N C H W (read) + 4 N C H W (write) + O(C).
 Replaces the Triton bodies of the reference's
 repros/canonical/var_mean_mean_19ffdb35cc67/oracle.py:167 and
 repros/canonical/var_mean_ceb5c315290a/oracle.py:238.
@@ -21,7 +23,7 @@ MOMENTUM = 0.1  # graph constants of repro.py
 EPS = 1e-05
 
 
-@oracle_impl(hardware="MI355X", point="7b860eea", description="BN train fwd + ReLU, split Welford")
+@oracle_impl(hardware="MI355X", point="7b860eea", description="BN train fwd + ReLU, single pass")
 @oracle_impl(hardware="MI355X", description="BN train fwd + ReLU, shape-general")
 def oracle_forward(inputs):
     x, gamma, beta, running_mean, running_var = inputs

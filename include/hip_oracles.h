@@ -116,7 +116,7 @@ int hipo_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma, uint16_t* y,
 
 /*
  * Bytes of device workspace hipo_batchnorm_train_fwd_f32 needs for this
- * shape (0 if the shape is unsupported).
+ * shape (0 if a size is not positive).
  */
 size_t hipo_batchnorm_workspace_bytes(int64_t n, int64_t c, int64_t hw);
 
@@ -130,9 +130,17 @@ size_t hipo_batchnorm_workspace_bytes(int64_t n, int64_t c, int64_t hw);
  *   running_var  = (1 - momentum) running_var
  *                  + momentum var * count / (count - 1)     (in place)
  * x, y are contiguous [n, c, hw]; gamma, beta, running_*, save_* are [c].
- * `workspace` is caller-allocated device memory of at least
- * hipo_batchnorm_workspace_bytes(n, c, hw) bytes; its contents on entry do
- * not matter.
+ * Supported shapes run as one persistent kernel that reads x once (HW a
+ * multiple of 4, 16-byte aligned x / y, x under 4 GiB); others as two
+ * split-K launches that read x twice.
+ * `workspace` is caller-allocated device memory, 8-byte aligned, of at
+ * least hipo_batchnorm_workspace_bytes(n, c, hw) bytes.  It must be
+ * zero-filled before its first use and then passed unmodified to later
+ * calls: the single-pass kernel keeps its cross-workgroup exchange state
+ * there (a completion count, a launch epoch, tagged partial statistics).
+ * Calls that share a workspace must be ordered (one stream); bytes 8..11
+ * hold a sticky error word, nonzero after an exchange wait timed out (the
+ * affected channels' outputs are then NaN).
  * Replaces the Triton bodies of oracle_forward in
  * repros/canonical/var_mean_mean_19ffdb35cc67/oracle.py:167 (one CTA per
  * channel) and repros/canonical/var_mean_ceb5c315290a/oracle.py:238

@@ -271,6 +271,67 @@ def test_batchnorm_closed_forms_and_edges(rocm_device):
     assert (y[:, :3] < 0).any(), "relu=False keeps negatives"
 
 
+# (N, C, HW, what the shape exercises in the single-pass kernel)
+BN_PLAN_SHAPES = [
+    (16, 300, 3136, "exact slabs, 1 slab/channel, 2 rounds (C > CUs)"),
+    (32, 8, 3136, "exact slabs, 2 slabs/channel, 1 round"),
+    (2, 6, 64, "masked V=4, one float4 row per thread"),
+    (5, 7, 1600, "masked V=8"),
+    (7, 5, 2800, "masked V=16"),
+    (30, 100, 4000, "masked V=24, 3 slabs/channel, 2 rounds"),
+    (2, 600, 16, "3 rounds (odd), tiny planes"),
+    (2, 1000, 16, "4 rounds (even)"),
+    (3, 20000, 16, "more than 64 rounds: split-K path"),
+    (4, 9, 60, "HW % 4 == 0 but F not a power of two"),
+]
+
+
+@pytest.mark.parametrize("n,c,hw,what", BN_PLAN_SHAPES, ids=[s[3] for s in BN_PLAN_SHAPES])
+def test_batchnorm_plans_vs_oracle(n, c, hw, what, rocm_device):
+    """Every instantiation of the single-pass kernel (and the split-K
+    fallback) against the CPU oracle, twice in a row on the shared workspace
+    (the second call runs under the next launch epoch)."""
+    import hip_oracles
+    import oracle as ref
+    print(f"[bn plan] {n}x{c}x{hw}: {what}", flush=True)
+    g = torch.Generator().manual_seed(n * 7919 + c * 31 + hw)
+    x = torch.randn(n, c, 1, hw, generator=g) * 2 + torch.linspace(-3, 5, c).view(1, c, 1, 1)
+    gamma = 1 + 0.1 * torch.randn(c, generator=g)
+    beta = 0.1 * torch.randn(c, generator=g)
+    rm, rv = 0.1 * torch.randn(c, generator=g), 1 + 0.1 * torch.rand(c, generator=g)
+    want = ref.batchnorm_train(x, gamma, beta, rm, rv, momentum=0.1, eps=1e-5, relu=True)
+    xd = x.to(rocm_device)
+    for call in range(2):
+        rm_d, rv_d = rm.to(rocm_device), rv.to(rocm_device)
+        y, sm, si = hip_oracles.batchnorm_train(xd, gamma.to(rocm_device), beta.to(rocm_device),
+                                                rm_d, rv_d, momentum=0.1, eps=1e-5, relu=True)
+        for name, a, w in zip(("y", "mean", "invstd", "rm", "rv"), (y, sm, si, rm_d, rv_d), want):
+            assert_close(a, w, F32_TOL, f"bn {n}x{c}x{hw} call {call} {name}")
+    assert hip_oracles.batchnorm_error_flag(rocm_device) == 0
+
+
+def test_batchnorm_workspace_contract(rocm_device):
+    """A caller-provided zeroed workspace works, is reusable across shapes,
+    and the shared one is never allocated inside graph capture."""
+    import hip_oracles
+    x = torch.randn(4, 8, 8, 8, device=rocm_device)
+    ones, zeros = torch.ones(8, device=rocm_device), torch.zeros(8, device=rocm_device)
+    need = max(hip_oracles.batchnorm_workspace_bytes(4, 8, 64),
+               hip_oracles.batchnorm_workspace_bytes(32, 8, 3136))
+    ws = torch.zeros(need, dtype=torch.uint8, device=rocm_device)
+    a = hip_oracles.batchnorm_train(x, ones, zeros, zeros.clone(), ones.clone(), momentum=0.1,
+                                    eps=1e-5, workspace=ws)
+    x2 = torch.randn(32, 8, 56, 56, device=rocm_device)
+    hip_oracles.batchnorm_train(x2, ones, zeros, zeros.clone(), ones.clone(), momentum=0.1,
+                                eps=1e-5, workspace=ws)
+    b = hip_oracles.batchnorm_train(x, ones, zeros, zeros.clone(), ones.clone(), momentum=0.1,
+                                    eps=1e-5, workspace=ws)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    assert int(ws[8:12].view(torch.int32).item()) == 0
+    assert int(ws[4:8].view(torch.int32).item()) == 3, "one epoch per launch"
+
+
 def test_graph_capture_replays_match_eager(rocm_device):
     """Each oracle is captured in a hipGraph and replayed several times with
     eager work in between; every replay must equal the eager call."""
