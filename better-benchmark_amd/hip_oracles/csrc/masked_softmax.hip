@@ -6,104 +6,101 @@
 // When `scale` is a power of two, x * scale is exact in fp32 and the first
 // rounding is the identity, so it is skipped.
 //
-// One wave64 per row, four rows per 256-thread workgroup.  A row of K
-// elements is held in registers: lane l owns elements [c*512 + 8l, +8) for
-// chunk c, read and written with one 16-byte access per chunk (each access
-// instruction covers 1 KiB of contiguous row).  The mask row (mask[q, :],
-// q = row % Q) is re-read by every batch entry and stays cache-resident.
-// Row max and row sum use DPP wave reductions.  HBM-bound: algorithmic bytes
-// per element = 2 (read) + 2 (write), plus the mask once.
-#include "hipo_common.h"
+// Layout (row_layout.h): W waves per row (W = 1 for K = 1024: one wave
+// holds a 2 KiB row), rows held in registers, non-temporal 16-byte
+// streaming accesses for x and out; the mask row (mask[q, :], q = row % Q)
+// is re-read by every batch entry and stays cache-resident.  Row max and
+// row sum: DPP within a wave, then a fixed-order combine of the W wave
+// results through LDS.  HBM-bound: algorithmic bytes per element = 2 (read)
+// + 2 (write), plus the mask once.
+#include "row_layout.h"
 
 namespace hipo {
 namespace {
 
-constexpr int kRowsPerBlock = 4;
-constexpr int kChunk = 8 * kWave;  // elements per 16-byte-per-lane chunk
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <int NCH, bool ROUND_SCALE>
-__global__ __launch_bounds__(256) void masked_softmax_rows(
+template <int U, bool ROUND_SCALE>
+__global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
     uint16_t* __restrict__ out, int64_t rows, int64_t Q, int64_t K,
-    int64_t mask_stride, float scale) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row =
-      static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;  // wave-uniform
-  const int64_t q = row % Q;
-  const uint16_t* xr = x + row * K;
+    int64_t mask_stride, float scale, int waves_per_row, int rows_per_block) {
+  __shared__ float pmax[kRowMaxWaves], psum[kRowMaxWaves];
+  const RowPlace p = row_place(waves_per_row, rows_per_block, rows);
+  const int64_t q = p.row % Q;
+  const uint16_t* xr = x + p.row * K;
   const uint16_t* mr = mask + q * mask_stride;
-  uint16_t* orow = out + row * K;
+  uint16_t* orow = out + p.row * K;
 
-  uint4 xv[NCH], mv[NCH];
+  u32x4_t xv[U], mv[U];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t col = static_cast<int64_t>(c) * kChunk + lane * 8;
-    if (col < K) {
-      xv[c] = *reinterpret_cast<const uint4*>(xr + col);
-      mv[c] = *reinterpret_cast<const uint4*>(mr + col);
-    } else {
-      xv[c] = make_uint4(0u, 0u, 0u, 0u);
-      mv[c] = make_uint4(0u, 0u, 0u, 0u);
-    }
+  for (int u = 0; u < U; ++u) {
+    const int64_t col = row_group_col(u, waves_per_row, p);
+    xv[u] = row_load_stream(xr, col, K);
+    mv[u] = row_load_cached(mr, col, K);
   }
 
-  float s[NCH][8];
+  float s[U][8];
   float m = -__builtin_inff();
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t col = static_cast<int64_t>(c) * kChunk + lane * 8;
-    const uint32_t xw[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
-    const uint32_t mw[4] = {mv[c].x, mv[c].y, mv[c].z, mv[c].w};
+  for (int u = 0; u < U; ++u) {
+    const bool in = row_group_col(u, waves_per_row, p) < K;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      float a0 = bf16lo(xw[d]) * scale;
-      float a1 = bf16hi(xw[d]) * scale;
+      float a0 = bf16lo(xv[u][d]) * scale;
+      float a1 = bf16hi(xv[u][d]) * scale;
       if (ROUND_SCALE) {
         const uint32_t r = pack_bf16x2(a0, a1);
         a0 = bf16lo(r);
         a1 = bf16hi(r);
       }
-      const uint32_t t = pack_bf16x2(a0 + bf16lo(mw[d]), a1 + bf16hi(mw[d]));
-      s[c][2 * d] = bf16lo(t);
-      s[c][2 * d + 1] = bf16hi(t);
-    }
-    if (col >= K) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s[c][e] = -__builtin_inff();
+      const uint32_t t = pack_bf16x2(a0 + bf16lo(mv[u][d]), a1 + bf16hi(mv[u][d]));
+      s[u][2 * d] = in ? bf16lo(t) : -__builtin_inff();
+      s[u][2 * d + 1] = in ? bf16hi(t) : -__builtin_inff();
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) m = fmaxf(m, s[c][e]);
+    for (int e = 0; e < 8; ++e) m = fmaxf(m, s[u][e]);
   }
   m = wave_max(m);
+  if (waves_per_row > 1) {
+    if (p.lane == 0) pmax[p.wave] = m;
+    __syncthreads();
+    const int first = p.wave - p.w;
+    m = pmax[first];
+    for (int k = 1; k < waves_per_row; ++k) m = fmaxf(m, pmax[first + k]);
+  }
 
   // exp(s - m) = 2^(s*log2e - m*log2e); (-inf) - (-inf) gives NaN exactly as
   // the eager formula does for an all-masked row.
   const float ml = m * kLog2e;
   float sum = 0.f;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
+  for (int u = 0; u < U; ++u) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      s[c][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][e], kLog2e, -ml));
-      sum += s[c][e];
+      s[u][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][e], kLog2e, -ml));
+      sum += s[u][e];
     }
   }
   sum = wave_sum(sum);
+  if (waves_per_row > 1) {
+    if (p.lane == 0) psum[p.wave] = sum;
+    __syncthreads();
+    const int first = p.wave - p.w;
+    sum = psum[first];
+    for (int k = 1; k < waves_per_row; ++k) sum += psum[first + k];
+  }
   const float inv = 1.0f / sum;
 
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t col = static_cast<int64_t>(c) * kChunk + lane * 8;
-    if (col < K) {
-      uint4 o;
-      o.x = pack_bf16x2(s[c][0] * inv, s[c][1] * inv);
-      o.y = pack_bf16x2(s[c][2] * inv, s[c][3] * inv);
-      o.z = pack_bf16x2(s[c][4] * inv, s[c][5] * inv);
-      o.w = pack_bf16x2(s[c][6] * inv, s[c][7] * inv);
-      *reinterpret_cast<uint4*>(orow + col) = o;
-    }
+  for (int u = 0; u < U; ++u) {
+    const int64_t col = row_group_col(u, waves_per_row, p);
+    u32x4_t o;
+    o[0] = pack_bf16x2(s[u][0] * inv, s[u][1] * inv);
+    o[1] = pack_bf16x2(s[u][2] * inv, s[u][3] * inv);
+    o[2] = pack_bf16x2(s[u][4] * inv, s[u][5] * inv);
+    o[3] = pack_bf16x2(s[u][6] * inv, s[u][7] * inv);
+    if (p.valid && col < K) row_store_stream(orow, col, o);
   }
 }
 
@@ -115,7 +112,7 @@ __global__ __launch_bounds__(256) void masked_softmax_rows_scalar(
     int64_t mask_stride, float scale, int round_scale) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row =
-      static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+      static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t q = row % Q;
   const uint16_t* xr = x + row * K;
@@ -147,16 +144,17 @@ bool is_power_of_two(float v) {
   return __builtin_frexpf(v, &e) == 0.5f;
 }
 
-template <int NCH>
-void launch_vec(bool round_scale, dim3 grid, hipStream_t stream,
+template <int U>
+void launch_vec(bool round_scale, dim3 grid, const RowPlan& plan, hipStream_t stream,
                 const uint16_t* x, const uint16_t* mask, uint16_t* out,
                 int64_t rows, int64_t Q, int64_t K, int64_t ms, float scale) {
+  const dim3 block(plan.threads());
   if (round_scale) {
-    masked_softmax_rows<NCH, true><<<grid, dim3(256), 0, stream>>>(
-        x, mask, out, rows, Q, K, ms, scale);
+    masked_softmax_rows<U, true><<<grid, block, 0, stream>>>(
+        x, mask, out, rows, Q, K, ms, scale, plan.waves_per_row, plan.rows_per_block);
   } else {
-    masked_softmax_rows<NCH, false><<<grid, dim3(256), 0, stream>>>(
-        x, mask, out, rows, Q, K, ms, scale);
+    masked_softmax_rows<U, false><<<grid, block, 0, stream>>>(
+        x, mask, out, rows, Q, K, ms, scale, plan.waves_per_row, plan.rows_per_block);
   }
 }
 
@@ -177,28 +175,24 @@ extern "C" int hipo_scaled_masked_softmax_bf16(const uint16_t* x,
   HIPO_REQUIRE(x && mask && out, "masked_softmax: null pointer");
   HIPO_REQUIRE(mask_row_stride >= k, "masked_softmax: mask_row_stride < k");
   const int64_t rows = batch * q;
-  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  HIPO_REQUIRE(blocks <= 0x7fffffff, "masked_softmax: too many rows");
-  const dim3 grid(static_cast<unsigned>(blocks));
   const bool round_scale = !is_power_of_two(scale);
-  const int64_t nch = (k + kChunk - 1) / kChunk;
-  const bool vec = (k % 8 == 0) && (mask_row_stride % 8 == 0) && nch <= 8 &&
-                   (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
-                   (reinterpret_cast<uintptr_t>(mask) % 16 == 0) &&
-                   (reinterpret_cast<uintptr_t>(out) % 16 == 0);
+  RowPlan plan;
+  const bool vec = (k % 8 == 0) && (mask_row_stride % 8 == 0) && row_plan(k, plan) &&
+                   aligned16(x) && aligned16(mask) && aligned16(out);
   if (vec) {
-    switch (nch) {
-      case 1: launch_vec<1>(round_scale, grid, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-      case 2: launch_vec<2>(round_scale, grid, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-      case 3: launch_vec<3>(round_scale, grid, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-      case 4: launch_vec<4>(round_scale, grid, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-      case 5: launch_vec<5>(round_scale, grid, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-      case 6: launch_vec<6>(round_scale, grid, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-      case 7: launch_vec<7>(round_scale, grid, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-      default: launch_vec<8>(round_scale, grid, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
+    const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "masked_softmax: too many rows");
+    const dim3 grid(static_cast<unsigned>(blocks));
+    switch (plan.groups) {
+      case 1: launch_vec<1>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
+      case 2: launch_vec<2>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
+      case 4: launch_vec<4>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
+      default: launch_vec<8>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
     }
   } else {
-    masked_softmax_rows_scalar<<<grid, dim3(256), 0, stream>>>(
+    const int64_t blocks = (rows + 3) / 4;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "masked_softmax: too many rows");
+    masked_softmax_rows_scalar<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
         x, mask, out, rows, q, k, mask_row_stride, scale, round_scale ? 1 : 0);
   }
   return check_launch("scaled_masked_softmax_bf16");

@@ -1,0 +1,123 @@
+// Work layout shared by the bf16 row kernels (LayerNorm, RMSNorm, softmax).
+//
+// A workgroup holds `rows_per_block` rows of `waves_per_row` waves each (at
+// most kRowMaxWaves waves).  A row of `cols` bf16 values is cut into groups
+// of 8 (16 bytes); lane l of wave w of a row owns groups
+//     g = (u * W + w) * 64 + l,   u = 0 .. U-1   (W = waves per row)
+// so each 16-byte access instruction of a wave covers 1 KiB of contiguous
+// row and the W waves sweep the row together.  The whole row stays in
+// registers between its statistics and its output.
+//
+// Waves whose row is past the last one still run (they take part in the
+// workgroup barrier): they read the last row and store nothing.  Groups
+// past the end of the row load the row's last group (the load stays in
+// bounds and needs no branch, which would make the compiler wait on each
+// load separately) and are zeroed.
+//
+// Per-wave footprint: the host picks W so that a wave holds about 4 KiB of
+// each streamed tensor (measured on MI355X for [16384, 4096]: 2 waves x 4
+// groups per lane, 2 rows per workgroup, non-temporal accesses reach 76 %
+// of 8 TB/s for RMSNorm and LayerNorm; one wave per row with 8 groups per
+// lane and cached accesses, 59-64 %).
+#pragma once
+
+#include <algorithm>
+
+#include "hipo_common.h"
+
+namespace hipo {
+
+constexpr int kRowMaxWaves = 8;
+constexpr int kRowMaxThreads = kRowMaxWaves * kWave;
+constexpr int kRowGroup = 8;                     // bf16 per 16-byte group
+constexpr int kRowSweep = kRowGroup * kWave;     // bf16 per wave per sweep
+
+struct RowPlace {
+  int lane;
+  int wave;     // in the workgroup
+  int w;        // in the row
+  int64_t row;  // clamped to the last row
+  bool valid;   // row < rows
+};
+
+__device__ __forceinline__ RowPlace row_place(int waves_per_row,
+                                              int rows_per_block,
+                                              int64_t rows) {
+  RowPlace p;
+  p.lane = threadIdx.x & (kWave - 1);
+  p.wave = threadIdx.x >> 6;
+  p.w = p.wave % waves_per_row;
+  const int64_t r =
+      static_cast<int64_t>(blockIdx.x) * rows_per_block + p.wave / waves_per_row;
+  p.valid = r < rows;
+  p.row = p.valid ? r : rows - 1;
+  return p;
+}
+
+// First column of the lane's u-th group.
+__device__ __forceinline__ int64_t row_group_col(int u, int waves_per_row,
+                                                 const RowPlace& p) {
+  return (static_cast<int64_t>(u * waves_per_row + p.w) * kWave + p.lane) *
+         kRowGroup;
+}
+
+// Valid values in wave w's groups of a row of `cols` (cols % 8 == 0).
+__device__ __forceinline__ int row_wave_count(int U, int waves_per_row,
+                                              const RowPlace& p, int64_t cols) {
+  int n = 0;
+  for (int u = 0; u < U; ++u) {
+    const int64_t first = static_cast<int64_t>(u * waves_per_row + p.w) * kRowSweep;
+    const int64_t left = cols - first;
+    n += static_cast<int>(left <= 0 ? 0 : (left < kRowSweep ? left : kRowSweep));
+  }
+  return n;
+}
+
+// 8 bf16 of `row` at `col` (non-temporal), or zeros past the row end.
+__device__ __forceinline__ u32x4_t row_load_stream(const uint16_t* row,
+                                                   int64_t col, int64_t cols) {
+  const int64_t c = col < cols ? col : cols - kRowGroup;
+  const u32x4_t v =
+      __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(row + c));
+  return col < cols ? v : u32x4_t{0u, 0u, 0u, 0u};
+}
+
+// 8 bf16 of a vector that every row re-reads (gamma, beta, mask rows):
+// cached load, zeros past the end.
+__device__ __forceinline__ u32x4_t row_load_cached(const uint16_t* v, int64_t col,
+                                                   int64_t cols) {
+  const int64_t c = col < cols ? col : cols - kRowGroup;
+  const u32x4_t r = *reinterpret_cast<const u32x4_t*>(v + c);
+  return col < cols ? r : u32x4_t{0u, 0u, 0u, 0u};
+}
+
+__device__ __forceinline__ void row_store_stream(uint16_t* row, int64_t col,
+                                                 u32x4_t v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(row + col));
+}
+
+// Host side: waves per row, groups per lane, rows per workgroup for a row of
+// `cols` bf16 values (cols % 8 == 0).  Groups per lane are rounded up to a
+// power of two (the kernels are instantiated for 1, 2, 4, 8); returns false
+// if the row does not fit in registers (cols > 8 waves x 8 groups x 512).
+struct RowPlan {
+  int waves_per_row;
+  int groups;  // U
+  int rows_per_block;
+  int threads() const { return waves_per_row * rows_per_block * kWave; }
+};
+
+inline bool row_plan(int64_t cols, RowPlan& plan) {
+  // About 4 groups (4 KiB) per lane-wave of each streamed tensor.
+  const int64_t per_wave = 4 * kRowSweep;
+  const int64_t w = std::min<int64_t>(kRowMaxWaves, (cols + per_wave - 1) / per_wave);
+  plan.waves_per_row = static_cast<int>(std::max<int64_t>(1, w));
+  const int64_t sweep = int64_t{plan.waves_per_row} * kRowSweep;
+  const int64_t u = (cols + sweep - 1) / sweep;
+  if (u > 8) return false;
+  plan.groups = u <= 1 ? 1 : u <= 2 ? 2 : u <= 4 ? 4 : 8;
+  plan.rows_per_block = std::max(1, 4 / plan.waves_per_row);
+  return true;
+}
+
+}  // namespace hipo

@@ -2,166 +2,152 @@
 //   residual-add LayerNorm  (outputs h, y, mean, rstd)
 //   RMSNorm                 (outputs y, rstd)
 //
-// One wave64 per row, four rows per 256-thread workgroup.  The row stays in
-// registers between the statistics and the normalisation: lane l owns
-// elements [c*512 + 8l, +8) of chunk c, moved with one 16-byte access per
-// chunk per tensor.  LayerNorm statistics are two-pass over the registers
-// (mean, then sum of squared deviations), reduced with DPP; gamma/beta rows
-// are re-read by every row and stay cache-resident.
+// Layout (row_layout.h): W waves per row, the row held in registers between
+// its statistics and its output, non-temporal 16-byte streaming accesses,
+// gamma / beta re-read by every row from cache.
+//
+// LayerNorm statistics are over the bf16-rounded h (the eager op order).
+// Each wave computes an exact two-pass (count, mean, M2) over its own
+// values in registers; the W triples of a row are merged with Chan's
+// formula through LDS in a fixed order (deterministic).  RMSNorm adds the
+// W wave sums of squares in a fixed order.
 //
 // HBM-bound.  Algorithmic bytes per row (cols = C):
 //   residual LayerNorm: 2C (x) + 2C (residual) + 2C (h) + 2C (y) + 8
 //   RMSNorm:            2C (x) + 2C (y) + 4
-#include "hipo_common.h"
+#include "row_layout.h"
+#include "welford.h"
 
 namespace hipo {
 namespace {
 
-constexpr int kRowsPerBlock = 4;
-constexpr int kChunk = 8 * kWave;
-
-template <int NCH>
-__global__ __launch_bounds__(256) void residual_layernorm_rows(
+template <int U>
+__global__ __launch_bounds__(kRowMaxThreads) void residual_layernorm_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
     const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
     uint16_t* __restrict__ h, uint16_t* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t rows,
-    int64_t cols, float eps) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row =
-      static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;  // wave-uniform
-  const int64_t base = row * cols;
+    int64_t cols, float eps, int waves_per_row, int rows_per_block) {
+  __shared__ Welford part[kRowMaxWaves];
+  const RowPlace p = row_place(waves_per_row, rows_per_block, rows);
+  const int64_t base = p.row * cols;
 
-  uint4 xv[NCH], rv[NCH];
+  u32x4_t hv[U], rv[U];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t col = static_cast<int64_t>(c) * kChunk + lane * 8;
-    if (col < cols) {
-      xv[c] = *reinterpret_cast<const uint4*>(x + base + col);
-      rv[c] = *reinterpret_cast<const uint4*>(res + base + col);
-    } else {
-      xv[c] = make_uint4(0u, 0u, 0u, 0u);
-      rv[c] = make_uint4(0u, 0u, 0u, 0u);
-    }
+  for (int u = 0; u < U; ++u) {
+    const int64_t col = row_group_col(u, waves_per_row, p);
+    hv[u] = row_load_stream(x + base, col, cols);
+    rv[u] = row_load_stream(res + base, col, cols);
   }
 
-  // h = bf16(x + residual); statistics use the bf16-rounded h.
-  uint4 hv[NCH];
+  // h = bf16(x + residual); statistics use the bf16-rounded h.  Groups past
+  // the row end are zero and add nothing to the sum.
   float sum = 0.f;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const uint32_t xw[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
-    const uint32_t rw[4] = {rv[c].x, rv[c].y, rv[c].z, rv[c].w};
-    uint32_t hw[4];
+  for (int u = 0; u < U; ++u) {
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      hw[d] = pack_bf16x2(bf16lo(xw[d]) + bf16lo(rw[d]),
-                          bf16hi(xw[d]) + bf16hi(rw[d]));
-      sum += bf16lo(hw[d]) + bf16hi(hw[d]);
+      hv[u][d] = pack_bf16x2(bf16lo(hv[u][d]) + bf16lo(rv[u][d]),
+                             bf16hi(hv[u][d]) + bf16hi(rv[u][d]));
+      sum += bf16lo(hv[u][d]) + bf16hi(hv[u][d]);
     }
-    hv[c] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    const int64_t col = static_cast<int64_t>(c) * kChunk + lane * 8;
-    if (col < cols) *reinterpret_cast<uint4*>(h + base + col) = hv[c];
+    const int64_t col = row_group_col(u, waves_per_row, p);
+    if (p.valid && col < cols) row_store_stream(h + base, col, hv[u]);
   }
-  const float fcols = static_cast<float>(cols);
-  const float mean = wave_sum(sum) / fcols;
-
+  const float n = static_cast<float>(row_wave_count(U, waves_per_row, p, cols));
+  const float wmean = n > 0.f ? wave_sum(sum) / n : 0.f;
   float sq = 0.f;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t col = static_cast<int64_t>(c) * kChunk + lane * 8;
-    if (col < cols) {
-      const uint32_t w[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const float a = bf16lo(w[d]) - mean;
-        const float b = bf16hi(w[d]) - mean;
-        sq = __builtin_fmaf(a, a, sq);
-        sq = __builtin_fmaf(b, b, sq);
-      }
-    }
-  }
-  const float var = wave_sum(sq) / fcols;
-  const float rstd = 1.0f / __builtin_sqrtf(var + eps);
-  const float shift = -mean * rstd;
-
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t col = static_cast<int64_t>(c) * kChunk + lane * 8;
-    if (col < cols) {
-      const uint4 gv = *reinterpret_cast<const uint4*>(gamma + col);
-      const uint4 bv = *reinterpret_cast<const uint4*>(beta + col);
-      const uint32_t w[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
-      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-      const uint32_t bw[4] = {bv.x, bv.y, bv.z, bv.w};
-      uint32_t o[4];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const float n0 = __builtin_fmaf(bf16lo(w[d]), rstd, shift);
-        const float n1 = __builtin_fmaf(bf16hi(w[d]), rstd, shift);
-        o[d] = pack_bf16x2(__builtin_fmaf(n0, bf16lo(gw[d]), bf16lo(bw[d])),
-                           __builtin_fmaf(n1, bf16hi(gw[d]), bf16hi(bw[d])));
-      }
-      *reinterpret_cast<uint4*>(y + base + col) = make_uint4(o[0], o[1], o[2], o[3]);
-    }
-  }
-  if (lane == 0) {
-    mean_out[row] = mean;
-    rstd_out[row] = rstd;
-  }
-}
-
-template <int NCH>
-__global__ __launch_bounds__(256) void rmsnorm_rows(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
-    uint16_t* __restrict__ y, float* __restrict__ rstd_out, int64_t rows,
-    int64_t cols, float eps) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row =
-      static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int64_t base = row * cols;
-
-  uint4 xv[NCH];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t col = static_cast<int64_t>(c) * kChunk + lane * 8;
-    xv[c] = col < cols ? *reinterpret_cast<const uint4*>(x + base + col)
-                       : make_uint4(0u, 0u, 0u, 0u);
-  }
-  float sq = 0.f;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const uint32_t w[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+  for (int u = 0; u < U; ++u) {
+    const bool in = row_group_col(u, waves_per_row, p) < cols;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const float a = bf16lo(w[d]);
-      const float b = bf16hi(w[d]);
+      const float a = in ? bf16lo(hv[u][d]) - wmean : 0.f;
+      const float b = in ? bf16hi(hv[u][d]) - wmean : 0.f;
       sq = __builtin_fmaf(a, a, sq);
       sq = __builtin_fmaf(b, b, sq);
     }
   }
-  const float ms = wave_sum(sq) / static_cast<float>(cols);
-  const float rstd = 1.0f / __builtin_sqrtf(ms + eps);
+  Welford t{n, wmean, wave_sum(sq)};
+  if (waves_per_row > 1) {
+    if (p.lane == 0) part[p.wave] = t;
+    __syncthreads();
+    const int first = p.wave - p.w;
+    t = part[first];
+    for (int k = 1; k < waves_per_row; ++k) t = welford_merge(t, part[first + k]);
+  }
+  const float mean = t.mean;
+  const float rstd = 1.0f / __builtin_sqrtf(t.m2 / static_cast<float>(cols) + eps);
+  const float shift = -mean * rstd;
 
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t col = static_cast<int64_t>(c) * kChunk + lane * 8;
-    if (col < cols) {
-      const uint4 gv = *reinterpret_cast<const uint4*>(gamma + col);
-      const uint32_t w[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
-      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-      uint32_t o[4];
+  for (int u = 0; u < U; ++u) {
+    const int64_t col = row_group_col(u, waves_per_row, p);
+    const u32x4_t gv = row_load_cached(gamma, col, cols);
+    const u32x4_t bv = row_load_cached(beta, col, cols);
+    u32x4_t o;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        o[d] = pack_bf16x2((bf16lo(w[d]) * rstd) * bf16lo(gw[d]),
-                           (bf16hi(w[d]) * rstd) * bf16hi(gw[d]));
-      }
-      *reinterpret_cast<uint4*>(y + base + col) = make_uint4(o[0], o[1], o[2], o[3]);
+    for (int d = 0; d < 4; ++d) {
+      const float n0 = __builtin_fmaf(bf16lo(hv[u][d]), rstd, shift);
+      const float n1 = __builtin_fmaf(bf16hi(hv[u][d]), rstd, shift);
+      o[d] = pack_bf16x2(__builtin_fmaf(n0, bf16lo(gv[d]), bf16lo(bv[d])),
+                         __builtin_fmaf(n1, bf16hi(gv[d]), bf16hi(bv[d])));
+    }
+    if (p.valid && col < cols) row_store_stream(y + base, col, o);
+  }
+  if (p.valid && p.w == 0 && p.lane == 0) {
+    mean_out[p.row] = mean;
+    rstd_out[p.row] = rstd;
+  }
+}
+
+template <int U>
+__global__ __launch_bounds__(kRowMaxThreads) void rmsnorm_rows(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
+    uint16_t* __restrict__ y, float* __restrict__ rstd_out, int64_t rows,
+    int64_t cols, float eps, int waves_per_row, int rows_per_block) {
+  __shared__ float part[kRowMaxWaves];
+  const RowPlace p = row_place(waves_per_row, rows_per_block, rows);
+  const int64_t base = p.row * cols;
+
+  u32x4_t xv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    xv[u] = row_load_stream(x + base, row_group_col(u, waves_per_row, p), cols);
+  float sq = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const float a = bf16lo(xv[u][d]);
+      const float b = bf16hi(xv[u][d]);
+      sq = __builtin_fmaf(a, a, sq);
+      sq = __builtin_fmaf(b, b, sq);
     }
   }
-  if (lane == 0) rstd_out[row] = rstd;
+  sq = wave_sum(sq);
+  if (waves_per_row > 1) {
+    if (p.lane == 0) part[p.wave] = sq;
+    __syncthreads();
+    const int first = p.wave - p.w;
+    sq = part[first];
+    for (int k = 1; k < waves_per_row; ++k) sq += part[first + k];
+  }
+  const float rstd = 1.0f / __builtin_sqrtf(sq / static_cast<float>(cols) + eps);
+
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t col = row_group_col(u, waves_per_row, p);
+    const u32x4_t gv = row_load_cached(gamma, col, cols);
+    u32x4_t o;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      o[d] = pack_bf16x2((bf16lo(xv[u][d]) * rstd) * bf16lo(gv[d]),
+                         (bf16hi(xv[u][d]) * rstd) * bf16hi(gv[d]));
+    }
+    if (p.valid && col < cols) row_store_stream(y + base, col, o);
+  }
+  if (p.valid && p.w == 0 && p.lane == 0) rstd_out[p.row] = rstd;
 }
 
 // Any cols / alignment: one wave per row, scalar accesses, row re-read from
@@ -174,7 +160,7 @@ __global__ __launch_bounds__(256) void residual_layernorm_rows_scalar(
     int64_t cols, float eps) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row =
-      static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+      static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t base = row * cols;
   float sum = 0.f;
@@ -211,7 +197,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_scalar(
     int64_t cols, float eps) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row =
-      static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+      static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t base = row * cols;
   float sq = 0.f;
@@ -231,16 +217,12 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_scalar(
 }  // namespace
 }  // namespace hipo
 
-#define HIPO_NCH_SWITCH(nch, KERNEL, grid, stream, ...)                      \
-  switch (nch) {                                                             \
-    case 1: KERNEL<1><<<grid, dim3(256), 0, stream>>>(__VA_ARGS__); break;   \
-    case 2: KERNEL<2><<<grid, dim3(256), 0, stream>>>(__VA_ARGS__); break;   \
-    case 3: KERNEL<3><<<grid, dim3(256), 0, stream>>>(__VA_ARGS__); break;   \
-    case 4: KERNEL<4><<<grid, dim3(256), 0, stream>>>(__VA_ARGS__); break;   \
-    case 5: KERNEL<5><<<grid, dim3(256), 0, stream>>>(__VA_ARGS__); break;   \
-    case 6: KERNEL<6><<<grid, dim3(256), 0, stream>>>(__VA_ARGS__); break;   \
-    case 7: KERNEL<7><<<grid, dim3(256), 0, stream>>>(__VA_ARGS__); break;   \
-    default: KERNEL<8><<<grid, dim3(256), 0, stream>>>(__VA_ARGS__); break;  \
+#define HIPO_ROW_SWITCH(plan, KERNEL, grid, stream, ...)                            \
+  switch ((plan).groups) {                                                          \
+    case 1: KERNEL<1><<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; \
+    case 2: KERNEL<2><<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; \
+    case 4: KERNEL<4><<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; \
+    default: KERNEL<8><<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; \
   }
 
 extern "C" int hipo_residual_layernorm_bf16(
@@ -254,18 +236,21 @@ extern "C" int hipo_residual_layernorm_bf16(
   HIPO_REQUIRE(cols > 0, "residual_layernorm: cols must be > 0");
   HIPO_REQUIRE(x && residual && gamma && beta && h && y && mean && rstd,
                "residual_layernorm: null pointer");
-  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  HIPO_REQUIRE(blocks <= 0x7fffffff, "residual_layernorm: too many rows");
-  const dim3 grid(static_cast<unsigned>(blocks));
-  const int64_t nch = (cols + kChunk - 1) / kChunk;
-  const bool vec = cols % 8 == 0 && nch <= 8 && aligned16(x) &&
+  RowPlan plan;
+  const bool vec = cols % 8 == 0 && row_plan(cols, plan) && aligned16(x) &&
                    aligned16(residual) && aligned16(gamma) && aligned16(beta) &&
                    aligned16(h) && aligned16(y);
   if (vec) {
-    HIPO_NCH_SWITCH(nch, residual_layernorm_rows, grid, stream, x, residual,
-                    gamma, beta, h, y, mean, rstd, rows, cols, eps);
+    const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "residual_layernorm: too many rows");
+    const dim3 grid(static_cast<unsigned>(blocks));
+    HIPO_ROW_SWITCH(plan, residual_layernorm_rows, grid, stream, x, residual,
+                    gamma, beta, h, y, mean, rstd, rows, cols, eps,
+                    plan.waves_per_row, plan.rows_per_block);
   } else {
-    residual_layernorm_rows_scalar<<<grid, dim3(256), 0, stream>>>(
+    const int64_t blocks = (rows + 3) / 4;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "residual_layernorm: too many rows");
+    residual_layernorm_rows_scalar<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
         x, residual, gamma, beta, h, y, mean, rstd, rows, cols, eps);
   }
   return check_launch("residual_layernorm_bf16");
@@ -280,18 +265,20 @@ extern "C" int hipo_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma,
   if (rows == 0) return 0;
   HIPO_REQUIRE(cols > 0, "rmsnorm: cols must be > 0");
   HIPO_REQUIRE(x && gamma && y && rstd, "rmsnorm: null pointer");
-  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  HIPO_REQUIRE(blocks <= 0x7fffffff, "rmsnorm: too many rows");
-  const dim3 grid(static_cast<unsigned>(blocks));
-  const int64_t nch = (cols + kChunk - 1) / kChunk;
-  const bool vec = cols % 8 == 0 && nch <= 8 && aligned16(x) &&
+  RowPlan plan;
+  const bool vec = cols % 8 == 0 && row_plan(cols, plan) && aligned16(x) &&
                    aligned16(gamma) && aligned16(y);
   if (vec) {
-    HIPO_NCH_SWITCH(nch, rmsnorm_rows, grid, stream, x, gamma, y, rstd, rows,
-                    cols, eps);
+    const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "rmsnorm: too many rows");
+    const dim3 grid(static_cast<unsigned>(blocks));
+    HIPO_ROW_SWITCH(plan, rmsnorm_rows, grid, stream, x, gamma, y, rstd, rows,
+                    cols, eps, plan.waves_per_row, plan.rows_per_block);
   } else {
-    rmsnorm_rows_scalar<<<grid, dim3(256), 0, stream>>>(x, gamma, y, rstd, rows,
-                                                        cols, eps);
+    const int64_t blocks = (rows + 3) / 4;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "rmsnorm: too many rows");
+    rmsnorm_rows_scalar<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
+        x, gamma, y, rstd, rows, cols, eps);
   }
   return check_launch("rmsnorm_bf16");
 }

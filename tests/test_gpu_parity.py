@@ -239,6 +239,43 @@ def test_norm_shapes_off_vector_path(rocm_device):
             assert_close(a, w, _tol(w), f"rms {rows}x{cols} {name}")
 
 
+def test_row_layouts_multiwave(rocm_device):
+    """Row kernels with several waves per row: ragged last groups, waves with
+    no valid group, rows not a multiple of rows-per-block, the largest row on
+    the register path (8 waves x 8 groups x 512 bf16) and one past it."""
+    import hip_oracles
+    import oracle as ref
+    bf = torch.bfloat16
+    for rows, cols in [(5, 4104), (3, 20000), (9, 1032), (2, 32768), (2, 32776), (7, 2056)]:
+        print(f"[multiwave] norms {rows}x{cols}", flush=True)
+        g = torch.Generator().manual_seed(rows + cols)
+        x = (torch.randn(rows, cols, generator=g) + 0.5).to(bf)
+        r = torch.randn(rows, cols, generator=g).to(bf)
+        gm = (1 + 0.1 * torch.randn(cols, generator=g)).to(bf)
+        bt = (0.1 * torch.randn(cols, generator=g)).to(bf)
+        got = hip_oracles.residual_layernorm(*(t.to(rocm_device) for t in (x, r, gm, bt)), 1e-5)
+        want = ref.residual_layernorm(x, r, gm, bt, 1e-5)
+        for name, a, w in zip(("h", "y", "mean", "rstd"), got, want):
+            assert_close(a, w, _tol(w), f"ln {rows}x{cols} {name}")
+        got = hip_oracles.rmsnorm(x.to(rocm_device), gm.to(rocm_device), 1e-5)
+        want = ref.rmsnorm(x, gm, 1e-5)
+        for name, a, w in zip(("y", "rstd"), got, want):
+            assert_close(a, w, _tol(w), f"rms {rows}x{cols} {name}")
+    for b, q, k in [(2, 5, 4104), (1, 3, 20000), (3, 17, 1032), (1, 2, 32768)]:
+        print(f"[multiwave] softmax {b}x{q}x{k}", flush=True)
+        g = torch.Generator().manual_seed(b * q + k)
+        x = torch.randn(b, q, k, generator=g).to(bf)
+        mask = torch.triu(torch.full((q, k), float("-inf")), 1).to(bf)
+        got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), mask.to(rocm_device), 0.125)
+        assert_close(got, ref.scaled_masked_softmax(x, mask, 0.125), BF16_TOL, f"softmax {b}x{q}x{k}")
+    for rows, cols in [(3, 4), (9, 132), (5, 1028), (4, 4100), (2, 32772), (2, 100000), (17, 4096)]:
+        print(f"[multiwave] row_mean {rows}x{cols}", flush=True)
+        g = torch.Generator().manual_seed(rows * 7 + cols)
+        x = torch.randn(rows, cols, generator=g) * 3 + 1
+        assert_close(hip_oracles.row_mean(x.to(rocm_device)), ref.row_mean(x), F32_TOL,
+                     f"row_mean {rows}x{cols}")
+
+
 def test_batchnorm_closed_forms_and_edges(rocm_device):
     import hip_oracles
     import oracle as ref
