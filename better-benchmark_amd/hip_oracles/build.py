@@ -76,18 +76,12 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     """Compile every source and link the shared library; returns its path."""
     cc = hipcc()
     BUILD_DIR.mkdir(exist_ok=True)
-    sys.path.insert(0, str(PKG_DIR))
-    try:
-        from gen_tables import write_tables  # build-time lookup tables
-    finally:
-        sys.path.pop(0)
-    write_tables(BUILD_DIR)
     objs = []
     cmds = []
     for src in SOURCES:
         obj = BUILD_DIR / (Path(src).stem + ".o")
         objs.append(obj)
-        cmds.append([cc, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", f"-I{BUILD_DIR}",
+        cmds.append([cc, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}",
                      "-c", str(CSRC / src), "-o", str(obj)])
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
         list(pool.map(lambda c: _run(c, verbose), cmds))

@@ -2,186 +2,110 @@
 //
 // Semantics (the eager op order of gelu(x + bias) on bf16 tensors):
 //   t = bf16(x + bias[c])            (fp32 add, round to nearest even)
-//   y = bf16(GELU_tanh(t))
-// Because t is a bf16 value there are only 65536 possible inputs to GELU,
-// so GELU is a table lookup: kGeluLut[bits(t)] holds the correctly rounded
-// bf16 GELU of every bf16 pattern (generated at build time in double
-// precision by hip_oracles/gen_tables.py and compiled into the code object).
-// That replaces ~17 VALU cycles per element (two quarter-rate
-// transcendentals) with ~5 VALU operations and one LDS read, leaving the
-// kernel bound by HBM instead of VALU.
+//   y = bf16(GELU_tanh(t))           (fp32 arithmetic, one rounding)
+// GELU_tanh(t) = 0.5 t (1 + tanh(u)), u = sqrt(2/pi) (t + 0.044715 t^3), is
+// evaluated as the same function in the form
+//   t * sigmoid(2u) = t / (1 + 2^z),   z = t * (K0 + K1 t^2),
+//   K0 = -2 sqrt(2/pi) log2(e),  K1 = 0.044715 K0,
+// with the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32): one FMA,
+// three multiplies, one add and two transcendentals per value.  This form
+// keeps the small negative tail that 1 + tanh(u) cancels to zero, gives
+// +inf at +inf and NaN at -inf (as -inf * 0 in the tanh form), and rounds to
+// the same bf16 as the correctly rounded function except within a few fp32
+// ulps of a bf16 rounding boundary.
 //
-// Layout: each workgroup (1024 threads, one per CU) first copies the 128 KiB
-// table into LDS.  Work unit = one wave64 tile: 64 channels x 64 spatial
-// positions of one image.  Lane l owns an 8x8 (channel x position) block:
-// cb = l / 8 picks 8 channels, hb = l % 8 picks 8 positions.  It issues 8
-// 16-byte loads, one per channel row (the 8 lanes of equal cb read one
-// contiguous 128-byte segment of that row), and 8 16-byte stores, one per
-// position (the 8 lanes of equal hb write one contiguous 128-byte segment of
-// that NHWC row).  The 8x8 transpose happens in registers: the packed bf16
-// conversion (v_cvt_pk_bf16_f32) rounds t for two adjacent channels into one
-// word, whose halves index the table, and the two looked-up halves form the
-// output word -- no LDS staging of the tile and no barrier per tile.
-//
-// Scheduling: persistent waves walk tiles t, t + W, ... (W = waves in the
-// grid), prefetching the next tile into a second register buffer while the
-// current one is computed (two buffers used alternately, so no register copy
-// forces a wait on the prefetch).  Tiles are numbered channel group fastest,
-// then position tile, then image.  Within a workgroup, groups of C/64 waves
-// take all channel groups of one position tile, so each group writes whole
-// NHWC rows at once, and the groups are spread gridDim.x position tiles
-// apart (measured on MI355X: 69.9 us for config 2 against 83 us when a
-// workgroup's waves take consecutive tiles).  Loads and stores are
-// non-temporal.
+// Layout: one wave64 per tile of 64 channels x 64 spatial positions of one
+// image.  Lane l owns an 8x8 (channel x position) block: cb = l / 8 picks 8
+// channels, hb = l % 8 picks 8 positions.  It issues 8 16-byte loads, one
+// per channel row (the 8 lanes of equal cb read one contiguous 128-byte
+// segment of that row), and 8 16-byte stores, one per position (the 8 lanes
+// of equal hb write one contiguous 128-byte segment of that NHWC row); the
+// 8x8 transpose happens in registers, with no LDS and no barrier.  Tiles are
+// numbered channel group fastest, then position tile, then image; a 256-
+// thread workgroup takes four consecutive tiles (with C = 256: all channel
+// groups of one position tile, i.e. 64 whole NHWC rows).  The grid is one-
+// shot (no persistent loop): on MI355X many short workgroups dispatched in
+// order keep the chip's in-flight address window compact, which measured
+// 67.5 us for config 2 against 71 us for a persistent one-workgroup-per-CU
+// version of this kernel with the GELU read from a 128 KiB LDS table.
+// Loads and stores are non-temporal.
 // HBM-bound: algorithmic bytes per element = 2 (read) + 2 (write).
 #include "hipo_common.h"
 
 namespace hipo {
 namespace {
 
-// bf16 bits of GELU_tanh(t) for every bf16 bit pattern t.
-__device__ const uint16_t kGeluLut[65536] = {
-#include "gelu_tanh_bf16_lut.inc"
-};
+constexpr int kTileHw = 64;  // positions per wave tile
+constexpr int kTileC = 64;   // channels per wave tile
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlockThreads = kWavesPerBlock * kWave;
 
-constexpr int kTileHw = 64;    // positions per wave tile
-constexpr int kTileC = 64;     // channels per wave tile
-constexpr int kBlockThreads = 1024;
-constexpr int kWavesPerBlock = kBlockThreads / kWave;
+constexpr float kGeluK0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+constexpr float kGeluK1 = kGeluK0 * 0.044715f;
+
+__device__ __forceinline__ float gelu_tanh_f32(float t) {
+  const float z = t * __builtin_fmaf(kGeluK1, t * t, kGeluK0);
+  return t * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
+}
 
 struct TileGeom {
   int64_t C, HW;
   int c_tiles, hw_tiles, ntiles;  // ntiles < 2^31 (checked on the host)
 };
 
-// Base element offsets of lane's 8x8 block in tile t; false if the lane's
-// block lies outside the tensor (partial channel / position tiles).  t is
-// wave-uniform, so the tile decomposition runs on the scalar unit.
-__device__ __forceinline__ bool tile_block(const TileGeom& g, int t, int lane,
-                                           int64_t& in_off, int64_t& out_off,
-                                           int64_t& c0) {
-  t = __builtin_amdgcn_readfirstlane(t);
+__global__ __launch_bounds__(kBlockThreads) void bias_gelu_nchw_to_nhwc_tiles(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ out, TileGeom g) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = __builtin_amdgcn_readfirstlane(
+      static_cast<int>(blockIdx.x) * kWavesPerBlock + static_cast<int>(threadIdx.x >> 6));
+  if (t >= g.ntiles) return;  // wave-uniform; the kernel has no barrier
   const int ct = t % g.c_tiles;
   const int rest = t / g.c_tiles;
   const int ht = rest % g.hw_tiles;
   const int64_t img = rest / g.hw_tiles;
-  c0 = static_cast<int64_t>(ct) * kTileC + (lane >> 3) * 8;
+  const int64_t c0 = static_cast<int64_t>(ct) * kTileC + (lane >> 3) * 8;
   const int64_t p0 = static_cast<int64_t>(ht) * kTileHw + (lane & 7) * 8;
-  in_off = (img * g.C + c0) * g.HW + p0;
-  out_off = (img * g.HW + p0) * g.C + c0;
-  return c0 < g.C && p0 < g.HW;
-}
+  // Lanes outside a partial tile load from the tile's first block (always in
+  // bounds, no branch around the loads) and store nothing.
+  const bool ok = c0 < g.C && p0 < g.HW;
+  const int64_t cl = ok ? c0 : static_cast<int64_t>(ct) * kTileC;
+  const int64_t pl = ok ? p0 : static_cast<int64_t>(ht) * kTileHw;
+  const int64_t in_off = (img * g.C + cl) * g.HW + pl;
 
-// One lane's share of a tile in flight: 8 channel rows of 8 positions and
-// the 8 channel biases, plus where the results go.
-struct Block {
   u32x4_t v[8];
-  u32x4_t bw;
-  int64_t out_off;
-  bool ok;
-};
-
-// Issue the 9 loads of tile t.  Lanes outside the tensor load from offset 0
-// (always valid) and are masked at the store, so the loads are branch-free.
-__device__ __forceinline__ void load_block(const TileGeom& g, int t, int lane,
-                                           const u32x4_t* __restrict__ x,
-                                           const uint16_t* __restrict__ bias, Block& b) {
-  int64_t in_off, c0;
-  b.ok = tile_block(g, t, lane, in_off, b.out_off, c0);
-  if (!b.ok) {
-    in_off = 0;
-    c0 = 0;
-  }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    b.v[j] = __builtin_nontemporal_load(x + ((in_off + j * g.HW) >> 3));
-  }
-  b.bw = *reinterpret_cast<const u32x4_t*>(bias + c0);
-}
-
-// Output word for position i and channels (2k, 2k+1): round t for both
-// channels into one word, look both halves up in the table.
-__device__ __forceinline__ uint32_t gelu_pair(const uint16_t* lut, const Block& blk,
-                                              const float (&b)[8], int i, int k) {
-  const uint32_t w0 = blk.v[2 * k][i >> 1];
-  const uint32_t w1 = blk.v[2 * k + 1][i >> 1];
-  const float x0 = (i & 1) ? bf16hi(w0) : bf16lo(w0);
-  const float x1 = (i & 1) ? bf16hi(w1) : bf16lo(w1);
-  const uint32_t t = pack_bf16x2(x0 + b[2 * k], x1 + b[2 * k + 1]);
-  return static_cast<uint32_t>(lut[t & 0xffffu]) |
-         (static_cast<uint32_t>(lut[t >> 16]) << 16);
-}
-
-__device__ __forceinline__ void compute_store(const uint16_t* lut, const Block& blk,
-                                              u32x4_t* __restrict__ out, int64_t C) {
+  for (int j = 0; j < 8; ++j)
+    v[j] = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t*>(x + in_off + j * g.HW));
+  const u32x4_t bw = *reinterpret_cast<const u32x4_t*>(bias + cl);
   float b[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) b[j] = (j & 1) ? bf16hi(blk.bw[j >> 1]) : bf16lo(blk.bw[j >> 1]);
+  for (int j = 0; j < 8; ++j) b[j] = (j & 1) ? bf16hi(bw[j >> 1]) : bf16lo(bw[j >> 1]);
+
+  if (!ok) return;
+  const int64_t out_off = (img * g.HW + p0) * g.C + c0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const u32x4_t o = {gelu_pair(lut, blk, b, i, 0), gelu_pair(lut, blk, b, i, 1),
-                       gelu_pair(lut, blk, b, i, 2), gelu_pair(lut, blk, b, i, 3)};
-    if (blk.ok) __builtin_nontemporal_store(o, out + ((blk.out_off + i * C) >> 3));
-  }
-}
-
-__global__ __launch_bounds__(kBlockThreads) void bias_gelu_nchw_to_nhwc_tiles(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ bias,
-    uint16_t* __restrict__ out, TileGeom g) {
-  __shared__ u32x4_t lut_words[65536 * 2 / 16];
-  {
-    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(kGeluLut);
+    // Position p0 + i, channels c0 .. c0 + 7: round t for two channels into
+    // one word (v_cvt_pk_bf16_f32), GELU both halves, pack the results.
+    u32x4_t o;
 #pragma unroll
-    for (int k = 0; k < 65536 * 2 / 16 / kBlockThreads; ++k) {
-      lut_words[threadIdx.x + k * kBlockThreads] = src[threadIdx.x + k * kBlockThreads];
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t w0 = v[2 * k][i >> 1];
+      const uint32_t w1 = v[2 * k + 1][i >> 1];
+      const float x0 = (i & 1) ? bf16hi(w0) : bf16lo(w0);
+      const float x1 = (i & 1) ? bf16hi(w1) : bf16lo(w1);
+      const uint32_t tt = pack_bf16x2(x0 + b[2 * k], x1 + b[2 * k + 1]);
+      o[k] = pack_bf16x2(gelu_tanh_f32(bf16lo(tt)), gelu_tanh_f32(bf16hi(tt)));
     }
-  }
-  __syncthreads();
-  const uint16_t* lut = reinterpret_cast<const uint16_t*>(lut_words);
-
-  const int lane = threadIdx.x & (kWave - 1);
-  const int nwaves = static_cast<int>(gridDim.x) * kWavesPerBlock;
-  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  int t;
-  if (kWavesPerBlock % g.c_tiles == 0) {
-    // Groups of c_tiles waves take all channel tiles of one position tile
-    // (so a group writes whole NHWC rows together); the groups of a
-    // workgroup are spread gridDim.x position tiles apart.
-    const int group = w / g.c_tiles;
-    t = (static_cast<int>(blockIdx.x) + group * static_cast<int>(gridDim.x)) * g.c_tiles +
-        w % g.c_tiles;
-  } else {
-    t = static_cast<int>(blockIdx.x) + w * static_cast<int>(gridDim.x);
-  }
-  if (t >= g.ntiles) return;  // wave-uniform; after the only barrier
-  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x);
-  u32x4_t* ov = reinterpret_cast<u32x4_t*>(out);
-
-  // Software pipeline with two register buffers used alternately: the next
-  // tile's loads are in flight while the current tile is computed, and no
-  // register copy (which would wait for those loads) separates iterations.
-  Block a, b;
-  load_block(g, t, lane, xv, bias, a);
-  while (true) {
-    if (t + nwaves >= g.ntiles) {
-      compute_store(lut, a, ov, g.C);
-      break;
-    }
-    load_block(g, t + nwaves, lane, xv, bias, b);
-    compute_store(lut, a, ov, g.C);
-    t += nwaves;
-    if (t + nwaves >= g.ntiles) {
-      compute_store(lut, b, ov, g.C);
-      break;
-    }
-    load_block(g, t + nwaves, lane, xv, bias, a);
-    compute_store(lut, b, ov, g.C);
-    t += nwaves;
+    __builtin_nontemporal_store(
+        o, reinterpret_cast<u32x4_t*>(out + out_off + static_cast<int64_t>(i) * g.C));
   }
 }
 
 // Any shape: one thread per output element, NHWC order (coalesced stores,
-// strided loads), table read from global memory.
+// strided loads); same arithmetic as the tile kernel.
 __global__ __launch_bounds__(256) void bias_gelu_nchw_to_nhwc_scalar(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ out, int64_t N, int64_t C, int64_t HW) {
@@ -191,8 +115,9 @@ __global__ __launch_bounds__(256) void bias_gelu_nchw_to_nhwc_scalar(
     const int64_t c = o % C;
     const int64_t p = (o / C) % HW;
     const int64_t img = o / (C * HW);
-    const float t = bf16_to_f32(x[(img * C + c) * HW + p]) + bf16_to_f32(bias[c]);
-    out[o] = kGeluLut[pack_bf16x2(t, 0.0f) & 0xffffu];
+    const float t =
+        round_bf16(bf16_to_f32(x[(img * C + c) * HW + p]) + bf16_to_f32(bias[c]));
+    out[o] = static_cast<uint16_t>(pack_bf16x2(gelu_tanh_f32(t), 0.0f) & 0xffffu);
   }
 }
 
@@ -215,7 +140,7 @@ extern "C" int hipo_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x,
     const int64_t c_tiles = (c + kTileC - 1) / kTileC;
     const int64_t hw_tiles = (hw + kTileHw - 1) / kTileHw;
     const int64_t ntiles = n * c_tiles * hw_tiles;
-    HIPO_REQUIRE(ntiles < (int64_t{1} << 31) - (int64_t{1} << 20),
+    HIPO_REQUIRE(ntiles < (int64_t{1} << 31) - kWavesPerBlock,
                  "bias_gelu: %lld tiles exceed the 32-bit tile index",
                  (long long)ntiles);
     TileGeom g;
@@ -224,12 +149,7 @@ extern "C" int hipo_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x,
     g.c_tiles = static_cast<int>(c_tiles);
     g.hw_tiles = static_cast<int>(hw_tiles);
     g.ntiles = static_cast<int>(ntiles);
-    const DeviceInfo* dev = device_info();
-    HIPO_REQUIRE(dev != nullptr, "bias_gelu: no current HIP device");
-    // One 1024-thread workgroup per CU (the table takes 128 KiB of LDS).
-    int64_t blocks = dev->cu_count;
-    const int64_t need = (ntiles + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (blocks > need) blocks = need;
+    const int64_t blocks = (ntiles + kWavesPerBlock - 1) / kWavesPerBlock;
     bias_gelu_nchw_to_nhwc_tiles<<<dim3(static_cast<unsigned>(blocks)),
                                    dim3(kBlockThreads), 0, stream>>>(x, bias, out, g);
   } else {
