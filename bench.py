@@ -216,6 +216,7 @@ def per_config(want_cpu, steady_steps=64):
                  "bytes": r.get("bytes"),
                  "steady_us": ss["device_us_per_step"], "steady_gbps": ss["achieved"],
                  "steady_sol_frac": round(ss["achieved"] / PEAK_GBPS, 4),
+                 "traffic": pmc_traffic(rid),
                  "us": r.get("oracle_us"), "median_us": r.get("oracle_median_us"),
                  "graph_us": r.get("oracle_graph_us"),
                  "gbps": r.get("gbps"), "sol_frac": r.get("sol_frac")}
