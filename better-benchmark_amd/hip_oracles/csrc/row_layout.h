@@ -14,11 +14,15 @@
 // bounds and needs no branch, which would make the compiler wait on each
 // load separately) and are zeroed.
 //
-// Per-wave footprint: the host picks W so that a wave holds about 4 KiB of
-// each streamed tensor (measured on MI355X for [16384, 4096]: 2 waves x 4
-// groups per lane, 2 rows per workgroup, non-temporal accesses reach 76 %
-// of 8 TB/s for RMSNorm and LayerNorm; one wave per row with 8 groups per
-// lane and cached accesses, 59-64 %).
+// Shape: the host picks W so that a wave holds about 2 KiB of each streamed
+// tensor (2 groups per lane) and packs rows so a workgroup has 8 waves.
+// Measured on MI355X, same process, interleaved: RMSNorm / LayerNorm
+// [16384, 4096] at 4 waves x 2 groups, 2 rows per workgroup: 74.6 / 75.0 %
+// of 8 TB/s, against 73.0 / 73.0 % at 2 waves x 4 groups (2 rows), 67-72 %
+// at 8 waves x 1 group, 71 % at 1 wave x 8 groups; softmax [384*1024, 1024]
+// at 1 wave x 2 groups, 8 rows per workgroup: 77.3 %, against 74.7 % at 4
+// rows and 68-70 % at 2 waves x 1 group.  One wave per row with 8 groups
+// per lane and cached accesses (the first version): 59-64 %.
 #pragma once
 
 #include <algorithm>
@@ -108,15 +112,16 @@ struct RowPlan {
 };
 
 inline bool row_plan(int64_t cols, RowPlan& plan) {
-  // About 4 groups (4 KiB) per lane-wave of each streamed tensor.
-  const int64_t per_wave = 4 * kRowSweep;
+  // About 2 groups (2 KiB) per wave of each streamed tensor, 8 waves per
+  // workgroup.
+  const int64_t per_wave = 2 * kRowSweep;
   const int64_t w = std::min<int64_t>(kRowMaxWaves, (cols + per_wave - 1) / per_wave);
   plan.waves_per_row = static_cast<int>(std::max<int64_t>(1, w));
   const int64_t sweep = int64_t{plan.waves_per_row} * kRowSweep;
   const int64_t u = (cols + sweep - 1) / sweep;
   if (u > 8) return false;
   plan.groups = u <= 1 ? 1 : u <= 2 ? 2 : u <= 4 ? 4 : 8;
-  plan.rows_per_block = std::max(1, 4 / plan.waves_per_row);
+  plan.rows_per_block = std::max(1, kRowMaxWaves / plan.waves_per_row);
   return true;
 }
 
