@@ -2,9 +2,10 @@
 MI355X oracle for amax_sum_scaled_masked_softmax:
 softmax(scores * 0.125 + mask, -1), bf16 in/out, fp32 max and sum.
 
-Kernel: hipo_scaled_masked_softmax_bf16 -- one wave64 per row with the row
-in registers (two 16-byte loads per lane for K = 1024), DPP max and sum,
-the [Q, K] mask row re-read from cache for every batch entry.  Algorithmic
+Kernel: hipo_scaled_masked_softmax_bf16 -- the row in registers (one wave
+per row at K = 1024, two non-temporal 16-byte loads per lane, 8 rows per
+workgroup), DPP max and sum, the [Q, K] mask row re-read from cache for
+every batch entry.  Algorithmic
 bytes: 2 B Q K (read) + 2 Q K (mask) + 2 B Q K (write).
 Replaces the Triton body of the reference's
 repros/canonical/amax_sum_20ccc18dda60/oracle.py:63.
@@ -19,7 +20,7 @@ from oracle_harness import oracle_impl  # noqa: E402
 SCALE = 0.125  # the graph constant of repro.py
 
 
-@oracle_impl(hardware="MI355X", point="dec743da", description="masked softmax, wave per row")
+@oracle_impl(hardware="MI355X", point="dec743da", description="masked softmax, rows in registers")
 @oracle_impl(hardware="MI355X", description="masked softmax, shape-general")
 def oracle_forward(inputs):
     x, mask = inputs

@@ -1,9 +1,9 @@
 """
 MI355X oracle for mean_lastdim_f32: x.mean(dim=-1) on fp32 [R, C].
 
-Kernel: hipo_row_mean_f32 (libhip_oracles.so) -- one wave64 per row,
-16-byte lane-interleaved loads (1 KiB per load instruction), fp32
-accumulation, DPP wave reduction.  Algorithmic bytes: 4 R C + 4 R.
+Kernel: hipo_row_mean_f32 (libhip_oracles.so) -- up to 8 waves per row,
+non-temporal 16-byte lane-interleaved loads (1 KiB per load instruction),
+fp32 accumulation, DPP wave reduction, fixed-order LDS combine.  Algorithmic bytes: 4 R C + 4 R.
 Replaces the Triton body of the reference's
 repros/canonical/mean_c9e1a8113328/oracle.py:95 (row mode, :45).
 """
@@ -15,7 +15,7 @@ import hip_oracles  # noqa: E402
 from oracle_harness import oracle_impl  # noqa: E402
 
 
-@oracle_impl(hardware="MI355X", point="a45be573", description="row mean, wave per row")
+@oracle_impl(hardware="MI355X", point="a45be573", description="row mean, waves per row")
 @oracle_impl(hardware="MI355X", description="row mean, shape-general")
 def oracle_forward(inputs):
     (x,) = inputs

@@ -1,8 +1,9 @@
 """
 MI355X oracle for mean_rmsnorm: y = x * rsqrt(mean(x^2) + eps) * gamma, rstd.
 
-Kernel: hipo_rmsnorm_bf16 -- one wave64 per row with the row in registers,
-fp32 sum of squares reduced with DPP, one rounding to bf16.  Algorithmic
+Kernel: hipo_rmsnorm_bf16 -- the row in registers (4 waves per row at
+C = 4096), fp32 sum of squares reduced with DPP and a fixed-order LDS
+combine, one rounding to bf16.  Algorithmic
 bytes: 4 R C + 2 C + 4 R.
 Replaces the Triton body of the reference's
 repros/canonical/mean_4462ce967d63/oracle.py:65.
@@ -17,7 +18,7 @@ from oracle_harness import oracle_impl  # noqa: E402
 EPS = 1e-05  # the graph constant of repro.py
 
 
-@oracle_impl(hardware="MI355X", point="0c98d8d1", description="RMSNorm, wave per row")
+@oracle_impl(hardware="MI355X", point="0c98d8d1", description="RMSNorm, rows in registers")
 @oracle_impl(hardware="MI355X", description="RMSNorm, shape-general")
 def oracle_forward(inputs):
     x, gamma = inputs

@@ -2,10 +2,10 @@
 MI355X oracle for var_mean_residual_layernorm:
 h = x + residual; y = LayerNorm(h) * gamma + beta; mean, rstd (fp32).
 
-Kernel: hipo_residual_layernorm_bf16 -- one wave64 per row with the row in
-registers between the statistics and the normalisation (x and residual are
-read once), two-pass fp32 statistics over the bf16-rounded h, DPP
-reductions.  Algorithmic bytes: 8 R C + 4 C + 8 R.
+Kernel: hipo_residual_layernorm_bf16 -- the row in registers between the
+statistics and the normalisation (x and residual are read once; 4 waves per
+row at C = 4096), exact two-pass fp32 statistics of each wave's values of
+the bf16-rounded h, merged across waves with Chan's formula.  Algorithmic bytes: 8 R C + 4 C + 8 R.
 Replaces the Triton body of the reference's
 repros/canonical/var_mean_80e7ff4dee7f/oracle.py:122 (without its
 anchor-clamp of the output).
@@ -20,7 +20,7 @@ from oracle_harness import oracle_impl  # noqa: E402
 EPS = 1e-05  # the graph constant of repro.py
 
 
-@oracle_impl(hardware="MI355X", point="bd27ce78", description="residual LN, wave per row")
+@oracle_impl(hardware="MI355X", point="bd27ce78", description="residual LN, rows in registers")
 @oracle_impl(hardware="MI355X", description="residual LN, shape-general")
 def oracle_forward(inputs):
     x, residual, gamma, beta = inputs

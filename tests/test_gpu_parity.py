@@ -435,3 +435,34 @@ def test_wrappers_reject_bad_operands(rocm_device):
         hip_oracles.batchnorm_train(x, ones, ones, ones.clone(), ones.clone(), momentum=0.1,
                                     eps=1e-5, workspace=torch.empty(1, dtype=torch.uint8,
                                                                     device=rocm_device))
+
+
+def test_bench_parallel_oracles_end_to_end(rocm_device, tmp_path):
+    """The parallel runner on the GPU: two canonical dirs, every shapes.json
+    point, one worker pinned with HIP_VISIBLE_DEVICES; the timings file has
+    one priced entry per dir with points_by_shape keyed by shape hash."""
+    import json
+    import subprocess
+    import sys
+    from conftest import PKG
+    out = tmp_path / "oracle_timings.json"
+    dirs = [str(CANONICAL / "mean_lastdim_f32"), str(CANONICAL / "mean_rmsnorm")]
+    print("[bench_parallel] running 6 points", flush=True)
+    proc = subprocess.run([sys.executable, "-u", "-m", "bench_parallel", *dirs, "--oracles",
+                           "--output", str(out), "--n-warmup", "2", "--n-rep", "5",
+                           "--task-timeout", "90"],
+                          cwd=str(PKG), capture_output=True, text=True, timeout=110)
+    print(proc.stdout[-3000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-2000:]
+    timed = json.loads(out.read_text())
+    assert "__failures__" not in timed
+    for name, baseline, ragged in (("mean_lastdim_f32", "a45be573", {"1ca01377", "12f6573e"}),
+                                   ("mean_rmsnorm", "0c98d8d1", {"984fcc7b", "5f1f5109"})):
+        entry = timed[name]
+        assert set(entry["points_by_shape"]) == {baseline} | ragged
+        assert entry["n_points"] == 3
+        for shape_hash, point in entry["points_by_shape"].items():
+            assert point["status"] == "ORACLE_ONLY" and point["oracle_us"] > 0
+            # the BASELINE point has a shape-specific MI355X registration; the
+            # ragged ones dispatch to the shape-general one
+            assert point["fallback"] is (shape_hash != baseline)
