@@ -450,3 +450,97 @@ def test_with_gpu_lock_cli_runs_the_command_pinned(tmp_path):
                         sys.executable, "-c",
                         f"import os; open({str(out)!r}, 'w').write(os.environ['HIP_VISIBLE_DEVICES'])"])
     assert rc == 0 and out.read_text() == "2"
+
+
+# ---------------------------------------------------------------------------
+# model_graph_accounting roll-up (reference tests/test_bench_accounting.py:1283-1418)
+# ---------------------------------------------------------------------------
+
+import model_graph_accounting as mga  # noqa: E402
+
+
+def _occ(pattern_hash, shape_hash, n_ops=1):
+    return mga.PartitionOccurrence(
+        graph_name="full_graph_000.py", pattern_hash=pattern_hash, shape_hash=shape_hash,
+        n_ops=n_ops, op_counts={"aten.add.Tensor": 1}, origin_ops=["aten.add.Tensor"],
+        input_shapes=["[4]:f32"], max_output_shape=[4], has_reduction=False)
+
+
+def _model(occs):
+    ga = mga.GraphAccounting(graph_path="full_graph_000.py", graph_name="full_graph_000.py")
+    ga.occurrences = list(occs)
+    acc = mga.ModelAccounting(model_name="TinyModel", model_dir="/tmp/TinyModel")
+    acc.graphs = [ga]
+    return acc
+
+
+def test_rollup_classifies_matched_fallback_and_unpriced():
+    timing = {"oracle_us": 10.0, "compile_us": 9.0,
+              "points_by_shape": {"shapeA": {"oracle_us": 5.0, "compile_us": 4.0}}}
+    roll = mga._rollup_occurrence_timings(timing, [_occ("p", "shapeA"), _occ("p", "shapeB")])
+    assert (roll["matched_occ"], roll["fallback_occ"], roll["unpriced_occ"], roll["total_occ"]) \
+        == (1, 1, 0, 2)
+    assert roll["mode"] == "partial" and roll["oracle_us_total"] == 15.0
+    assert roll["compile_us_total"] == 13.0
+    roll = mga._rollup_occurrence_timings(None, [_occ("p", "a"), _occ("p", "b")])
+    assert roll["unpriced_occ"] == 2 and roll["mode"] == "untimed"
+    assert roll["oracle_us_total"] is None
+    # timed dir without a representative: a missing shape is unpriced, not 0
+    roll = mga._rollup_occurrence_timings(
+        {"points_by_shape": {"shapeA": {"oracle_us": 5.0}}}, [_occ("p", "shapeA"), _occ("p", "x")])
+    assert (roll["matched_occ"], roll["fallback_occ"], roll["unpriced_occ"]) == (1, 0, 1)
+    assert roll["oracle_us_total"] == 5.0
+    # legacy timings (no points_by_shape): every occurrence at the dir number
+    roll = mga._rollup_occurrence_timings({"oracle_us": 2.5}, [_occ("p", "a")] * 4)
+    assert roll["mode"] == "legacy" and roll["oracle_us_total"] == 10.0
+    assert roll["fallback_occ"] == 4
+
+
+def test_model_report_gates_the_projection():
+    timings = {"pointwise_priced": {"oracle_us": 7.0, "compile_us": 6.0,
+                                    "points_by_shape": {"shapeA": {"oracle_us": 7.0,
+                                                                   "compile_us": 6.0}}}}
+    h2r = {"priced": "pointwise_priced", "untimed": "pointwise_untimed"}
+    rep = mga.build_model_report(_model([_occ("priced", "shapeA"), _occ("priced", "shapeA"),
+                                         _occ("untimed", "shapeC")]), h2r, timings, {})
+    assert rep["projection_complete"] is False and rep["fusible_oracle_us_total"] is None
+    assert rep["fusible_compile_us_total"] is None
+    assert rep["fusible_oracle_us_total_is_lower_bound"] is True
+    assert rep["fusible_oracle_us_total_partial"] == 14.0
+    assert (rep["unpriced_occurrences"], rep["priced_occurrences"], rep["total_occurrences"]) \
+        == (1, 2, 3)
+    assert [k["pattern_hash"] for k in rep["unpriced_kernels"]] == ["untimed"]
+    text = mga.format_text_report(rep)
+    assert "INCOMPLETE" in text and "UNAVAILABLE" in text
+    rep = mga.build_model_report(_model([_occ("priced", "shapeA")] * 2), h2r, timings, {})
+    assert rep["projection_complete"] is True and rep["fusible_oracle_us_total"] == 14.0
+    assert rep["fusible_oracle_us_total_is_lower_bound"] is False
+    assert rep["unpriced_kernels"] == []
+
+
+def test_occurrences_from_the_canonical_shapes(tmp_path):
+    models = mga.collect_model_occurrences(CANONICAL)
+    assert "baseline/config2_bias_gelu_nhwc" in models
+    acc = models["baseline/config4a_residual_layernorm"]
+    assert len(acc.all_occurrences) == 1
+    occ = acc.all_occurrences[0]
+    assert occ.pattern_hash == "var_mean_residual_layernorm" and occ.has_reduction
+    h2r = mga.build_hash_to_repro(CANONICAL)
+    assert h2r["var_mean_residual_layernorm"] == "var_mean_residual_layernorm"
+    # a timings file shaped like bench_parallel's output prices it at its own shape
+    timings = bp._aggregate_oracle_timings({
+        bp._make_shape_task_key(str(CANONICAL / "var_mean_residual_layernorm"),
+                                f"config4a_residual_layernorm_{occ.shape_hash}"):
+            {f"config4a_residual_layernorm_{occ.shape_hash}":
+                 {"status": "ORACLE_ONLY", "oracle_us": 89.4}}})
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps(timings))
+    rep = mga.build_model_report(acc, h2r, mga.load_timings(path))
+    assert rep["projection_complete"] and rep["fusible_oracle_us_total"] == 89.4
+    assert rep["matched_occurrences"] == 1
+    # CLI over every model: the other five models have no timing -> INCOMPLETE
+    out = tmp_path / "r.json"
+    assert mga.main(["--all", "--json", "--timings", str(path), "--output", str(out)]) == 0
+    reports = {r["model_name"]: r for r in json.loads(out.read_text())}
+    assert reports["baseline/config4a_residual_layernorm"]["projection_complete"] is True
+    assert reports["baseline/config1_row_mean"]["projection_complete"] is False

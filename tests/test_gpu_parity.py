@@ -466,3 +466,15 @@ def test_bench_parallel_oracles_end_to_end(rocm_device, tmp_path):
             # the BASELINE point has a shape-specific MI355X registration; the
             # ragged ones dispatch to the shape-general one
             assert point["fallback"] is (shape_hash != baseline)
+    # the model roll-up prices each BASELINE model at its own measured point
+    import model_graph_accounting as mga
+    report_path = tmp_path / "models.json"
+    assert mga.main(["--all", "--json", "--timings", str(out), "--output",
+                     str(report_path)]) == 0
+    reports = {r["model_name"]: r for r in json.loads(report_path.read_text())}
+    for model, name, baseline in (("baseline/config1_row_mean", "mean_lastdim_f32", "a45be573"),
+                                  ("baseline/config4b_rmsnorm", "mean_rmsnorm", "0c98d8d1")):
+        rep = reports[model]
+        assert rep["projection_complete"] and rep["matched_occurrences"] == 1
+        assert rep["fusible_oracle_us_total"] == timed[name]["points_by_shape"][baseline]["oracle_us"]
+    assert reports["baseline/config5_batchnorm_train"]["projection_complete"] is False
