@@ -42,6 +42,15 @@ _SIGNATURES = {
         [_c_ptr] * 8 + [_c_i64, _c_i64, _c_f32, _c_ptr]),
     "hipo_rmsnorm_bf16": (
         ctypes.c_int, [_c_ptr] * 4 + [_c_i64, _c_i64, _c_f32, _c_ptr]),
+    "hipo_rmsnorm_ex_bf16": (
+        ctypes.c_int, [_c_ptr] * 5 + [_c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int, _c_ptr]),
+    "hipo_scaled_bias_softmax_bf16": (
+        ctypes.c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32,
+         _c_ptr]),
+    "hipo_spatial_mean_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
+    "hipo_spatial_mean_nhwc_bf16": (
+        ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, ctypes.c_size_t, _c_ptr]),
     "hipo_batchnorm_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
     "hipo_batchnorm_train_fwd_f32": (
         ctypes.c_int,
@@ -167,18 +176,23 @@ def scaled_masked_softmax(x: torch.Tensor, mask: torch.Tensor, scale: float) -> 
     b, q, k = x.shape
     _require(mask.dim() == 2 and tuple(mask.shape) == (q, k) and mask.stride(1) == 1,
              "masked_softmax: mask must be [Q, K] with unit inner stride")
+    if q > 1 and mask.stride(0) < k:
+        # Rows that overlap (a mask broadcast over Q): the kernel addresses
+        # row q at q * row_stride and needs row_stride >= K.
+        mask = mask.contiguous()
     mstride = mask.stride(0) if q > 1 else k
     out = torch.empty_like(x)
     with torch.cuda.device(dev):
         _check(lib.hipo_scaled_masked_softmax_bf16(_ptr(x), _ptr(mask), _ptr(out),
-                                                   b, q, k, max(mstride, k),
+                                                   b, q, k, mstride,
                                                    float(scale), _stream(dev)),
                "scaled_masked_softmax")
     return out
 
 
-def residual_layernorm(x, residual, gamma, beta, eps: float):
-    """(h, y, mean, rstd) of LayerNorm(x + residual) over the last dim."""
+def residual_layernorm(x, residual, gamma, beta, eps: float, *, outputs: str = "all"):
+    """(h, y, mean, rstd) of LayerNorm(x + residual) over the last dim;
+    outputs="y" returns y alone and writes nothing else."""
     lib = load_library()
     dev = _require_rocm(x, residual, gamma, beta)
     for t in (x, residual, gamma, beta):
@@ -187,16 +201,21 @@ def residual_layernorm(x, residual, gamma, beta, eps: float):
     _require(x.dim() == 2 and residual.shape == x.shape, "residual_layernorm: x, residual [R, C]")
     rows, cols = x.shape
     _require(gamma.shape == (cols,) and beta.shape == (cols,), "residual_layernorm: gamma/beta [C]")
-    h = torch.empty_like(x)
+    _require(outputs in ("all", "y"), "residual_layernorm: outputs must be 'all' or 'y'")
     y = torch.empty_like(x)
-    mean = torch.empty(rows, dtype=torch.float32, device=dev)
-    rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+    if outputs == "all":
+        h = torch.empty_like(x)
+        mean = torch.empty(rows, dtype=torch.float32, device=dev)
+        rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+        ptrs = (_ptr(h), _ptr(mean), _ptr(rstd))
+    else:
+        ptrs = (None, None, None)
     with torch.cuda.device(dev):
         _check(lib.hipo_residual_layernorm_bf16(
-            _ptr(x), _ptr(residual), _ptr(gamma), _ptr(beta), _ptr(h), _ptr(y),
-            _ptr(mean), _ptr(rstd), rows, cols, float(eps), _stream(dev)),
+            _ptr(x), _ptr(residual), _ptr(gamma), _ptr(beta), ptrs[0], _ptr(y),
+            ptrs[1], ptrs[2], rows, cols, float(eps), _stream(dev)),
             "residual_layernorm")
-    return h, y, mean, rstd
+    return (h, y, mean, rstd) if outputs == "all" else y
 
 
 def rmsnorm(x, gamma, eps: float):
@@ -216,6 +235,79 @@ def rmsnorm(x, gamma, eps: float):
                                      rows, cols, float(eps), _stream(dev)),
                "rmsnorm")
     return y, rstd
+
+
+def rmsnorm_ex(x, gamma, eps: float, *, residual=None, scale: float = 1.0, mode: int = 0,
+               want_rstd: bool = False):
+    """RMSNorm over the last dim with an optional residual (h = bf16(x + r)),
+    an output scale and the eager rounding order: mode 0 = torch rms_norm
+    (one rounding), mode 1 = HF T5 (bf16(h*rstd), then *gamma, then *scale,
+    each rounded).  Returns y, or (y, rstd) with want_rstd."""
+    lib = load_library()
+    ops = (x, gamma) if residual is None else (x, gamma, residual)
+    dev = _require_rocm(*ops)
+    for t in ops:
+        _require(t.dtype == torch.bfloat16 and t.is_contiguous(),
+                 "rmsnorm_ex: contiguous bf16 operands required")
+    _require(x.dim() == 2, "rmsnorm_ex: x must be [R, C]")
+    rows, cols = x.shape
+    _require(gamma.shape == (cols,), "rmsnorm_ex: gamma must be [C]")
+    _require(residual is None or residual.shape == x.shape, "rmsnorm_ex: residual [R, C]")
+    _require(mode in (0, 1), "rmsnorm_ex: mode must be 0 or 1")
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, dtype=torch.float32, device=dev) if want_rstd else None
+    with torch.cuda.device(dev):
+        _check(lib.hipo_rmsnorm_ex_bf16(
+            _ptr(x), None if residual is None else _ptr(residual), _ptr(gamma), _ptr(y),
+            None if rstd is None else _ptr(rstd), rows, cols, float(eps), float(scale),
+            int(mode), _stream(dev)), "rmsnorm_ex")
+    return (y, rstd) if want_rstd else y
+
+
+def scaled_bias_softmax(x, bias, scale: float, heads: int):
+    """softmax(x * scale + bias, -1) for bf16 x [B, Q, K] and a bias
+    [B / heads, Q, K] (any layout with unit inner stride and 8-aligned row and
+    batch strides) shared by `heads` consecutive batch entries."""
+    lib = load_library()
+    dev = _require_rocm(x, bias)
+    _require(x.dtype == torch.bfloat16 and bias.dtype == torch.bfloat16,
+             "bias_softmax: bf16 operands required")
+    _require(x.dim() == 3 and x.is_contiguous(), "bias_softmax: x must be contiguous [B,Q,K]")
+    b, q, k = x.shape
+    _require(heads >= 1 and b % heads == 0, "bias_softmax: heads must divide the batch")
+    _require(bias.dim() == 3 and tuple(bias.shape) == (b // heads, q, k) and bias.stride(2) == 1,
+             "bias_softmax: bias must be [B / heads, Q, K] with unit inner stride")
+    if q > 1 and bias.stride(1) < k:
+        bias = bias.contiguous()  # rows that overlap: the kernel needs row stride >= K
+    rs = bias.stride(1) if q > 1 else k
+    bs = bias.stride(0) if b // heads > 1 else 0
+    out = torch.empty_like(x)
+    with torch.cuda.device(dev):
+        _check(lib.hipo_scaled_bias_softmax_bf16(_ptr(x), _ptr(bias), _ptr(out), b, q, k,
+                                                 rs, bs, heads, float(scale),
+                                                 _stream(dev)),
+               "scaled_bias_softmax")
+    return out
+
+
+def spatial_mean_nhwc(x, keepdim: bool = True):
+    """Mean over H, W of a channels-last bf16 [N, C, H, W] tensor ->
+    [N, C, 1, 1] (keepdim) or [N, C], contiguous bf16."""
+    lib = load_library()
+    dev = _require_rocm(x)
+    _require(x.dtype == torch.bfloat16 and x.dim() == 4, "spatial_mean: bf16 NCHW tensor")
+    n, c, h, w = x.shape
+    _require(x.is_contiguous(memory_format=torch.channels_last),
+             "spatial_mean: x must be stored channels-last")
+    out = torch.empty((n, c, 1, 1) if keepdim else (n, c), dtype=torch.bfloat16, device=dev)
+    need = int(lib.hipo_spatial_mean_workspace_bytes(n, h * w, c))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev) if need else None
+    with torch.cuda.device(dev):
+        _check(lib.hipo_spatial_mean_nhwc_bf16(_ptr(x), _ptr(out), n, h * w, c,
+                                               None if ws is None else _ptr(ws), need,
+                                               _stream(dev)),
+               "spatial_mean_nhwc")
+    return out
 
 
 def batchnorm_workspace_bytes(n: int, c: int, hw: int) -> int:
@@ -290,6 +382,7 @@ def batchnorm_error_flag(dev: torch.device | None = None) -> int:
 __all__ = [
     "HipOraclesUnavailable", "LIB_PATH", "load_library", "header_symbols",
     "row_mean", "bias_gelu_nchw_to_nhwc", "scaled_masked_softmax",
-    "residual_layernorm", "rmsnorm", "batchnorm_workspace_bytes", "batchnorm_train",
+    "residual_layernorm", "rmsnorm", "rmsnorm_ex", "scaled_bias_softmax", "spatial_mean_nhwc",
+    "batchnorm_workspace_bytes", "batchnorm_train",
     "batchnorm_cached_workspace", "batchnorm_error_flag",
 ]

@@ -34,6 +34,7 @@ SOURCES = [
     "row_norms.hip",
     "batchnorm.hip",
     "batchnorm_fused.hip",
+    "spatial_mean.hip",
 ]
 
 # Packed-FP32 VALU forms are disabled for all device code (the compiler

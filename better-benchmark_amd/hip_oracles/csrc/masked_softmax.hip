@@ -24,12 +24,14 @@ template <int U, bool ROUND_SCALE>
 __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
     uint16_t* __restrict__ out, int64_t rows, int64_t Q, int64_t K,
-    int64_t mask_stride, float scale, int waves_per_row, int rows_per_block) {
+    int64_t mask_stride, int64_t mask_batch_stride, int64_t heads, float scale,
+    int waves_per_row, int rows_per_block) {
   __shared__ float pmax[kRowMaxWaves], psum[kRowMaxWaves];
   const RowPlace p = row_place(waves_per_row, rows_per_block, rows);
-  const int64_t q = p.row % Q;
+  const int64_t b = p.row / Q;
+  const int64_t q = p.row - b * Q;
   const uint16_t* xr = x + p.row * K;
-  const uint16_t* mr = mask + q * mask_stride;
+  const uint16_t* mr = mask + (b / heads) * mask_batch_stride + q * mask_stride;
   uint16_t* orow = out + p.row * K;
 
   u32x4_t xv[U], mv[U];
@@ -109,14 +111,16 @@ __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
 __global__ __launch_bounds__(256) void masked_softmax_rows_scalar(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
     uint16_t* __restrict__ out, int64_t rows, int64_t Q, int64_t K,
-    int64_t mask_stride, float scale, int round_scale) {
+    int64_t mask_stride, int64_t mask_batch_stride, int64_t heads, float scale,
+    int round_scale) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row =
       static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const int64_t q = row % Q;
+  const int64_t b = row / Q;
+  const int64_t q = row - b * Q;
   const uint16_t* xr = x + row * K;
-  const uint16_t* mr = mask + q * mask_stride;
+  const uint16_t* mr = mask + (b / heads) * mask_batch_stride + q * mask_stride;
   uint16_t* orow = out + row * K;
   auto score = [&](int64_t j) {
     float a = bf16_to_f32(xr[j]) * scale;
@@ -147,15 +151,60 @@ bool is_power_of_two(float v) {
 template <int U>
 void launch_vec(bool round_scale, dim3 grid, const RowPlan& plan, hipStream_t stream,
                 const uint16_t* x, const uint16_t* mask, uint16_t* out,
-                int64_t rows, int64_t Q, int64_t K, int64_t ms, float scale) {
+                int64_t rows, int64_t Q, int64_t K, int64_t ms, int64_t mbs,
+                int64_t heads, float scale) {
   const dim3 block(plan.threads());
   if (round_scale) {
     masked_softmax_rows<U, true><<<grid, block, 0, stream>>>(
-        x, mask, out, rows, Q, K, ms, scale, plan.waves_per_row, plan.rows_per_block);
+        x, mask, out, rows, Q, K, ms, mbs, heads, scale, plan.waves_per_row,
+        plan.rows_per_block);
   } else {
     masked_softmax_rows<U, false><<<grid, block, 0, stream>>>(
-        x, mask, out, rows, Q, K, ms, scale, plan.waves_per_row, plan.rows_per_block);
+        x, mask, out, rows, Q, K, ms, mbs, heads, scale, plan.waves_per_row,
+        plan.rows_per_block);
   }
+}
+
+}  // namespace
+}  // namespace hipo
+
+namespace hipo {
+namespace {
+
+int softmax_impl(const uint16_t* x, const uint16_t* mask, uint16_t* out, int64_t batch,
+                 int64_t q, int64_t k, int64_t mask_row_stride, int64_t mask_batch_stride,
+                 int64_t heads, float scale, hipStream_t stream, const char* what) {
+  clear_error();
+  HIPO_REQUIRE(batch >= 0 && q >= 0 && k >= 0, "%s: negative size", what);
+  if (batch == 0 || q == 0 || k == 0) return 0;
+  HIPO_REQUIRE(x && mask && out, "%s: null pointer", what);
+  HIPO_REQUIRE(mask_row_stride >= k, "%s: mask_row_stride < k", what);
+  HIPO_REQUIRE(heads >= 1 && batch % heads == 0, "%s: heads must divide batch", what);
+  HIPO_REQUIRE(mask_batch_stride >= 0, "%s: negative mask_batch_stride", what);
+  const int64_t rows = batch * q;
+  const bool round_scale = !is_power_of_two(scale);
+  RowPlan plan;
+  const bool vec = (k % 8 == 0) && (mask_row_stride % 8 == 0) &&
+                   (mask_batch_stride % 8 == 0) && row_plan(k, plan) && aligned16(x) &&
+                   aligned16(mask) && aligned16(out);
+  if (vec) {
+    const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);
+    const dim3 grid(static_cast<unsigned>(blocks));
+    switch (plan.groups) {
+      case 1: launch_vec<1>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale); break;
+      case 2: launch_vec<2>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale); break;
+      case 4: launch_vec<4>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale); break;
+      default: launch_vec<8>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale); break;
+    }
+  } else {
+    const int64_t blocks = (rows + 3) / 4;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);
+    masked_softmax_rows_scalar<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
+        x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale,
+        round_scale ? 1 : 0);
+  }
+  return check_launch(what);
 }
 
 }  // namespace
@@ -168,32 +217,15 @@ extern "C" int hipo_scaled_masked_softmax_bf16(const uint16_t* x,
                                                int64_t mask_row_stride,
                                                float scale,
                                                hipStream_t stream) {
-  using namespace hipo;
-  clear_error();
-  HIPO_REQUIRE(batch >= 0 && q >= 0 && k >= 0, "masked_softmax: negative size");
-  if (batch == 0 || q == 0 || k == 0) return 0;
-  HIPO_REQUIRE(x && mask && out, "masked_softmax: null pointer");
-  HIPO_REQUIRE(mask_row_stride >= k, "masked_softmax: mask_row_stride < k");
-  const int64_t rows = batch * q;
-  const bool round_scale = !is_power_of_two(scale);
-  RowPlan plan;
-  const bool vec = (k % 8 == 0) && (mask_row_stride % 8 == 0) && row_plan(k, plan) &&
-                   aligned16(x) && aligned16(mask) && aligned16(out);
-  if (vec) {
-    const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
-    HIPO_REQUIRE(blocks <= 0x7fffffff, "masked_softmax: too many rows");
-    const dim3 grid(static_cast<unsigned>(blocks));
-    switch (plan.groups) {
-      case 1: launch_vec<1>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-      case 2: launch_vec<2>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-      case 4: launch_vec<4>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-      default: launch_vec<8>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, scale); break;
-    }
-  } else {
-    const int64_t blocks = (rows + 3) / 4;
-    HIPO_REQUIRE(blocks <= 0x7fffffff, "masked_softmax: too many rows");
-    masked_softmax_rows_scalar<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
-        x, mask, out, rows, q, k, mask_row_stride, scale, round_scale ? 1 : 0);
-  }
-  return check_launch("scaled_masked_softmax_bf16");
+  return hipo::softmax_impl(x, mask, out, batch, q, k, mask_row_stride, 0, 1, scale, stream,
+                            "scaled_masked_softmax_bf16");
+}
+
+extern "C" int hipo_scaled_bias_softmax_bf16(const uint16_t* x, const uint16_t* bias,
+                                             uint16_t* out, int64_t batch, int64_t q,
+                                             int64_t k, int64_t bias_row_stride,
+                                             int64_t bias_batch_stride, int64_t heads,
+                                             float scale, hipStream_t stream) {
+  return hipo::softmax_impl(x, bias, out, batch, q, k, bias_row_stride, bias_batch_stride,
+                            heads, scale, stream, "scaled_bias_softmax_bf16");
 }

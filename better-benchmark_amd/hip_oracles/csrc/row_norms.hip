@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kRowMaxThreads) void residual_layernorm_rows(
       sum += bf16lo(hv[u][d]) + bf16hi(hv[u][d]);
     }
     const int64_t col = row_group_col(u, waves_per_row, p);
-    if (p.valid && col < cols) row_store_stream(h + base, col, hv[u]);
+    if (h != nullptr && p.valid && col < cols) row_store_stream(h + base, col, hv[u]);
   }
   const float n = static_cast<float>(row_wave_count(U, waves_per_row, p, cols));
   const float wmean = n > 0.f ? wave_sum(sum) / n : 0.f;
@@ -96,16 +96,21 @@ __global__ __launch_bounds__(kRowMaxThreads) void residual_layernorm_rows(
     if (p.valid && col < cols) row_store_stream(y + base, col, o);
   }
   if (p.valid && p.w == 0 && p.lane == 0) {
-    mean_out[p.row] = mean;
-    rstd_out[p.row] = rstd;
+    if (mean_out != nullptr) mean_out[p.row] = mean;
+    if (rstd_out != nullptr) rstd_out[p.row] = rstd;
   }
 }
 
-template <int U>
+// MODE 0 (torch rms_norm): y = bf16(h * rstd * gamma * scale), one rounding.
+// MODE 1 (HF T5 op order): t = bf16(h * rstd); u = bf16(gamma * t);
+//                          y = scale == 1 ? u : bf16(u * scale).
+// With a residual, h = bf16(x + residual) (the eager bf16 add), else h = x.
+template <int U, bool RES, int MODE>
 __global__ __launch_bounds__(kRowMaxThreads) void rmsnorm_rows(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
-    uint16_t* __restrict__ y, float* __restrict__ rstd_out, int64_t rows,
-    int64_t cols, float eps, int waves_per_row, int rows_per_block) {
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ y,
+    float* __restrict__ rstd_out, int64_t rows, int64_t cols, float eps,
+    float scale, int waves_per_row, int rows_per_block) {
   __shared__ float part[kRowMaxWaves];
   const RowPlace p = row_place(waves_per_row, rows_per_block, rows);
   const int64_t base = p.row * cols;
@@ -114,6 +119,17 @@ __global__ __launch_bounds__(kRowMaxThreads) void rmsnorm_rows(
 #pragma unroll
   for (int u = 0; u < U; ++u)
     xv[u] = row_load_stream(x + base, row_group_col(u, waves_per_row, p), cols);
+  if (RES) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const u32x4_t rv =
+          row_load_stream(res + base, row_group_col(u, waves_per_row, p), cols);
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        xv[u][d] = pack_bf16x2(bf16lo(xv[u][d]) + bf16lo(rv[d]),
+                               bf16hi(xv[u][d]) + bf16hi(rv[d]));
+    }
+  }
   float sq = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -142,12 +158,25 @@ __global__ __launch_bounds__(kRowMaxThreads) void rmsnorm_rows(
     u32x4_t o;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      o[d] = pack_bf16x2((bf16lo(xv[u][d]) * rstd) * bf16lo(gv[d]),
-                         (bf16hi(xv[u][d]) * rstd) * bf16hi(gv[d]));
+      float a = bf16lo(xv[u][d]) * rstd, b = bf16hi(xv[u][d]) * rstd;
+      if (MODE == 0) {
+        a *= bf16lo(gv[d]);
+        b *= bf16hi(gv[d]);
+        if (scale != 1.0f) {
+          a *= scale;
+          b *= scale;
+        }
+        o[d] = pack_bf16x2(a, b);
+      } else {
+        const uint32_t t = pack_bf16x2(a, b);
+        uint32_t w = pack_bf16x2(bf16lo(gv[d]) * bf16lo(t), bf16hi(gv[d]) * bf16hi(t));
+        if (scale != 1.0f) w = pack_bf16x2(bf16lo(w) * scale, bf16hi(w) * scale);
+        o[d] = w;
+      }
     }
     if (p.valid && col < cols) row_store_stream(y + base, col, o);
   }
-  if (p.valid && p.w == 0 && p.lane == 0) rstd_out[p.row] = rstd;
+  if (rstd_out != nullptr && p.valid && p.w == 0 && p.lane == 0) rstd_out[p.row] = rstd;
 }
 
 // Any cols / alignment: one wave per row, scalar accesses, row re-read from
@@ -166,7 +195,7 @@ __global__ __launch_bounds__(256) void residual_layernorm_rows_scalar(
   float sum = 0.f;
   for (int64_t j = lane; j < cols; j += kWave) {
     const float hv = round_bf16(bf16_to_f32(x[base + j]) + bf16_to_f32(res[base + j]));
-    h[base + j] = static_cast<uint16_t>(pack_bf16x2(hv, 0.f) & 0xffffu);
+    if (h != nullptr) h[base + j] = static_cast<uint16_t>(pack_bf16x2(hv, 0.f) & 0xffffu);
     sum += hv;
   }
   const float mean = wave_sum(sum) / static_cast<float>(cols);
@@ -186,43 +215,55 @@ __global__ __launch_bounds__(256) void residual_layernorm_rows_scalar(
     y[base + j] = static_cast<uint16_t>(pack_bf16x2(v, 0.f) & 0xffffu);
   }
   if (lane == 0) {
-    mean_out[row] = mean;
-    rstd_out[row] = rstd;
+    if (mean_out != nullptr) mean_out[row] = mean;
+    if (rstd_out != nullptr) rstd_out[row] = rstd;
   }
 }
 
 __global__ __launch_bounds__(256) void rmsnorm_rows_scalar(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
-    uint16_t* __restrict__ y, float* __restrict__ rstd_out, int64_t rows,
-    int64_t cols, float eps) {
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ y,
+    float* __restrict__ rstd_out, int64_t rows, int64_t cols, float eps,
+    float scale, int mode) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row =
-      static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t base = row * cols;
+  auto hval = [&](int64_t j) {
+    const float a = bf16_to_f32(x[base + j]);
+    return res != nullptr ? round_bf16(a + bf16_to_f32(res[base + j])) : a;
+  };
   float sq = 0.f;
   for (int64_t j = lane; j < cols; j += kWave) {
-    const float a = bf16_to_f32(x[base + j]);
+    const float a = hval(j);
     sq = __builtin_fmaf(a, a, sq);
   }
   const float rstd =
       1.0f / __builtin_sqrtf(wave_sum(sq) / static_cast<float>(cols) + eps);
   for (int64_t j = lane; j < cols; j += kWave) {
-    const float v = (bf16_to_f32(x[base + j]) * rstd) * bf16_to_f32(gamma[j]);
+    float v = hval(j) * rstd;
+    if (mode == 0) {
+      v = v * bf16_to_f32(gamma[j]);
+      if (scale != 1.0f) v *= scale;
+    } else {
+      v = round_bf16(bf16_to_f32(gamma[j]) * round_bf16(v));
+      if (scale != 1.0f) v = v * scale;
+    }
     y[base + j] = static_cast<uint16_t>(pack_bf16x2(v, 0.f) & 0xffffu);
   }
-  if (lane == 0) rstd_out[row] = rstd;
+  if (rstd_out != nullptr && lane == 0) rstd_out[row] = rstd;
 }
 
 }  // namespace
 }  // namespace hipo
 
-#define HIPO_ROW_SWITCH(plan, KERNEL, grid, stream, ...)                            \
-  switch ((plan).groups) {                                                          \
-    case 1: KERNEL<1><<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; \
-    case 2: KERNEL<2><<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; \
-    case 4: KERNEL<4><<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; \
-    default: KERNEL<8><<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; \
+// Launch KERNEL (an expression naming U_) with U_ = plan.groups.
+#define HIPO_ROW_SWITCH(plan, KERNEL, grid, stream, ...)                          \
+  switch ((plan).groups) {                                                        \
+    case 1: { constexpr int U_ = 1; KERNEL<<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; } \
+    case 2: { constexpr int U_ = 2; KERNEL<<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; } \
+    case 4: { constexpr int U_ = 4; KERNEL<<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; } \
+    default: { constexpr int U_ = 8; KERNEL<<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; } \
   }
 
 extern "C" int hipo_residual_layernorm_bf16(
@@ -234,17 +275,17 @@ extern "C" int hipo_residual_layernorm_bf16(
   HIPO_REQUIRE(rows >= 0 && cols >= 0, "residual_layernorm: negative size");
   if (rows == 0) return 0;
   HIPO_REQUIRE(cols > 0, "residual_layernorm: cols must be > 0");
-  HIPO_REQUIRE(x && residual && gamma && beta && h && y && mean && rstd,
+  HIPO_REQUIRE(x && residual && gamma && beta && y,
                "residual_layernorm: null pointer");
   RowPlan plan;
   const bool vec = cols % 8 == 0 && row_plan(cols, plan) && aligned16(x) &&
                    aligned16(residual) && aligned16(gamma) && aligned16(beta) &&
-                   aligned16(h) && aligned16(y);
+                   (h == nullptr || aligned16(h)) && aligned16(y);
   if (vec) {
     const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "residual_layernorm: too many rows");
     const dim3 grid(static_cast<unsigned>(blocks));
-    HIPO_ROW_SWITCH(plan, residual_layernorm_rows, grid, stream, x, residual,
+    HIPO_ROW_SWITCH(plan, residual_layernorm_rows<U_>, grid, stream, x, residual,
                     gamma, beta, h, y, mean, rstd, rows, cols, eps,
                     plan.waves_per_row, plan.rows_per_block);
   } else {
@@ -256,29 +297,73 @@ extern "C" int hipo_residual_layernorm_bf16(
   return check_launch("residual_layernorm_bf16");
 }
 
+namespace hipo {
+namespace {
+
+template <bool RES, int MODE>
+void launch_rmsnorm(const RowPlan& plan, dim3 grid, hipStream_t stream,
+                    const uint16_t* x, const uint16_t* residual,
+                    const uint16_t* gamma, uint16_t* y, float* rstd,
+                    int64_t rows, int64_t cols, float eps, float scale) {
+  const dim3 block(plan.threads());
+  const int w = plan.waves_per_row, r = plan.rows_per_block;
+  switch (plan.groups) {
+    case 1: rmsnorm_rows<1, RES, MODE><<<grid, block, 0, stream>>>(x, residual, gamma, y, rstd, rows, cols, eps, scale, w, r); break;
+    case 2: rmsnorm_rows<2, RES, MODE><<<grid, block, 0, stream>>>(x, residual, gamma, y, rstd, rows, cols, eps, scale, w, r); break;
+    case 4: rmsnorm_rows<4, RES, MODE><<<grid, block, 0, stream>>>(x, residual, gamma, y, rstd, rows, cols, eps, scale, w, r); break;
+    default: rmsnorm_rows<8, RES, MODE><<<grid, block, 0, stream>>>(x, residual, gamma, y, rstd, rows, cols, eps, scale, w, r); break;
+  }
+}
+
+int rmsnorm_impl(const uint16_t* x, const uint16_t* residual, const uint16_t* gamma,
+                 uint16_t* y, float* rstd, int64_t rows, int64_t cols, float eps,
+                 float scale, int mode, bool require_rstd, hipStream_t stream,
+                 const char* what) {
+  clear_error();
+  HIPO_REQUIRE(rows >= 0 && cols >= 0, "%s: negative size", what);
+  if (rows == 0) return 0;
+  HIPO_REQUIRE(cols > 0, "%s: cols must be > 0", what);
+  HIPO_REQUIRE(x && gamma && y && (rstd || !require_rstd), "%s: null pointer", what);
+  HIPO_REQUIRE(mode == 0 || mode == 1, "%s: mode must be 0 or 1", what);
+  RowPlan plan;
+  const bool vec = cols % 8 == 0 && row_plan(cols, plan) && aligned16(x) &&
+                   aligned16(gamma) && aligned16(y) &&
+                   (residual == nullptr || aligned16(residual));
+  if (vec) {
+    const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);
+    const dim3 grid(static_cast<unsigned>(blocks));
+    if (residual != nullptr) {
+      if (mode == 0) launch_rmsnorm<true, 0>(plan, grid, stream, x, residual, gamma, y, rstd, rows, cols, eps, scale);
+      else launch_rmsnorm<true, 1>(plan, grid, stream, x, residual, gamma, y, rstd, rows, cols, eps, scale);
+    } else {
+      if (mode == 0) launch_rmsnorm<false, 0>(plan, grid, stream, x, residual, gamma, y, rstd, rows, cols, eps, scale);
+      else launch_rmsnorm<false, 1>(plan, grid, stream, x, residual, gamma, y, rstd, rows, cols, eps, scale);
+    }
+  } else {
+    const int64_t blocks = (rows + 3) / 4;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);
+    rmsnorm_rows_scalar<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
+        x, residual, gamma, y, rstd, rows, cols, eps, scale, mode);
+  }
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace hipo
+
 extern "C" int hipo_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma,
                                  uint16_t* y, float* rstd, int64_t rows,
                                  int64_t cols, float eps, hipStream_t stream) {
-  using namespace hipo;
-  clear_error();
-  HIPO_REQUIRE(rows >= 0 && cols >= 0, "rmsnorm: negative size");
-  if (rows == 0) return 0;
-  HIPO_REQUIRE(cols > 0, "rmsnorm: cols must be > 0");
-  HIPO_REQUIRE(x && gamma && y && rstd, "rmsnorm: null pointer");
-  RowPlan plan;
-  const bool vec = cols % 8 == 0 && row_plan(cols, plan) && aligned16(x) &&
-                   aligned16(gamma) && aligned16(y);
-  if (vec) {
-    const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
-    HIPO_REQUIRE(blocks <= 0x7fffffff, "rmsnorm: too many rows");
-    const dim3 grid(static_cast<unsigned>(blocks));
-    HIPO_ROW_SWITCH(plan, rmsnorm_rows, grid, stream, x, gamma, y, rstd, rows,
-                    cols, eps, plan.waves_per_row, plan.rows_per_block);
-  } else {
-    const int64_t blocks = (rows + 3) / 4;
-    HIPO_REQUIRE(blocks <= 0x7fffffff, "rmsnorm: too many rows");
-    rmsnorm_rows_scalar<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
-        x, gamma, y, rstd, rows, cols, eps);
-  }
-  return check_launch("rmsnorm_bf16");
+  return hipo::rmsnorm_impl(x, nullptr, gamma, y, rstd, rows, cols, eps, 1.0f, 0, true,
+                            stream, "rmsnorm_bf16");
+}
+
+extern "C" int hipo_rmsnorm_ex_bf16(const uint16_t* x, const uint16_t* residual,
+                                    const uint16_t* gamma, uint16_t* y,
+                                    float* rstd, int64_t rows, int64_t cols,
+                                    float eps, float scale, int mode,
+                                    hipStream_t stream) {
+  return hipo::rmsnorm_impl(x, residual, gamma, y, rstd, rows, cols, eps, scale, mode, false,
+                            stream, "rmsnorm_ex_bf16");
 }

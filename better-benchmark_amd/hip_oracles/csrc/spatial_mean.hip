@@ -1,0 +1,196 @@
+// Spatial mean of a channels-last bf16 tensor: the reduction over a
+// non-innermost axis.
+//   x: [N, C, H, W] bf16 stored channels-last (physical [N, P, C], P = H*W)
+//   out[n, c] = bf16(sum_p x[n, p, c] / P)          (fp32 accumulation)
+// (torch.mean(x, [2, 3], keepdim) of the reference's mean_c9e1a8113328.)
+//
+// Layout.  G = C / 8 channel groups of 16 bytes.  A workgroup of T threads
+// (T a multiple of G) reduces the positions [p0, p1) of one image: thread t
+// owns group t % G and positions p0 + t / G + k * (T / G), so each load
+// instruction of the workgroup covers T / G whole rows, T * 16 contiguous
+// bytes, and each thread keeps 4 loads in flight.  The T / G partial sums of
+// a group meet in LDS and the first G threads add them in a fixed order.
+// With one position slice per image the result is written as bf16 directly;
+// with S > 1 slices (more workgroups than images alone give) each slice
+// writes fp32 partials and a second kernel adds the S slices of a channel in
+// a fixed order.  Deterministic.
+// HBM-bound: algorithmic bytes = 2 N P C (read) + 2 N C (write).
+#include <algorithm>
+
+#include "hipo_common.h"
+
+namespace hipo {
+namespace {
+
+constexpr int kUnroll = 4;
+constexpr int kMaxThreads = 1024;
+
+__global__ __launch_bounds__(kMaxThreads) void spatial_mean_nhwc_partial(
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ out,
+    float* __restrict__ partial, int64_t P, int64_t C, int G, int slices,
+    int64_t slice_len) {
+  extern __shared__ float lds[];  // [T][8]
+  const int T = blockDim.x;
+  const int t = threadIdx.x;
+  const int g = t % G;
+  const int r = t / G;        // row offset of this thread
+  const int R = T / G;        // rows per workgroup instruction
+  const int64_t n = blockIdx.x / slices;
+  const int s = blockIdx.x - static_cast<int>(n) * slices;
+  const int64_t p0 = s * slice_len;
+  const int64_t p1 = std::min<int64_t>(P, p0 + slice_len);
+  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x + n * P * C) + g;
+  const int64_t G64 = G;
+
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t p = p0 + r; p < p1; p += static_cast<int64_t>(R) * kUnroll) {
+    u32x4_t v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      // Positions past the slice re-read the slice's first row (in bounds)
+      // and are zeroed.
+      const int64_t pu = p + static_cast<int64_t>(u) * R;
+      v[u] = __builtin_nontemporal_load(xv + (pu < p1 ? pu : p0) * G64);
+      if (pu >= p1) v[u] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        acc[2 * d] += bf16lo(v[u][d]);
+        acc[2 * d + 1] += bf16hi(v[u][d]);
+      }
+    }
+  }
+  if (R > 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lds[t * 8 + e] = acc[e];
+    __syncthreads();
+    if (t < G) {
+      for (int k = 1; k < R; ++k) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += lds[(k * G + t) * 8 + e];
+      }
+    }
+  }
+  if (t >= G) return;
+  if (slices == 1) {
+    const float inv = 1.0f / static_cast<float>(P);
+    u32x4_t o;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[d] = pack_bf16x2(acc[2 * d] * inv, acc[2 * d + 1] * inv);
+    *reinterpret_cast<u32x4_t*>(out + n * C + 8 * g) = o;
+  } else {
+    float* dst = partial + (n * slices + s) * C + 8 * g;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[e] = acc[e];
+  }
+}
+
+// out[n, c] = bf16(sum_s partial[n, s, c] / P), slices added in order.
+__global__ __launch_bounds__(256) void spatial_mean_finish(
+    const float* __restrict__ partial, uint16_t* __restrict__ out, int64_t N,
+    int64_t P, int64_t C, int slices) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= N * C) return;
+  const int64_t n = i / C, c = i - n * C;
+  const float* src = partial + n * slices * C + c;
+  float sum = src[0];
+  for (int s = 1; s < slices; ++s) sum += src[static_cast<int64_t>(s) * C];
+  out[i] = static_cast<uint16_t>(pack_bf16x2(sum / static_cast<float>(P), 0.f) & 0xffffu);
+}
+
+// Any C: one thread per (n, c), strided loads.
+__global__ __launch_bounds__(256) void spatial_mean_nhwc_scalar(
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ out, int64_t N,
+    int64_t P, int64_t C) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= N * C) return;
+  const int64_t n = i / C, c = i - n * C;
+  const uint16_t* src = x + n * P * C + c;
+  float sum = 0.f;
+  for (int64_t p = 0; p < P; ++p) sum += bf16_to_f32(src[p * C]);
+  out[i] = static_cast<uint16_t>(pack_bf16x2(sum / static_cast<float>(P), 0.f) & 0xffffu);
+}
+
+int64_t gcd64(int64_t a, int64_t b) {
+  while (b) {
+    const int64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+// Threads per workgroup and position slices per image for the vector path
+// (0 threads: use the scalar kernel).
+struct SpatialPlan {
+  int threads = 0;
+  int slices = 1;
+  int64_t slice_len = 0;
+};
+
+SpatialPlan spatial_plan(int64_t n, int64_t p, int64_t c) {
+  SpatialPlan plan;
+  if (c % 8 != 0 || c / 8 > kMaxThreads || n <= 0 || p <= 0) return plan;
+  const int64_t G = c / 8;
+  const int64_t lcm = G / gcd64(G, kWave) * kWave;
+  int64_t T = lcm <= kMaxThreads ? lcm * std::max<int64_t>(1, 512 / lcm) : G;
+  const int64_t rows = T / G;
+  if (rows > p) T = G * std::max<int64_t>(1, p);  // no more rows than positions
+  plan.threads = static_cast<int>(std::min<int64_t>(T, kMaxThreads));
+  const int64_t R = plan.threads / G;
+  // About 256 workgroups, each slice at least 4 loads per thread deep and
+  // the fp32 partials at most ~6 % of the input traffic (2 S / P).
+  int64_t S = std::min<int64_t>((256 + n - 1) / n, std::max<int64_t>(1, p / (4 * R)));
+  S = std::max<int64_t>(1, std::min<int64_t>(S, p / 32));
+  plan.slices = static_cast<int>(S);
+  plan.slice_len = (p + S - 1) / S;
+  return plan;
+}
+
+}  // namespace
+}  // namespace hipo
+
+extern "C" size_t hipo_spatial_mean_workspace_bytes(int64_t n, int64_t hw, int64_t c) {
+  const hipo::SpatialPlan plan = hipo::spatial_plan(n, hw, c);
+  if (plan.threads == 0 || plan.slices <= 1) return 0;
+  return static_cast<size_t>(n * plan.slices * c) * sizeof(float);
+}
+
+extern "C" int hipo_spatial_mean_nhwc_bf16(const uint16_t* x, uint16_t* out, int64_t n,
+                                          int64_t hw, int64_t c, void* workspace,
+                                          size_t workspace_bytes, hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  HIPO_REQUIRE(n >= 0 && hw >= 0 && c >= 0, "spatial_mean: negative size");
+  if (n == 0 || c == 0) return 0;
+  HIPO_REQUIRE(hw > 0, "spatial_mean: empty spatial extent");
+  HIPO_REQUIRE(x && out, "spatial_mean: null pointer");
+  const SpatialPlan plan = spatial_plan(n, hw, c);
+  if (plan.threads > 0 && aligned16(x) && aligned16(out)) {
+    const size_t need = plan.slices > 1 ? static_cast<size_t>(n * plan.slices * c) * 4 : 0;
+    HIPO_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+                 "spatial_mean: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    const int64_t blocks = n * plan.slices;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "spatial_mean: too many images");
+    const int G = static_cast<int>(c / 8);
+    const int R = plan.threads / G;
+    const size_t lds = R > 1 ? static_cast<size_t>(plan.threads) * 8 * sizeof(float) : 0;
+    spatial_mean_nhwc_partial<<<dim3(static_cast<unsigned>(blocks)), dim3(plan.threads), lds,
+                                stream>>>(x, out, static_cast<float*>(workspace), hw, c, G,
+                                          plan.slices, plan.slice_len);
+    if (plan.slices > 1) {
+      const int64_t total = n * c;
+      spatial_mean_finish<<<dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                            stream>>>(static_cast<const float*>(workspace), out, n, hw, c,
+                                      plan.slices);
+    }
+  } else {
+    const int64_t total = n * c;
+    HIPO_REQUIRE((total + 255) / 256 <= 0x7fffffff, "spatial_mean: too large");
+    spatial_mean_nhwc_scalar<<<dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                               stream>>>(x, out, n, hw, c);
+  }
+  return check_launch("spatial_mean_nhwc_bf16");
+}

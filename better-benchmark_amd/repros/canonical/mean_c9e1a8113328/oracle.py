@@ -1,0 +1,34 @@
+"""
+MI355X oracle for mean_c9e1a8113328: spatial mean of a channels-last bf16
+tensor over H, W (keepdim).
+
+Kernel: hipo_spatial_mean_nhwc_bf16 -- per image a column reduction of the
+[H*W, C] block: each workgroup instruction reads whole contiguous rows, every
+thread keeps fp32 sums for one 8-channel group, partial sums meet in LDS in a
+fixed order (and, when positions are split for parallelism, a second pass
+adds the slices in order).  Algorithmic bytes: 2 N H W C + 2 N C.
+Replaces the Triton body of the reference's
+repros/canonical/mean_c9e1a8113328/oracle.py:95 (_spatial_mean_cl_kernel, :11).
+"""
+import sys
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+import hip_oracles  # noqa: E402
+from oracle_harness import oracle_impl  # noqa: E402
+
+_POINTS = ("69db7514", "280fa7d2", "2645a53e", "4ca56f88", "d1686c77", "333b11d0",
+           "547c8164", "f0a667e3", "44f1e75f", "4784273d", "3cf84b69", "2150fa2c",
+           "6b68d184", "d3381898", "473b7062", "630d0797")
+
+
+def oracle_forward(inputs):
+    (x,) = inputs
+    return hip_oracles.spatial_mean_nhwc(x, keepdim=True)
+
+
+for _point in _POINTS:
+    oracle_forward = oracle_impl(hardware="MI355X", point=_point,
+                                 description="channels-last spatial mean")(oracle_forward)
+oracle_forward = oracle_impl(hardware="MI355X",
+                             description="channels-last spatial mean, shape-general")(oracle_forward)

@@ -58,8 +58,9 @@ int hipo_row_mean_f32(const float* x, float* out, int64_t rows, int64_t cols,
  * Channel bias + GELU(tanh) + NCHW -> NHWC:
  *   t = bf16(x[n,c,hw] + bias[c])       (eager order: the add rounds to bf16)
  *   y = 0.5 t (1 + tanh(sqrt(2/pi) (t + 0.044715 t^3)))
- *   out[n,hw,c] = bf16(y)    (correctly rounded: y comes from a 65536-entry
- *                             table over every bf16 t, computed in double)
+ *   out[n,hw,c] = bf16(y)    (y in fp32 as t / (1 + 2^(t (K0 + K1 t^2))),
+ *                             the same function, with the hardware exp2 and
+ *                             reciprocal; one rounding)
  * x is contiguous NCHW [n, c, hw]; out is the same logical tensor stored
  * channels-last (physical [n, hw, c]).
  * Replaces the Triton bodies of oracle_forward in
@@ -91,7 +92,8 @@ int hipo_scaled_masked_softmax_bf16(const uint16_t* x, const uint16_t* mask,
  *   h = bf16(x + residual);  mean, var = fp32 stats of h (population var)
  *   rstd = 1/sqrt(var + eps);  y = bf16((h - mean) * rstd * gamma + beta)
  * x, residual, h, y are [rows, cols] contiguous; gamma, beta are [cols];
- * mean, rstd are fp32 [rows].
+ * mean, rstd are fp32 [rows].  h, mean and rstd may be NULL: that output is
+ * not written (the reference's var_mean_80e7ff4dee7f returns y only).
  * Replaces the Triton body of oracle_forward in
  * repros/canonical/var_mean_80e7ff4dee7f/oracle.py:122
  * (_residual_layernorm_kernel, same file :51).
@@ -113,6 +115,62 @@ int hipo_residual_layernorm_bf16(const uint16_t* x, const uint16_t* residual,
 int hipo_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma, uint16_t* y,
                       float* rstd, int64_t rows, int64_t cols, float eps,
                       hipStream_t stream);
+
+/*
+ * RMSNorm with the options the corpus variants use:
+ *   h = residual ? bf16(x + residual) : x       (the eager bf16 add)
+ *   rstd = 1/sqrt(mean(h^2) + eps)             (fp32)
+ *   mode 0: y = bf16(h * rstd * gamma * scale)  (torch rms_norm, one rounding)
+ *   mode 1: t = bf16(h * rstd); u = bf16(gamma * t);
+ *           y = scale == 1 ? u : bf16(u * scale)   (HF T5 LayerNorm op order)
+ * residual and rstd may be NULL.  Shapes as hipo_rmsnorm_bf16.
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/mean_4462ce967d63/oracle.py:65 (T5: residual, eps 1e-6,
+ * mode 1, scale 0.04419417382415922).
+ */
+int hipo_rmsnorm_ex_bf16(const uint16_t* x, const uint16_t* residual,
+                         const uint16_t* gamma, uint16_t* y, float* rstd,
+                         int64_t rows, int64_t cols, float eps, float scale,
+                         int mode, hipStream_t stream);
+
+/*
+ * Softmax over the last dim with an additive bias shared by groups of
+ * `heads` consecutive batch entries:
+ *   s[b,q,k] = bf16(bf16(x[b,q,k] * scale) + bias[b / heads][q, k])
+ *   out[b,q,:] = bf16(softmax_fp32(s[b,q,:]))
+ * bias row of (b, q): bias + (b / heads) * bias_batch_stride
+ *                          + q * bias_row_stride   (elements).
+ * hipo_scaled_masked_softmax_bf16 is the case bias_batch_stride = 0.
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/amax_sum_20ccc18dda60/oracle.py:63 (x viewed
+ * [64, 16, 256, 256] + bias [64, 1, 256, 256]: heads = 16, scale = 1).
+ */
+int hipo_scaled_bias_softmax_bf16(const uint16_t* x, const uint16_t* bias,
+                                  uint16_t* out, int64_t batch, int64_t q,
+                                  int64_t k, int64_t bias_row_stride,
+                                  int64_t bias_batch_stride, int64_t heads,
+                                  float scale, hipStream_t stream);
+
+/*
+ * Bytes of fp32 workspace hipo_spatial_mean_nhwc_bf16 needs (0: none).
+ */
+size_t hipo_spatial_mean_workspace_bytes(int64_t n, int64_t hw, int64_t c);
+
+/*
+ * Spatial mean of a channels-last bf16 tensor (a reduction over a
+ * non-innermost axis):
+ *   out[n, c] = bf16(sum_p x[n, p, c] / hw)     (fp32 accumulation)
+ * x is [n, c, h, w] stored channels-last, i.e. physical [n, hw, c] with c
+ * contiguous; out is [n, c] contiguous ([n, c, 1, 1] keepdim).  `workspace`
+ * holds fp32 partial sums when the kernel splits positions; size from
+ * hipo_spatial_mean_workspace_bytes (may be NULL when that is 0).
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/mean_c9e1a8113328/oracle.py:95
+ * (_spatial_mean_cl_kernel, same file :11).
+ */
+int hipo_spatial_mean_nhwc_bf16(const uint16_t* x, uint16_t* out, int64_t n,
+                                int64_t hw, int64_t c, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream);
 
 /*
  * Bytes of device workspace hipo_batchnorm_train_fwd_f32 needs for this

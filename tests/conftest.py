@@ -23,6 +23,16 @@ REPRO_IDS = [
 ]
 
 
+# Corpus families the kernels generalise to (the reference's canonical dir
+# names, their shape points and model counts).
+VARIANT_IDS = [
+    "mean_c9e1a8113328",
+    "mean_4462ce967d63",
+    "amax_sum_20ccc18dda60",
+    "var_mean_80e7ff4dee7f",
+]
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs the ROCm device (MI355X)")
 

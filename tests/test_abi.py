@@ -46,6 +46,14 @@ def test_abi_version_and_error_string(lib):
     (lambda l: l.hipo_residual_layernorm_bf16(None, None, None, None, None, None, None, None,
                                               4, 0, 1e-5, None), b"cols"),
     (lambda l: l.hipo_rmsnorm_bf16(None, None, None, None, -2, 8, 1e-5, None), b"negative"),
+    (lambda l: l.hipo_rmsnorm_bf16(1, 1, 1, None, 2, 8, 1e-5, None), b"null"),
+    (lambda l: l.hipo_rmsnorm_ex_bf16(1, None, 1, 1, None, 2, 8, 1e-5, 1.0, 2, None), b"mode"),
+    (lambda l: l.hipo_rmsnorm_ex_bf16(None, None, 1, 1, None, 2, 8, 1e-5, 1.0, 0, None), b"null"),
+    (lambda l: l.hipo_scaled_bias_softmax_bf16(1, 1, 1, 6, 4, 8, 8, 0, 4, 1.0, None), b"heads"),
+    (lambda l: l.hipo_scaled_bias_softmax_bf16(1, 1, 1, 6, 4, 8, 8, -8, 3, 1.0, None),
+     b"mask_batch_stride"),
+    (lambda l: l.hipo_spatial_mean_nhwc_bf16(1, 1, 2, 0, 8, None, 0, None), b"spatial"),
+    (lambda l: l.hipo_spatial_mean_nhwc_bf16(16, 16, 128, 4096, 256, None, 0, None), b"workspace"),
     (lambda l: l.hipo_batchnorm_train_fwd_f32(1, 1, 1, 1, 1, 1, 1, 1, 2, 4, 9, 0.1, 1e-5, 1,
                                               1, 0, None), b"workspace"),
     (lambda l: l.hipo_batchnorm_train_fwd_f32(None, 1, 1, 1, 1, 1, 1, 1, 2, 4, 9, 0.1, 1e-5, 1,
@@ -60,7 +68,20 @@ def test_empty_inputs_are_no_ops(lib):
     assert lib.hipo_row_mean_f32(None, None, 0, 16, 16, None) == 0
     assert lib.hipo_bias_gelu_nchw_to_nhwc_bf16(None, None, None, 0, 8, 8, None) == 0
     assert lib.hipo_scaled_masked_softmax_bf16(None, None, None, 3, 0, 8, 8, 1.0, None) == 0
+    assert lib.hipo_scaled_bias_softmax_bf16(None, None, None, 0, 4, 8, 8, 0, 1, 1.0, None) == 0
+    assert lib.hipo_rmsnorm_ex_bf16(None, None, None, None, None, 0, 8, 1e-5, 1.0, 0, None) == 0
+    assert lib.hipo_spatial_mean_nhwc_bf16(None, None, 0, 64, 8, None, 0, None) == 0
     assert lib.hipo_last_error() == b""
+
+
+def test_spatial_mean_workspace_bytes(lib):
+    # one slice per image when there are enough images or few positions
+    assert lib.hipo_spatial_mean_workspace_bytes(128, 36, 1536) == 0
+    assert lib.hipo_spatial_mean_workspace_bytes(0, 64, 8) == 0
+    # [128, 256, 64, 64]: two position slices -> fp32 partials [128, 2, 256]
+    assert lib.hipo_spatial_mean_workspace_bytes(128, 4096, 256) == 128 * 2 * 256 * 4
+    # C not a multiple of 8: the scalar kernel, no workspace
+    assert lib.hipo_spatial_mean_workspace_bytes(4, 4096, 100) == 0
 
 
 def test_batchnorm_workspace_bytes(lib):

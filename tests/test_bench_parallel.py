@@ -17,7 +17,7 @@ import pytest
 
 import bench_parallel as bp
 import gpu_lock
-from conftest import CANONICAL, REPRO_IDS
+from conftest import CANONICAL, REPRO_IDS, VARIANT_IDS
 from oracle_harness import _INVALID_STATUSES
 
 
@@ -48,10 +48,11 @@ def test_dir_and_display_names():
 
 def test_find_and_expand_the_canonical_dirs():
     dirs = bp.find_oracle_dirs([CANONICAL])
-    assert sorted(d.name for d in dirs) == sorted(REPRO_IDS)
+    assert sorted(d.name for d in dirs) == sorted(REPRO_IDS + VARIANT_IDS)
     tasks = bp._expand_oracle_shape_tasks(dirs)
-    # three shapes.json points per repro (BASELINE size + two ragged)
-    assert len(tasks) == 3 * len(REPRO_IDS)
+    # three shapes.json points per BASELINE repro (BASELINE size + two
+    # ragged); the corpus families carry the reference's points
+    assert len(tasks) == 3 * len(REPRO_IDS) + 16 + 1 + 1 + 1
     assert all("::SHAPE::" in t for t in tasks)
     from repro_harness import load_shape_configs
     for d in dirs:

@@ -13,7 +13,7 @@ import math
 import pytest
 import torch
 
-from conftest import CANONICAL, REPRO_IDS
+from conftest import CANONICAL, REPRO_IDS, VARIANT_IDS
 
 pytestmark = pytest.mark.gpu
 
@@ -89,6 +89,39 @@ def test_all_points_vs_oracle_and_eager(rid, rocm_device):
         for i, (g, e) in enumerate(zip(got, eager)):
             assert_close(g, e, _tol(e), f"{rid}/{label} out{i} vs eager")
         del cpu_in, dev_in, got, want, eager
+
+
+@pytest.mark.parametrize("rid", VARIANT_IDS)
+def test_family_points_vs_eager(rid, rocm_device):
+    """The reference's corpus families at their transcribed shapes.json
+    points, against the eager repro on the CPU (the reference harness's own
+    gate) and, for the bf16 outputs, against the fp64 eager result."""
+    from oracle_harness import _normalize_outputs, resolve_oracle
+    from repro_harness import make_inputs_from_config
+    fn, inst = _load(rid)
+    import oracle_harness
+    inst64 = oracle_harness.get_repro_instance(CANONICAL / rid).double()
+    for label, cfg in _points(rid).items():
+        print(f"[{rid}] point {label}", flush=True)
+        torch.manual_seed(1)
+        cpu_in = make_inputs_from_config(cfg, device="cpu")
+        dev_in = [t.to(rocm_device) if isinstance(t, torch.Tensor) else t for t in cpu_in]
+        impl, info = resolve_oracle(fn, dev_in)
+        assert info["matched"] == "hardware+shape", info
+        got = _normalize_outputs(impl(dev_in))
+        torch.cuda.synchronize()
+        with torch.no_grad():
+            eager = _normalize_outputs(inst(*[t.clone() if isinstance(t, torch.Tensor) else t
+                                             for t in cpu_in]))
+            exact = _normalize_outputs(inst64(*[t.double() if isinstance(t, torch.Tensor) else t
+                                               for t in cpu_in]))
+        assert len(got) == len(eager)
+        for i, (g, e, x) in enumerate(zip(got, eager, exact)):
+            assert g.dtype == e.dtype and g.shape == e.shape, f"{label} out{i}"
+            assert g.stride() == e.stride(), f"{label} out{i} strides {g.stride()} vs {e.stride()}"
+            assert_close(g, e, _tol(e), f"{rid}/{label} out{i} vs eager")
+            assert_close(g, x, _tol(e), f"{rid}/{label} out{i} vs fp64")
+        del cpu_in, dev_in, got, eager, exact
 
 
 # ---------------------------------------------------------------------------
@@ -283,6 +316,133 @@ def test_row_layouts_multiwave(rocm_device):
         x = torch.randn(rows, cols, generator=g) * 3 + 1
         assert_close(hip_oracles.row_mean(x.to(rocm_device)), ref.row_mean(x), F32_TOL,
                      f"row_mean {rows}x{cols}")
+
+
+def _rms_ref(x, gamma, eps, residual=None, scale=1.0, mode=0):
+    """fp32 torch restatement of the eager op orders (CPU)."""
+    bf = torch.bfloat16
+    h = x if residual is None else (x + residual)          # bf16 add, rounded
+    hf = h.float()
+    rstd = torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + eps)
+    if mode == 0:
+        y = (hf * rstd * gamma.float() * scale).to(bf)
+    else:
+        y = gamma * (hf * rstd).to(bf)                      # bf16 mul, rounded
+        if scale != 1.0:
+            y = y * scale
+    return y, rstd.squeeze(-1)
+
+
+def test_rmsnorm_ex_modes(rocm_device):
+    import hip_oracles
+    bf = torch.bfloat16
+    for rows, cols in [(7, 100), (64, 512), (5, 4104), (3, 8), (2, 32776)]:
+        g = torch.Generator().manual_seed(rows * 31 + cols)
+        x = torch.randn(rows, cols, generator=g).to(bf)
+        r = torch.randn(rows, cols, generator=g).to(bf)
+        gm = (1 + 0.1 * torch.randn(cols, generator=g)).to(bf)
+        for residual, scale, mode, eps in [(None, 1.0, 0, 1e-5), (r, 1.0, 0, 1e-5),
+                                           (r, 0.04419417382415922, 1, 1e-6),
+                                           (None, 1.0, 1, 1e-6), (r, 2.5, 0, 1e-6)]:
+            what = f"rmsnorm_ex {rows}x{cols} res={residual is not None} scale={scale} mode={mode}"
+            print(f"[edges] {what}", flush=True)
+            y, rstd = hip_oracles.rmsnorm_ex(
+                x.to(rocm_device), gm.to(rocm_device), eps, scale=scale, mode=mode,
+                residual=None if residual is None else residual.to(rocm_device), want_rstd=True)
+            wy, wr = _rms_ref(x, gm, eps, residual, scale, mode)
+            assert_close(y, wy, BF16_TOL, what + " y")
+            assert_close(rstd, wr, F32_TOL, what + " rstd")
+            y2 = hip_oracles.rmsnorm_ex(
+                x.to(rocm_device), gm.to(rocm_device), eps, scale=scale, mode=mode,
+                residual=None if residual is None else residual.to(rocm_device))
+            assert torch.equal(y2.cpu(), y.cpu()), what + ": rstd=NULL changes y"
+    # closed form: rows of a constant c have rstd = 1/sqrt(c^2 + eps) and, in
+    # mode 1 with gamma = 1, y = bf16(c * rstd) * scale rounded
+    x = torch.full((4, 512), 3.0, dtype=bf)
+    gm = torch.ones(512, dtype=bf)
+    y, rstd = hip_oracles.rmsnorm_ex(x.to(rocm_device), gm.to(rocm_device), 1e-6, mode=1,
+                                     scale=0.5, want_rstd=True)
+    assert_close(rstd, torch.full((4,), 1 / math.sqrt(9 + 1e-6)), F32_TOL, "rstd constant")
+    assert torch.equal(y.cpu(), torch.full((4, 512), 0.5, dtype=bf))
+
+
+def test_scaled_bias_softmax_heads_and_strides(rocm_device):
+    import hip_oracles
+    bf = torch.bfloat16
+
+    def ref(x, bias, scale, heads):
+        b, q, k = x.shape
+        s = (x * scale) if scale != 1.0 else x
+        s = (s.view(b // heads, heads, q, k) + bias.unsqueeze(1)).view(b, q, k)
+        return torch.softmax(s.float(), -1).to(bf)
+
+    for b, heads, q, k, scale in [(12, 4, 17, 1032, 1.0), (8, 8, 5, 256, 0.125), (6, 2, 9, 100, 1.0),
+                                  (4, 1, 3, 4104, 0.5), (2, 2, 2, 32768, 1.0)]:
+        what = f"bias_softmax b={b} heads={heads} q={q} k={k}"
+        print(f"[edges] {what}", flush=True)
+        g = torch.Generator().manual_seed(b * q + k)
+        x = torch.randn(b, q, k, generator=g).to(bf)
+        bias = torch.randn(b // heads, q, k, generator=g).to(bf)
+        got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), scale, heads)
+        assert_close(got, ref(x, bias, scale, heads), BF16_TOL, what)
+        # the same bias as a padded view (row stride > K) and as a broadcast
+        # over Q (row stride 0, materialised by the wrapper)
+        padded = torch.randn(b // heads, q, k + 8, generator=g).to(bf)
+        view = padded.to(rocm_device)[:, :, :k]
+        got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), view, scale, heads)
+        assert_close(got, ref(x, padded[:, :, :k], scale, heads), BF16_TOL, what + " padded")
+        row = torch.randn(b // heads, 1, k, generator=g).to(bf)
+        got = hip_oracles.scaled_bias_softmax(x.to(rocm_device),
+                                              row.to(rocm_device).expand(b // heads, q, k),
+                                              scale, heads)
+        assert_close(got, ref(x, row.expand(b // heads, q, k), scale, heads), BF16_TOL,
+                     what + " broadcast over q")
+    # closed form: a bias of -inf except one column gives a one-hot row
+    x = torch.randn(4, 3, 64).to(bf)
+    bias = torch.full((2, 3, 64), float("-inf")).to(bf)
+    bias[:, :, 5] = 0
+    got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), 1.0, 2).cpu()
+    want = torch.zeros(4, 3, 64, dtype=bf)
+    want[:, :, 5] = 1
+    assert torch.equal(got, want)
+
+
+def test_masked_softmax_broadcast_mask_rows(rocm_device):
+    """A mask expanded over Q (row stride 0) is materialised, not misread."""
+    import hip_oracles
+    import oracle as ref
+    bf = torch.bfloat16
+    x = torch.randn(3, 6, 264).to(bf)
+    row = torch.randn(1, 264).to(bf)
+    got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), row.to(rocm_device).expand(6, 264), 0.125)
+    assert_close(got, ref.scaled_masked_softmax(x, row.expand(6, 264).contiguous(), 0.125),
+                 BF16_TOL, "broadcast mask")
+
+
+def test_spatial_mean_layouts(rocm_device):
+    """Vector path (one slice and several), C not a multiple of 8 and
+    C / 8 above 1024 (scalar kernel), one position, non-power-of-two group
+    counts, keepdim off."""
+    import hip_oracles
+    bf = torch.bfloat16
+    for n, c, h, w in [(2, 96, 7, 7), (1, 240, 33, 33), (3, 20, 5, 5), (1, 8, 1, 1),
+                       (1, 8192, 2, 2), (2, 8200, 3, 3), (4, 1536, 6, 6), (1, 256, 72, 72),
+                       (256, 64, 2, 3), (1, 24, 300, 7)]:
+        what = f"spatial_mean n={n} c={c} {h}x{w}"
+        print(f"[edges] {what}", flush=True)
+        g = torch.Generator().manual_seed(n * c + h * w)
+        x = (torch.randn(n, c, h, w, generator=g) + 0.25).to(bf).contiguous(
+            memory_format=torch.channels_last)
+        got = hip_oracles.spatial_mean_nhwc(x.to(rocm_device))
+        want = x.double().mean((2, 3), keepdim=True)
+        assert got.shape == (n, c, 1, 1) and got.is_contiguous()
+        assert_close(got, want, BF16_TOL, what)
+        flat = hip_oracles.spatial_mean_nhwc(x.to(rocm_device), keepdim=False)
+        assert torch.equal(flat.cpu(), got.cpu().view(n, c)), what + " keepdim"
+    # closed form: a constant tensor averages to itself exactly
+    x = torch.full((2, 512, 24, 24), 1.25, dtype=bf).contiguous(memory_format=torch.channels_last)
+    assert torch.equal(hip_oracles.spatial_mean_nhwc(x.to(rocm_device)).cpu(),
+                       torch.full((2, 512, 1, 1), 1.25, dtype=bf))
 
 
 def test_batchnorm_closed_forms_and_edges(rocm_device):

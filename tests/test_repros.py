@@ -76,3 +76,86 @@ def test_repro_contract(rid):
     torch.manual_seed(0)
     out = mod.Repro()(*make_inputs_from_config(small, device="cpu"))
     assert out is not None
+
+
+# ---------------------------------------------------------------------------
+# Corpus families (the reference's canonical dirs; small inputs of the same
+# structure, checked against independent formulations)
+# ---------------------------------------------------------------------------
+
+from conftest import VARIANT_IDS  # noqa: E402
+
+bf = torch.bfloat16
+
+
+def test_spatial_mean_family_repro():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 40, 5, 6, generator=g).to(bf).contiguous(memory_format=torch.channels_last)
+    y = get_repro_instance(CANONICAL / "mean_c9e1a8113328")(x)
+    assert y.shape == (3, 40, 1, 1) and y.dtype == bf
+    assert torch.equal(y, x.mean(dim=(2, 3), keepdim=True))
+
+
+def test_t5_rmsnorm_family_repro():
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(6, 64, generator=g).to(bf)
+    r = torch.randn(2, 3, 64, generator=g).to(bf)
+    w = torch.randn(64, generator=g).to(bf)
+    y = get_repro_instance(CANONICAL / "mean_4462ce967d63")(x, r, w, [2, 3, 64], [6, 64])
+    h = (r + x.view(2, 3, 64)).float()
+    rstd = torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)
+    normed = (h * rstd).to(bf)
+    want = ((w * normed) * 0.04419417382415922).view(6, 64)
+    assert torch.equal(y, want) and y.dtype == bf
+
+
+def test_bias_softmax_family_repro():
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(8, 5, 12, generator=g).to(bf)      # 2 groups x 4 heads
+    b = torch.randn(2, 1, 5, 12, generator=g).to(bf)
+    y = get_repro_instance(CANONICAL / "amax_sum_20ccc18dda60")(x, b, [2, 4, 5, 12], [8, 5, 12])
+    want = torch.softmax((x.view(2, 4, 5, 12) + b).float(), -1).to(bf).view(8, 5, 12)
+    assert torch.equal(y, want)
+
+
+def test_longformer_layernorm_family_repro():
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(6, 32, generator=g).to(bf)
+    r = torch.randn(2, 3, 32, generator=g).to(bf)
+    w, b = torch.randn(32, generator=g).to(bf), torch.randn(32, generator=g).to(bf)
+    y = get_repro_instance(CANONICAL / "var_mean_80e7ff4dee7f")(x, r, w, b, [2, 3, 32])
+    h = (x.view(2, 3, 32) + r).float()
+    want = F.layer_norm(h, [32], w.float(), b.float(), 1e-5).to(bf)
+    assert y.shape == (2, 3, 32)
+    assert (y.float() - want.float()).abs().max() <= 1.6e-2 * want.float().abs().max()
+
+
+def test_family_repros_compute_in_fp64_for_the_gate():
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(6, 64, generator=g).double()
+    r = torch.randn(2, 3, 64, generator=g).double()
+    w = torch.randn(64, generator=g).double()
+    y = get_repro_instance(CANONICAL / "mean_4462ce967d63").double()(x, r, w, [2, 3, 64], [6, 64])
+    assert y.dtype == torch.float64
+    b = torch.randn(64, generator=g).double()
+    y = get_repro_instance(CANONICAL / "var_mean_80e7ff4dee7f").double()(x, r, w, b, [2, 3, 64])
+    assert y.dtype == torch.float64
+
+
+@pytest.mark.parametrize("rid", VARIANT_IDS)
+def test_family_repro_contract(rid):
+    mod = load_repro_module(CANONICAL / rid)
+    assert hasattr(mod, "Repro") and hasattr(mod, "make_inputs") and mod._repro_version == 3
+    cfgs = load_shape_configs(str(CANONICAL / rid / "repro.py"))
+    assert len(cfgs) >= 1
+    import json
+    meta = json.loads((CANONICAL / rid / "meta.json").read_text())
+    assert rid.endswith(meta["pattern_hash"])
+    # every shapes.json point has its MI355X registration, plus one
+    # shape-general entry for shapes outside the corpus
+    import oracle_harness as oh
+    _, fn, _ = oh._load_oracle_module(CANONICAL / rid)
+    entries = oh.get_module_registry(fn.__module__)._entries
+    hashes = {p["shape_hash"] for p in json.loads((CANONICAL / rid / "shapes.json").read_text())["points"]}
+    assert {e["point"] for e in entries if e["point"]} == hashes
+    assert any(e["shape"] is None and e["hardware"] == "MI355X" for e in entries)
