@@ -99,14 +99,15 @@ def _task_display_name(task_key: str) -> str:
 
 
 def find_oracle_dirs(paths: list[Path]) -> list[Path]:
-    """Canonical dirs holding an oracle (oracle*.py) next to a repro.py."""
+    """Canonical dirs holding an oracle (oracle*.py) next to a repro.py, as
+    absolute paths (the workers run from the package dir)."""
     def has_oracle(d: Path) -> bool:
         return (d / "repro.py").is_file() and any(d.glob("oracle*.py"))
 
     out: list[Path] = []
     seen: set[str] = set()
     for p in paths:
-        p = Path(p)
+        p = Path(p).resolve()
         cands = [p] if p.is_dir() and has_oracle(p) else (
             sorted({f.parent for f in p.rglob("repro.py")}) if p.is_dir() else
             [p.parent] if p.name == "repro.py" else [])

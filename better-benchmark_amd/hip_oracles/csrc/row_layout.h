@@ -100,6 +100,45 @@ __device__ __forceinline__ void row_store_stream(uint16_t* row, int64_t col,
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(row + col));
 }
 
+// Short rows (cols <= 512): a row owns L = 2^j consecutive lanes (L groups
+// of 8 bf16), so one 16-byte access instruction of a wave covers 64 / L
+// rows.  seg_sum / seg_max reduce within each aligned segment of L lanes
+// (DPP quad swaps, half-row and row mirrors, then lane-xor shuffles across
+// 16-lane rows); every lane of a segment receives the same value, and the
+// order of the additions is fixed.  All 64 lanes must be active.
+constexpr int kDppRowMirror = 0x140;      // lane i <- 15 - i within a row
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <- 7 - i within a half-row
+
+template <int L>
+__device__ __forceinline__ float seg_sum(float v) {
+  if constexpr (L >= 2) v += dpp<kDppQuadXor1>(v);
+  if constexpr (L >= 4) v += dpp<kDppQuadXor2>(v);
+  if constexpr (L >= 8) v += dpp<kDppRowHalfMirror>(v);
+  if constexpr (L >= 16) v += dpp<kDppRowMirror>(v);
+  if constexpr (L >= 32) v += __shfl_xor(v, 16);
+  if constexpr (L >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+template <int L>
+__device__ __forceinline__ float seg_max(float v) {
+  if constexpr (L >= 2) v = fmaxf(v, dpp<kDppQuadXor1>(v));
+  if constexpr (L >= 4) v = fmaxf(v, dpp<kDppQuadXor2>(v));
+  if constexpr (L >= 8) v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+  if constexpr (L >= 16) v = fmaxf(v, dpp<kDppRowMirror>(v));
+  if constexpr (L >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+  if constexpr (L >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// Lanes per row for a short row (0: not short).
+inline int short_row_lanes(int64_t cols) {
+  if (cols <= 0 || cols > kRowSweep) return 0;
+  int L = 1;
+  while (L * kRowGroup < cols) L *= 2;
+  return L;
+}
+
 // Host side: waves per row, groups per lane, rows per workgroup for a row of
 // `cols` bf16 values (cols % 8 == 0).  Groups per lane are rounded up to a
 // power of two (the kernels are instantiated for 1, 2, 4, 8); returns false

@@ -61,6 +61,14 @@ def test_find_and_expand_the_canonical_dirs():
                 if bp._split_shape_task_key(t)[0] == str(d)] == labels
 
 
+def test_find_resolves_relative_dirs(monkeypatch):
+    """Workers run from the package dir: a relative path on the command line
+    must reach them as an absolute one."""
+    monkeypatch.chdir(CANONICAL.parent)
+    dirs = bp.find_oracle_dirs([Path("canonical") / REPRO_IDS[0]])
+    assert [d.name for d in dirs] == [REPRO_IDS[0]] and dirs[0].is_absolute()
+
+
 def test_expand_falls_back_to_default(monkeypatch, tmp_path):
     import repro_harness
     good, none, boom = tmp_path / "good", tmp_path / "none", tmp_path / "boom"

@@ -243,6 +243,40 @@ def test_softmax_closed_forms(rocm_device):
     assert_close(got.float().sum(-1), torch.ones(4, 128), 1e-2, "row sums")
 
 
+def test_softmax_short_rows(rocm_device):
+    """K <= 512 (several rows per wave, reductions within lane segments):
+    every segment width, K not a power of two (idle lanes), row counts that
+    leave the last wave partly empty, per-group biases, fully masked rows."""
+    import hip_oracles
+    import oracle as ref
+    bf = torch.bfloat16
+    for k in (8, 16, 24, 40, 64, 72, 128, 136, 200, 248, 256, 264, 384, 504, 512):
+        for b, q, scale in ((3, 7, 0.125), (1, 1, 1.0), (5, 33, 0.3)):
+            what = f"short softmax b={b} q={q} k={k} scale={scale}"
+            print(f"[short] {what}", flush=True)
+            g = torch.Generator().manual_seed(k * 100 + q)
+            x = (2 * torch.randn(b, q, k, generator=g)).to(bf)
+            m = torch.triu(torch.full((q, k), float("-inf")), 1 + k // 3).to(bf)
+            m[q // 2] = float("-inf")                      # one fully masked row -> NaN
+            got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), m.to(rocm_device), scale)
+            want = ref.scaled_masked_softmax(x, m, scale)
+            assert_close(got, want, BF16_TOL, what)
+            assert torch.isnan(got[:, q // 2].float()).all().item(), what + " masked row"
+        x = torch.randn(12, 9, k).to(bf)
+        bias = torch.randn(3, 9, k).to(bf)
+        got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), 1.0, 4)
+        want = torch.softmax((x.view(3, 4, 9, k) + bias.unsqueeze(1)).float(), -1).to(bf).view(12, 9, k)
+        assert_close(got, want, BF16_TOL, f"short bias softmax k={k}")
+    # the TrOCR shape: 1024 rows of 256 per group of 16 heads
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(64, 256, 256, generator=g).to(bf)
+    bias = torch.randn(4, 256, 256, generator=g).to(bf)
+    got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), 1.0, 16)
+    want = torch.softmax((x.view(4, 16, 256, 256) + bias.unsqueeze(1)).float(), -1).to(bf).view(64, 256, 256)
+    assert_close(got, want, BF16_TOL, "trocr-like")
+    assert_close(got.float().sum(-1), torch.ones(64, 256), 1e-2, "row sums")
+
+
 def test_norm_closed_forms(rocm_device):
     import hip_oracles
     bf = torch.bfloat16
