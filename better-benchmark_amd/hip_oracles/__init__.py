@@ -51,6 +51,16 @@ _SIGNATURES = {
     "hipo_spatial_mean_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
     "hipo_spatial_mean_nhwc_bf16": (
         ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, ctypes.c_size_t, _c_ptr]),
+    "hipo_batchnorm_nhwc_workspace_bytes": (ctypes.c_size_t, [_c_i64] * 4),
+    "hipo_batchnorm_nhwc_act_pad_bf16": (
+        ctypes.c_int,
+        [_c_ptr] * 8 + [_c_i64] * 6 + [_c_f32] * 3 + [ctypes.c_int, _c_ptr, ctypes.c_size_t,
+                                                   _c_ptr]),
+    "hipo_batchnorm_nchw_mean_workspace_bytes": (ctypes.c_size_t, [_c_i64] * 3),
+    "hipo_batchnorm_nchw_act_mean_bf16": (
+        ctypes.c_int,
+        [_c_ptr] * 8 + [_c_i64] * 3 + [_c_f32] * 3 + [ctypes.c_int, _c_ptr, ctypes.c_size_t,
+                                                   _c_ptr]),
     "hipo_batchnorm_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
     "hipo_batchnorm_train_fwd_f32": (
         ctypes.c_int,
@@ -369,6 +379,74 @@ def batchnorm_train(x, gamma, beta, running_mean, running_var, *, momentum: floa
     return y, save_mean, save_invstd
 
 
+_BN_ACTS = {None: 0, "none": 0, "relu": 1, "silu": 2}
+
+
+def _bn_bf16_params(what, c, dev, gamma, beta, running_mean, running_var):
+    for t in (gamma, beta, running_mean, running_var):
+        _require(t.device == dev and t.dtype == torch.float32 and t.numel() == c
+                 and t.is_contiguous(),
+                 f"{what}: gamma/beta/running stats must be contiguous fp32 [C]")
+
+
+def batchnorm_nhwc_act_pad(x, gamma, beta, running_mean, running_var, *, momentum: float,
+                           eps: float, var_scale: float, act: str | None = "silu",
+                           pad_bottom: int = 0, pad_right: int = 0):
+    """BatchNorm training forward of a channels-last bf16 [N, C, H, W] tensor
+    with fp32 statistics, an activation and a zero pad of the bottom/right
+    border.  Returns (save_mean [1, C, 1, 1], save_rstd [1, C, 1, 1], out
+    [N, C, H + pad_bottom, W + pad_right] channels-last bf16); running_mean
+    / running_var are updated in place."""
+    lib = load_library()
+    dev = _require_rocm(x)
+    _require(x.dim() == 4 and x.dtype == torch.bfloat16
+             and x.is_contiguous(memory_format=torch.channels_last),
+             "batchnorm_nhwc: x must be a channels-last bf16 [N, C, H, W] tensor")
+    _require(act in _BN_ACTS, f"batchnorm_nhwc: act must be one of {sorted(map(str, _BN_ACTS))}")
+    n, c, h, w = x.shape
+    _bn_bf16_params("batchnorm_nhwc", c, dev, gamma, beta, running_mean, running_var)
+    out = torch.empty((n, c, h + pad_bottom, w + pad_right), dtype=torch.bfloat16, device=dev,
+                      memory_format=torch.channels_last)
+    save_mean = torch.empty((1, c, 1, 1), dtype=torch.float32, device=dev)
+    save_rstd = torch.empty((1, c, 1, 1), dtype=torch.float32, device=dev)
+    need = int(lib.hipo_batchnorm_nhwc_workspace_bytes(n, h, w, c))
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib.hipo_batchnorm_nhwc_act_pad_bf16(
+            _ptr(x), _ptr(gamma), _ptr(beta), _ptr(running_mean), _ptr(running_var),
+            _ptr(save_mean), _ptr(save_rstd), _ptr(out), n, h, w, c, int(pad_bottom),
+            int(pad_right), float(momentum), float(eps), float(var_scale), _BN_ACTS[act],
+            _ptr(ws), ws.numel(), _stream(dev)), "batchnorm_nhwc_act_pad")
+    return save_mean, save_rstd, out
+
+
+def batchnorm_nchw_act_mean(x, gamma, beta, running_mean, running_var, *, momentum: float,
+                            eps: float, var_scale: float, act: str | None = "relu"):
+    """BatchNorm training forward of a contiguous NCHW bf16 tensor with fp32
+    statistics, an activation and the mean over H, W.  Returns (save_mean
+    [1, C, 1, 1], save_rstd [1, C, 1, 1], out [N, C] bf16); running_mean /
+    running_var are updated in place."""
+    lib = load_library()
+    dev = _require_rocm(x)
+    _require(x.dim() == 4 and x.dtype == torch.bfloat16 and x.is_contiguous(),
+             "batchnorm_nchw: x must be a contiguous NCHW bf16 tensor")
+    _require(act in _BN_ACTS, f"batchnorm_nchw: act must be one of {sorted(map(str, _BN_ACTS))}")
+    n, c, h, w = x.shape
+    _bn_bf16_params("batchnorm_nchw", c, dev, gamma, beta, running_mean, running_var)
+    out = torch.empty((n, c), dtype=torch.bfloat16, device=dev)
+    save_mean = torch.empty((1, c, 1, 1), dtype=torch.float32, device=dev)
+    save_rstd = torch.empty((1, c, 1, 1), dtype=torch.float32, device=dev)
+    need = int(lib.hipo_batchnorm_nchw_mean_workspace_bytes(n, c, h * w))
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib.hipo_batchnorm_nchw_act_mean_bf16(
+            _ptr(x), _ptr(gamma), _ptr(beta), _ptr(running_mean), _ptr(running_var),
+            _ptr(save_mean), _ptr(save_rstd), _ptr(out), n, c, h * w, float(momentum),
+            float(eps), float(var_scale), _BN_ACTS[act], _ptr(ws), ws.numel(), _stream(dev)),
+            "batchnorm_nchw_act_mean")
+    return save_mean, save_rstd, out
+
+
 def batchnorm_error_flag(dev: torch.device | None = None) -> int:
     """Sticky error word of the device's shared BatchNorm workspace: nonzero
     once an exchange wait of the single-pass kernel has timed out (that
@@ -383,6 +461,7 @@ __all__ = [
     "HipOraclesUnavailable", "LIB_PATH", "load_library", "header_symbols",
     "row_mean", "bias_gelu_nchw_to_nhwc", "scaled_masked_softmax",
     "residual_layernorm", "rmsnorm", "rmsnorm_ex", "scaled_bias_softmax", "spatial_mean_nhwc",
+    "batchnorm_nhwc_act_pad", "batchnorm_nchw_act_mean",
     "batchnorm_workspace_bytes", "batchnorm_train",
     "batchnorm_cached_workspace", "batchnorm_error_flag",
 ]

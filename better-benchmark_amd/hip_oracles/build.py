@@ -35,6 +35,7 @@ SOURCES = [
     "batchnorm.hip",
     "batchnorm_fused.hip",
     "spatial_mean.hip",
+    "batchnorm_bf16.hip",
 ]
 
 # Packed-FP32 VALU forms are disabled for all device code (the compiler

@@ -1,0 +1,541 @@
+// BatchNorm training forward on bf16 activations (fp32 statistics) with the
+// epilogues of two corpus families:
+//   * channels-last x [N, C, H, W] (physical [N*H*W, C]) -> activation ->
+//     zero pad of the bottom / right border, channels-last output
+//     (reference repros/canonical/var_mean_ceb5c315290a: SiLU, pad 1);
+//   * NCHW x [N, C, H, W] -> activation -> mean over H, W -> [N, C]
+//     (reference repros/canonical/var_mean_mean_19ffdb35cc67: ReLU).
+// Semantics (the eager graphs' op order):
+//   mean, var = var_mean(fp32(x), [0, 2, 3], correction 0)
+//   save_rstd = 1 / sqrt(var + eps)
+//   y = act(bf16(((x - mean) * save_rstd) * gamma + beta))   (fp32 ops)
+//   running_mean = mean * momentum + running_mean * (1 - momentum)
+//   running_var  = (var * var_scale) * momentum + running_var * (1 - momentum)
+// var_scale is the graph's Bessel constant (N/(N-1) of the shape the graph
+// was captured at), passed through unchanged.
+//
+// Three launches, no atomics, deterministic:
+//   1. partial statistics per slice of the reduction axis -> workspace
+//      (mean, M2) per (slice, channel);
+//   2. one wave per channel merges the slices (Chan's formula in fp64, a
+//      fixed butterfly order) and writes save_mean, save_rstd and the running
+//      statistics;
+//   3. the normalise + activation pass (padded store / spatial mean).
+// HBM-bound: x is read twice (the second read often hits the 256 MB
+// Infinity Cache for the corpus shapes), the output written once.
+#include <algorithm>
+
+#include "hipo_common.h"
+
+namespace hipo {
+namespace {
+
+constexpr int kUnroll = 4;
+constexpr int kMaxThreads = 1024;
+constexpr float kLog2e = 1.4426950408889634f;
+
+enum { kActNone = 0, kActRelu = 1, kActSilu = 2 };
+
+// act(bf16(((x - mean) * rstd) * gamma + beta)), fp32 ops in the eager order
+// (no contraction).  SiLU is t / (1 + e^-t) with the hardware exp2 and
+// reciprocal; the caller rounds the result to bf16.
+__device__ __forceinline__ float bn_act(float x, float mean, float rstd, float g, float b,
+                                        int act) {
+  float y = __fmul_rn(__fsub_rn(x, mean), rstd);
+  y = round_bf16(__fadd_rn(__fmul_rn(y, g), b));
+  if (act == kActRelu) {
+    y = y < 0.f ? 0.f : y;
+  } else if (act == kActSilu) {
+    y = y * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-y * kLog2e));
+  }
+  return y;
+}
+
+// Chan's pairwise merge of (count, mean, M2) partials: (n, mean, m2) <-
+// (n, mean, m2) + (nb, meanb, m2b).
+template <typename T>
+__device__ __forceinline__ void chan_merge(T& n, T& mean, T& m2, T nb, T meanb, T m2b) {
+  if (nb == T(0)) return;
+  const T nn = n + nb;
+  const T d = meanb - mean;
+  const T f = nb / nn;
+  mean = mean + d * f;
+  m2 = m2 + m2b + d * d * n * f;
+  n = nn;
+}
+
+__device__ __forceinline__ void unpack8(const u32x4_t v, float (&f)[8]) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    f[2 * d] = bf16lo(v[d]);
+    f[2 * d + 1] = bf16hi(v[d]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Channels-last: x is [M, C] rows (M = N*H*W), G = C / 8 groups of 16 bytes.
+// A workgroup of T threads (T a multiple of G) covers T / G whole rows per
+// access instruction; thread t owns group t % G.
+// ---------------------------------------------------------------------------
+
+// Workgroup s reduces rows [s*L, min(M, (s+1)*L)): sums of (x - shift) and
+// (x - shift)^2 per channel, shift = the slice's first row, added over the
+// T / G rows of an instruction in a fixed order through LDS, then turned into
+// (mean, M2) for the slice.
+__global__ __launch_bounds__(kMaxThreads) void bn_nhwc_partial(
+    const uint16_t* __restrict__ x, float2* __restrict__ part, int64_t M, int64_t C, int G,
+    int64_t L) {
+  extern __shared__ float lds[];  // [T][8]
+  const int T = blockDim.x;
+  const int t = threadIdx.x;
+  const int g = t % G;
+  const int r = t / G;
+  const int R = T / G;
+  const int64_t s = blockIdx.x;
+  const int64_t p0 = s * L;
+  const int64_t p1 = std::min<int64_t>(M, p0 + L);
+  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x) + g;
+  const int64_t G64 = G;
+
+  const u32x4_t shv = xv[p0 * G64];
+  float shift[8];
+  unpack8(shv, shift);
+  float s1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float s2[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t p = p0 + r; p < p1; p += static_cast<int64_t>(R) * kUnroll) {
+    u32x4_t v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      // Rows past the slice re-read its first row and count as the shift
+      // (a zero deviation).
+      const int64_t pu = p + static_cast<int64_t>(u) * R;
+      v[u] = xv[(pu < p1 ? pu : p0) * G64];
+      if (pu >= p1) v[u] = shv;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      float f[8];
+      unpack8(v[u], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = f[e] - shift[e];
+        s1[e] += d;
+        s2[e] = __builtin_fmaf(d, d, s2[e]);
+      }
+    }
+  }
+  if (R > 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lds[t * 8 + e] = s1[e];
+    __syncthreads();
+    if (t < G) {
+      for (int k = 1; k < R; ++k) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s1[e] += lds[(k * G + t) * 8 + e];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lds[t * 8 + e] = s2[e];
+    __syncthreads();
+    if (t < G) {
+      for (int k = 1; k < R; ++k) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s2[e] += lds[(k * G + t) * 8 + e];
+      }
+    }
+  }
+  if (t >= G) return;
+  const float n = static_cast<float>(p1 - p0);
+  float2* dst = part + s * C + 8 * g;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float d = s1[e] / n;
+    dst[e] = make_float2(shift[e] + d, fmaxf(s2[e] - s1[e] * d, 0.f));
+  }
+}
+
+// Output row o = (n, ho, wo) of the padded [N, Ho, Wo, C] tensor: the
+// normalised, activated x row (n, ho, wo) when ho < H and wo < W, else zeros.
+// Workgroup b writes rows [b*R*kUnroll, (b+1)*R*kUnroll).
+__global__ __launch_bounds__(kMaxThreads) void bn_nhwc_apply_pad(
+    const uint16_t* __restrict__ x, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ gamma,
+    const float* __restrict__ beta, uint16_t* __restrict__ out, uint32_t rows_out, uint32_t H,
+    uint32_t W, uint32_t Ho, uint32_t Wo, int G, int act) {
+  const int T = blockDim.x;
+  const int t = threadIdx.x;
+  const int g = t % G;
+  const int r = t / G;
+  const int R = T / G;
+  float m[8], rs[8], ga[8], be[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    m[e] = mean[8 * g + e];
+    rs[e] = rstd[8 * g + e];
+    ga[e] = gamma[8 * g + e];
+    be[e] = beta[8 * g + e];
+  }
+  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x) + g;
+  u32x4_t* ov = reinterpret_cast<u32x4_t*>(out) + g;
+  const uint32_t o0 = blockIdx.x * static_cast<uint32_t>(R * kUnroll) + r;
+  const int64_t G64 = G;
+  u32x4_t v[kUnroll];
+  bool inside[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t o = o0 + static_cast<uint32_t>(u * R);
+    const uint32_t img = o / (Ho * Wo);
+    const uint32_t rem = o - img * (Ho * Wo);
+    const uint32_t ho = rem / Wo;
+    const uint32_t wo = rem - ho * Wo;
+    inside[u] = o < rows_out && ho < H && wo < W;
+    // Padding and rows past the end read row 0 (in bounds) and store zeros.
+    const int64_t src = inside[u] ? (static_cast<int64_t>(img) * H + ho) * W + wo : 0;
+    v[u] = __builtin_nontemporal_load(xv + src * G64);
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t o = o0 + static_cast<uint32_t>(u * R);
+    if (o >= rows_out) continue;
+    float f[8];
+    unpack8(v[u], f);
+    u32x4_t w;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const float a = inside[u] ? bn_act(f[2 * d], m[2 * d], rs[2 * d], ga[2 * d], be[2 * d], act) : 0.f;
+      const float b = inside[u] ? bn_act(f[2 * d + 1], m[2 * d + 1], rs[2 * d + 1], ga[2 * d + 1],
+                                         be[2 * d + 1], act)
+                                : 0.f;
+      w[d] = pack_bf16x2(a, b);
+    }
+    __builtin_nontemporal_store(w, ov + static_cast<int64_t>(o) * G64);
+  }
+}
+
+// Any C / alignment: one thread per (slice, channel).
+__global__ __launch_bounds__(256) void bn_nhwc_partial_scalar(
+    const uint16_t* __restrict__ x, float2* __restrict__ part, int64_t M, int64_t C, int64_t L) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  const int64_t s = blockIdx.y;
+  const int64_t p0 = s * L;
+  const int64_t p1 = std::min<int64_t>(M, p0 + L);
+  const float shift = bf16_to_f32(x[p0 * C + c]);
+  float s1 = 0.f, s2 = 0.f;
+  for (int64_t p = p0; p < p1; ++p) {
+    const float d = bf16_to_f32(x[p * C + c]) - shift;
+    s1 += d;
+    s2 = __builtin_fmaf(d, d, s2);
+  }
+  const float n = static_cast<float>(p1 - p0);
+  const float d = s1 / n;
+  part[s * C + c] = make_float2(shift + d, fmaxf(s2 - s1 * d, 0.f));
+}
+
+__global__ __launch_bounds__(256) void bn_nhwc_apply_pad_scalar(
+    const uint16_t* __restrict__ x, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ gamma,
+    const float* __restrict__ beta, uint16_t* __restrict__ out, int64_t total, int64_t H,
+    int64_t W, int64_t Ho, int64_t Wo, int64_t C, int act) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t c = i % C;
+  const int64_t o = i / C;
+  const int64_t img = o / (Ho * Wo);
+  const int64_t rem = o - img * (Ho * Wo);
+  const int64_t ho = rem / Wo;
+  const int64_t wo = rem - ho * Wo;
+  float y = 0.f;
+  if (ho < H && wo < W) {
+    const float xv = bf16_to_f32(x[((img * H + ho) * W + wo) * C + c]);
+    y = bn_act(xv, mean[c], rstd[c], gamma[c], beta[c], act);
+  }
+  out[i] = static_cast<uint16_t>(pack_bf16x2(y, 0.f) & 0xffffu);
+}
+
+// ---------------------------------------------------------------------------
+// NCHW with a small spatial extent: a workgroup of kNchwImages waves covers
+// a block of 64 channels (lane = channel) of kNchwImages consecutive images
+// (wave = image).  When the slab of an (image, channel block) is 16-byte
+// aligned and fits (STAGED), each wave copies it to LDS with 16-byte loads
+// and the lanes read their channel's HW values from there; otherwise the
+// lanes read them from memory directly.
+// ---------------------------------------------------------------------------
+constexpr int kNchwImages = 4;
+constexpr int kNchwChannels = 64;
+constexpr int64_t kNchwMaxStagedHw = 92;  // LDS: 4 x 64 x 92 x 2 B + 2 KiB < 48 KiB
+
+template <bool STAGED, bool LAST_USE>
+__device__ __forceinline__ const uint16_t* nchw_stage(const uint16_t* __restrict__ x,
+                                                      uint16_t* lds_wave, int64_t img,
+                                                      int64_t C, int64_t c0, int64_t HW,
+                                                      bool img_valid, int lane) {
+  const uint16_t* seg = x + (img * C + c0) * HW;
+  if constexpr (STAGED) {
+    const int64_t len = std::min<int64_t>(kNchwChannels, C - c0) * HW;  // multiple of 8
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(seg);
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(lds_wave);
+    if (img_valid) {
+      for (int64_t i = lane; i < len / 8; i += kWave)
+        dst[i] = LAST_USE ? __builtin_nontemporal_load(src + i) : src[i];
+    }
+    __syncthreads();
+    return lds_wave;
+  } else {
+    return seg;
+  }
+}
+
+// MODE 0: per (slice of kNchwImages images, channel) partial (mean, M2),
+//         exact two-pass statistics of each (image, channel) segment merged
+//         over the images in order.
+// MODE 1: out[n, c] = bf16(sum_hw act(bn(x[n, c, hw])) / HW).
+template <int MODE, bool STAGED>
+__global__ __launch_bounds__(kNchwImages * kWave) void bn_nchw_small_hw(
+    const uint16_t* __restrict__ x, float2* __restrict__ part, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ gamma,
+    const float* __restrict__ beta, uint16_t* __restrict__ out, int64_t N, int64_t C,
+    int64_t HW, int act) {
+  extern __shared__ uint16_t slab[];  // [kNchwImages][64 * HW] when STAGED
+  __shared__ float2 stats[kNchwImages][kNchwChannels];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x >> 6;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kNchwChannels;
+  const int64_t img = static_cast<int64_t>(blockIdx.y) * kNchwImages + w;
+  const int64_t c = c0 + lane;
+  const bool img_valid = img < N;
+  const bool valid = img_valid && c < C;
+  const uint16_t* base = nchw_stage<STAGED, MODE == 1>(x, slab + w * kNchwChannels * HW,
+                                            img_valid ? img : 0, C, c0, HW, img_valid, lane);
+  const uint16_t* seg = base + static_cast<int64_t>(lane) * HW;
+  if constexpr (MODE == 0) {
+    float mu = 0.f, m2 = 0.f;
+    if (valid) {
+      float sum = 0.f;
+      for (int64_t j = 0; j < HW; ++j) sum += bf16_to_f32(seg[j]);
+      mu = sum / static_cast<float>(HW);
+      for (int64_t j = 0; j < HW; ++j) {
+        const float d = bf16_to_f32(seg[j]) - mu;
+        m2 = __builtin_fmaf(d, d, m2);
+      }
+    }
+    stats[w][lane] = make_float2(mu, m2);
+    __syncthreads();
+    if (w == 0 && c < C) {
+      float n = 0.f, mm = 0.f, mq = 0.f;
+      for (int k = 0; k < kNchwImages; ++k) {
+        if (static_cast<int64_t>(blockIdx.y) * kNchwImages + k >= N) break;
+        chan_merge(n, mm, mq, static_cast<float>(HW), stats[k][lane].x, stats[k][lane].y);
+      }
+      part[static_cast<int64_t>(blockIdx.y) * C + c] = make_float2(mm, mq);
+    }
+  } else {
+    if (!valid) return;
+    const float mc = mean[c], rc = rstd[c], gc = gamma[c], bc = beta[c];
+    float sum = 0.f;
+    for (int64_t j = 0; j < HW; ++j) sum += bn_act(bf16_to_f32(seg[j]), mc, rc, gc, bc, act);
+    out[img * C + c] = static_cast<uint16_t>(pack_bf16x2(sum / static_cast<float>(HW), 0.f) & 0xffffu);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per-channel merge.  Slice s holds count (min(units, (s+1)*per) - s*per) *
+// mult values of the channel.  Lane l merges slices l, l + 64, ... in order
+// (fp64), then a butterfly over the lanes merges (lower lane, upper lane) at
+// each step, so every lane holds the same, order-fixed result.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kWave) void bn_finalize(
+    const float2* __restrict__ part, int64_t slices, int64_t C, int64_t units, int64_t per,
+    int64_t mult, float* __restrict__ running_mean, float* __restrict__ running_var,
+    float* __restrict__ save_mean, float* __restrict__ save_rstd, float momentum, float eps,
+    float var_scale) {
+  const int64_t c = blockIdx.x;
+  const int lane = threadIdx.x;
+  double n = 0.0, mu = 0.0, m2 = 0.0;
+  for (int64_t s = lane; s < slices; s += kWave) {
+    const int64_t cnt = (std::min<int64_t>(units, (s + 1) * per) - s * per) * mult;
+    const float2 p = part[s * C + c];
+    chan_merge(n, mu, m2, static_cast<double>(cnt), static_cast<double>(p.x),
+               static_cast<double>(p.y));
+  }
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const double n2 = __shfl_xor(n, off);
+    const double mu2 = __shfl_xor(mu, off);
+    const double m22 = __shfl_xor(m2, off);
+    const bool upper = (lane & off) != 0;
+    double an = upper ? n2 : n, amu = upper ? mu2 : mu, am2 = upper ? m22 : m2;
+    chan_merge(an, amu, am2, upper ? n : n2, upper ? mu : mu2, upper ? m2 : m22);
+    n = an;
+    mu = amu;
+    m2 = am2;
+  }
+  if (lane != 0) return;
+  const float mean_f = static_cast<float>(mu);
+  const float var_f = static_cast<float>(m2 / n);
+  save_mean[c] = mean_f;
+  save_rstd[c] = 1.0f / __builtin_sqrtf(__fadd_rn(var_f, eps));
+  const float keep = 1.0f - momentum;
+  running_mean[c] = __fadd_rn(__fmul_rn(mean_f, momentum), __fmul_rn(running_mean[c], keep));
+  running_var[c] = __fadd_rn(__fmul_rn(__fmul_rn(var_f, var_scale), momentum),
+                             __fmul_rn(running_var[c], keep));
+}
+
+int64_t gcd64(int64_t a, int64_t b) {
+  while (b) {
+    const int64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+// Channels-last plan: threads per workgroup (0: scalar kernels), rows per
+// slice and slice count.  Slices of at least 256 rows, at most about 1024
+// of them; the slicing does not depend on the kernel choice, so the
+// workspace size is a function of the shape alone.  The workspace traffic
+// (8 B per channel per slice) stays under 4 % of x for the corpus shapes.
+struct NhwcPlan {
+  int threads = 0;
+  int64_t slice_len = 0;
+  int64_t slices = 0;
+};
+
+constexpr int64_t kNhwcSliceStep = 256;
+
+NhwcPlan nhwc_plan(int64_t M, int64_t C, bool vec_ok) {
+  NhwcPlan plan;
+  if (M <= 0 || C <= 0) return plan;
+  if (vec_ok && C % 8 == 0 && C / 8 <= kMaxThreads) {
+    const int64_t G = C / 8;
+    const int64_t lcm = G / gcd64(G, kWave) * kWave;
+    plan.threads = static_cast<int>(lcm <= kMaxThreads ? lcm * std::max<int64_t>(1, 512 / lcm) : G);
+  }
+  const int64_t want = (M + 1023) / 1024;
+  plan.slice_len = (want + kNhwcSliceStep - 1) / kNhwcSliceStep * kNhwcSliceStep;
+  plan.slices = (M + plan.slice_len - 1) / plan.slice_len;
+  return plan;
+}
+
+int64_t nchw_slices(int64_t n) { return (n + kNchwImages - 1) / kNchwImages; }
+
+}  // namespace
+}  // namespace hipo
+
+extern "C" size_t hipo_batchnorm_nhwc_workspace_bytes(int64_t n, int64_t h, int64_t w,
+                                                     int64_t c) {
+  if (n <= 0 || h <= 0 || w <= 0 || c <= 0) return 0;
+  const hipo::NhwcPlan plan = hipo::nhwc_plan(n * h * w, c, true);
+  return static_cast<size_t>(plan.slices * c) * sizeof(float2);
+}
+
+extern "C" int hipo_batchnorm_nhwc_act_pad_bf16(
+    const uint16_t* x, const float* gamma, const float* beta, float* running_mean,
+    float* running_var, float* save_mean, float* save_rstd, uint16_t* out, int64_t n, int64_t h,
+    int64_t w, int64_t c, int64_t pad_bottom, int64_t pad_right, float momentum, float eps,
+    float var_scale, int act, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  const char* what = "batchnorm_nhwc_act_pad_bf16";
+  HIPO_REQUIRE(n >= 0 && h >= 0 && w >= 0 && c >= 0 && pad_bottom >= 0 && pad_right >= 0,
+               "%s: negative size", what);
+  HIPO_REQUIRE(act >= kActNone && act <= kActSilu, "%s: act must be 0, 1 or 2", what);
+  if (c == 0) return 0;
+  HIPO_REQUIRE(n > 0 && h > 0 && w > 0, "%s: empty reduction (n * h * w == 0)", what);
+  HIPO_REQUIRE(x && gamma && beta && running_mean && running_var && save_mean && save_rstd && out,
+               "%s: null pointer", what);
+  const int64_t M = n * h * w;
+  const int64_t Ho = h + pad_bottom, Wo = w + pad_right;
+  const int64_t rows_out = n * Ho * Wo;
+  const bool vec_ok = aligned16(x) && aligned16(out) && rows_out < (int64_t{1} << 31) &&
+                      M < (int64_t{1} << 31);
+  const NhwcPlan plan = nhwc_plan(M, c, vec_ok);
+  const size_t need = static_cast<size_t>(plan.slices * c) * sizeof(float2);
+  HIPO_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace),
+               "%s: workspace of %zu bytes (16-byte aligned), need %zu", what, workspace_bytes,
+               need);
+  HIPO_REQUIRE(plan.slices <= 65535 || plan.threads > 0, "%s: too many rows", what);
+  float2* part = static_cast<float2*>(workspace);
+  if (plan.threads > 0) {
+    const int G = static_cast<int>(c / 8);
+    const int R = plan.threads / G;
+    const size_t lds = R > 1 ? static_cast<size_t>(plan.threads) * 8 * sizeof(float) : 0;
+    bn_nhwc_partial<<<dim3(static_cast<unsigned>(plan.slices)), dim3(plan.threads), lds,
+                      stream>>>(x, part, M, c, G, plan.slice_len);
+  } else {
+    bn_nhwc_partial_scalar<<<dim3(static_cast<unsigned>((c + 255) / 256),
+                                  static_cast<unsigned>(plan.slices)),
+                             dim3(256), 0, stream>>>(x, part, M, c, plan.slice_len);
+  }
+  bn_finalize<<<dim3(static_cast<unsigned>(c)), dim3(kWave), 0, stream>>>(
+      part, plan.slices, c, M, plan.slice_len, 1, running_mean, running_var, save_mean,
+      save_rstd, momentum, eps, var_scale);
+  if (plan.threads > 0) {
+    const int G = static_cast<int>(c / 8);
+    const int64_t rows_per_block = static_cast<int64_t>(plan.threads / G) * kUnroll;
+    const int64_t blocks = (rows_out + rows_per_block - 1) / rows_per_block;
+    bn_nhwc_apply_pad<<<dim3(static_cast<unsigned>(blocks)), dim3(plan.threads), 0, stream>>>(
+        x, save_mean, save_rstd, gamma, beta, out, static_cast<uint32_t>(rows_out),
+        static_cast<uint32_t>(h), static_cast<uint32_t>(w), static_cast<uint32_t>(Ho),
+        static_cast<uint32_t>(Wo), G, act);
+  } else {
+    const int64_t total = rows_out * c;
+    HIPO_REQUIRE((total + 255) / 256 <= 0x7fffffff, "%s: too large", what);
+    bn_nhwc_apply_pad_scalar<<<dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                               stream>>>(x, save_mean, save_rstd, gamma, beta, out, total, h, w,
+                                         Ho, Wo, c, act);
+  }
+  return check_launch(what);
+}
+
+extern "C" size_t hipo_batchnorm_nchw_mean_workspace_bytes(int64_t n, int64_t c, int64_t hw) {
+  if (n <= 0 || c <= 0 || hw <= 0) return 0;
+  return static_cast<size_t>(hipo::nchw_slices(n) * c) * sizeof(float2);
+}
+
+extern "C" int hipo_batchnorm_nchw_act_mean_bf16(
+    const uint16_t* x, const float* gamma, const float* beta, float* running_mean,
+    float* running_var, float* save_mean, float* save_rstd, uint16_t* out, int64_t n, int64_t c,
+    int64_t hw, float momentum, float eps, float var_scale, int act, void* workspace,
+    size_t workspace_bytes, hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  const char* what = "batchnorm_nchw_act_mean_bf16";
+  HIPO_REQUIRE(n >= 0 && c >= 0 && hw >= 0, "%s: negative size", what);
+  HIPO_REQUIRE(act >= kActNone && act <= kActSilu, "%s: act must be 0, 1 or 2", what);
+  if (c == 0) return 0;
+  HIPO_REQUIRE(n > 0 && hw > 0, "%s: empty reduction (n * hw == 0)", what);
+  HIPO_REQUIRE(x && gamma && beta && running_mean && running_var && save_mean && save_rstd && out,
+               "%s: null pointer", what);
+  const int64_t slices = nchw_slices(n);
+  const size_t need = static_cast<size_t>(slices * c) * sizeof(float2);
+  HIPO_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace),
+               "%s: workspace of %zu bytes (16-byte aligned), need %zu", what, workspace_bytes,
+               need);
+  HIPO_REQUIRE(slices <= 65535, "%s: too many images", what);
+  float2* part = static_cast<float2*>(workspace);
+  const bool staged = c % 8 == 0 && hw <= kNchwMaxStagedHw && aligned16(x);
+  const dim3 grid(static_cast<unsigned>((c + kNchwChannels - 1) / kNchwChannels),
+                  static_cast<unsigned>(slices));
+  const dim3 block(kNchwImages * kWave);
+  const size_t lds = staged ? static_cast<size_t>(kNchwImages * kNchwChannels * hw) * 2 : 0;
+  if (staged) {
+    bn_nchw_small_hw<0, true><<<grid, block, lds, stream>>>(x, part, nullptr, nullptr, nullptr,
+                                                            nullptr, nullptr, n, c, hw, act);
+  } else {
+    bn_nchw_small_hw<0, false><<<grid, block, 0, stream>>>(x, part, nullptr, nullptr, nullptr,
+                                                           nullptr, nullptr, n, c, hw, act);
+  }
+  bn_finalize<<<dim3(static_cast<unsigned>(c)), dim3(kWave), 0, stream>>>(
+      part, slices, c, n, kNchwImages, hw, running_mean, running_var, save_mean, save_rstd,
+      momentum, eps, var_scale);
+  if (staged) {
+    bn_nchw_small_hw<1, true><<<grid, block, lds, stream>>>(x, nullptr, save_mean, save_rstd,
+                                                            gamma, beta, out, n, c, hw, act);
+  } else {
+    bn_nchw_small_hw<1, false><<<grid, block, 0, stream>>>(x, nullptr, save_mean, save_rstd,
+                                                           gamma, beta, out, n, c, hw, act);
+  }
+  return check_launch(what);
+}

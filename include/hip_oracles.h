@@ -173,6 +173,64 @@ int hipo_spatial_mean_nhwc_bf16(const uint16_t* x, uint16_t* out, int64_t n,
                                 size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * BatchNorm training forward on bf16 activations, fp32 statistics, in the
+ * op order of the reference's bf16 BN graphs:
+ *   mean[c], var[c] = var_mean(fp32(x), dims (0, 2, 3), correction 0)
+ *   save_mean = mean;  save_rstd = 1 / sqrt(var + eps)
+ *   y = act(bf16(((x - mean) * save_rstd) * gamma + beta))     (fp32 ops)
+ *       act: 0 none, 1 ReLU, 2 SiLU (t / (1 + e^-t), rounded to bf16)
+ *   running_mean = mean * momentum + running_mean * (1 - momentum)
+ *   running_var  = (var * var_scale) * momentum
+ *                  + running_var * (1 - momentum)             (in place)
+ * var_scale is the graph's Bessel constant (N/(N-1) at the shape the graph
+ * was captured at); it is applied as given.  gamma, beta, running_*,
+ * save_* are fp32 [c].  The statistics pass writes (mean, M2) per slice and
+ * channel into `workspace` (16-byte aligned, at least the size the matching
+ * *_workspace_bytes call returns; no initialisation needed); calls that
+ * share a workspace must be ordered.  Deterministic (fixed merge order).
+ */
+
+/* Workspace bytes of hipo_batchnorm_nhwc_act_pad_bf16 (0: empty shape). */
+size_t hipo_batchnorm_nhwc_workspace_bytes(int64_t n, int64_t h, int64_t w, int64_t c);
+
+/*
+ * x is [n, c, h, w] stored channels-last (physical [n, h, w, c]); out is
+ * [n, c, h + pad_bottom, w + pad_right] stored channels-last, y in the
+ * top-left h x w window and zeros in the padding.
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/var_mean_ceb5c315290a/oracle.py:238 (split-K statistics,
+ * then the normalise + SiLU + pad epilogue; eps 1e-3, SiLU, pad 1).
+ */
+int hipo_batchnorm_nhwc_act_pad_bf16(const uint16_t* x, const float* gamma,
+                                     const float* beta, float* running_mean,
+                                     float* running_var, float* save_mean,
+                                     float* save_rstd, uint16_t* out, int64_t n,
+                                     int64_t h, int64_t w, int64_t c,
+                                     int64_t pad_bottom, int64_t pad_right,
+                                     float momentum, float eps, float var_scale,
+                                     int act, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes of hipo_batchnorm_nchw_act_mean_bf16 (0: empty shape). */
+size_t hipo_batchnorm_nchw_mean_workspace_bytes(int64_t n, int64_t c, int64_t hw);
+
+/*
+ * x is contiguous NCHW [n, c, hw]; out[n, c] = bf16(mean over hw of y)
+ * (fp32 sum), a contiguous [n, c] bf16 tensor.
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/var_mean_mean_19ffdb35cc67/oracle.py:167 (one CTA per
+ * channel, then the normalise + ReLU + spatial-mean epilogue; eps 1e-5).
+ */
+int hipo_batchnorm_nchw_act_mean_bf16(const uint16_t* x, const float* gamma,
+                                      const float* beta, float* running_mean,
+                                      float* running_var, float* save_mean,
+                                      float* save_rstd, uint16_t* out, int64_t n,
+                                      int64_t c, int64_t hw, float momentum,
+                                      float eps, float var_scale, int act,
+                                      void* workspace, size_t workspace_bytes,
+                                      hipStream_t stream);
+
+/*
  * Bytes of device workspace hipo_batchnorm_train_fwd_f32 needs for this
  * shape (0 if a size is not positive).
  */

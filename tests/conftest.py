@@ -30,6 +30,8 @@ VARIANT_IDS = [
     "mean_4462ce967d63",
     "amax_sum_20ccc18dda60",
     "var_mean_80e7ff4dee7f",
+    "var_mean_ceb5c315290a",
+    "var_mean_mean_19ffdb35cc67",
 ]
 
 

@@ -58,6 +58,26 @@ def test_abi_version_and_error_string(lib):
                                               1, 0, None), b"workspace"),
     (lambda l: l.hipo_batchnorm_train_fwd_f32(None, 1, 1, 1, 1, 1, 1, 1, 2, 4, 9, 0.1, 1e-5, 1,
                                               1, 1 << 20, None), b"null"),
+    (lambda l: l.hipo_batchnorm_nhwc_act_pad_bf16(*[1] * 8, 2, 4, 4, 8, 1, 1, 0.1, 1e-3, 1.0, 3,
+                                                  16, 1 << 20, None), b"act"),
+    (lambda l: l.hipo_batchnorm_nhwc_act_pad_bf16(*[1] * 8, 2, 4, 4, 8, 1, 1, 0.1, 1e-3, 1.0, 2,
+                                                  16, 8, None), b"workspace"),
+    (lambda l: l.hipo_batchnorm_nhwc_act_pad_bf16(*[1] * 8, 2, 4, 4, 8, 1, 1, 0.1, 1e-3, 1.0, 2,
+                                                  8, 1 << 20, None), b"aligned"),
+    (lambda l: l.hipo_batchnorm_nhwc_act_pad_bf16(None, *[1] * 7, 2, 4, 4, 8, 0, 0, 0.1, 1e-3, 1.0,
+                                                  0, 16, 1 << 20, None), b"null"),
+    (lambda l: l.hipo_batchnorm_nhwc_act_pad_bf16(*[1] * 8, 0, 4, 4, 8, 0, 0, 0.1, 1e-3, 1.0, 0,
+                                                  16, 1 << 20, None), b"empty reduction"),
+    (lambda l: l.hipo_batchnorm_nhwc_act_pad_bf16(*[1] * 8, 2, 4, 4, 8, -1, 0, 0.1, 1e-3, 1.0, 0,
+                                                  16, 1 << 20, None), b"negative"),
+    (lambda l: l.hipo_batchnorm_nchw_act_mean_bf16(*[1] * 8, 2, 8, 49, 0.1, 1e-5, 1.0, 5,
+                                                   16, 1 << 20, None), b"act"),
+    (lambda l: l.hipo_batchnorm_nchw_act_mean_bf16(*[1] * 8, 5, 8, 49, 0.1, 1e-5, 1.0, 1,
+                                                   16, 64, None), b"workspace"),
+    (lambda l: l.hipo_batchnorm_nchw_act_mean_bf16(*[1] * 7, None, 5, 8, 49, 0.1, 1e-5, 1.0, 1,
+                                                   16, 1 << 20, None), b"null"),
+    (lambda l: l.hipo_batchnorm_nchw_act_mean_bf16(*[1] * 8, 5, 8, 0, 0.1, 1e-5, 1.0, 1,
+                                                   16, 1 << 20, None), b"empty reduction"),
 ])
 def test_argument_errors_before_launch(lib, call, msg):
     assert call(lib) == HIPO_EINVAL
@@ -71,6 +91,10 @@ def test_empty_inputs_are_no_ops(lib):
     assert lib.hipo_scaled_bias_softmax_bf16(None, None, None, 0, 4, 8, 8, 0, 1, 1.0, None) == 0
     assert lib.hipo_rmsnorm_ex_bf16(None, None, None, None, None, 0, 8, 1e-5, 1.0, 0, None) == 0
     assert lib.hipo_spatial_mean_nhwc_bf16(None, None, 0, 64, 8, None, 0, None) == 0
+    assert lib.hipo_batchnorm_nhwc_act_pad_bf16(*[None] * 8, 2, 4, 4, 0, 1, 1, 0.1, 1e-3, 1.0, 2,
+                                                None, 0, None) == 0
+    assert lib.hipo_batchnorm_nchw_act_mean_bf16(*[None] * 8, 2, 0, 49, 0.1, 1e-5, 1.0, 1,
+                                                 None, 0, None) == 0
     assert lib.hipo_last_error() == b""
 
 
@@ -82,6 +106,19 @@ def test_spatial_mean_workspace_bytes(lib):
     assert lib.hipo_spatial_mean_workspace_bytes(128, 4096, 256) == 128 * 2 * 256 * 4
     # C not a multiple of 8: the scalar kernel, no workspace
     assert lib.hipo_spatial_mean_workspace_bytes(4, 4096, 100) == 0
+
+
+def test_bf16_batchnorm_workspace_bytes(lib):
+    """(mean, M2) fp32 pairs per slice and channel.  Channels-last: slices of
+    a multiple of 256 rows, at most about 1024 of them; NCHW: one slice per 4
+    images."""
+    assert lib.hipo_batchnorm_nhwc_workspace_bytes(128, 28, 28, 240) == 392 * 240 * 8
+    assert lib.hipo_batchnorm_nhwc_workspace_bytes(128, 112, 112, 96) == 896 * 96 * 8
+    assert lib.hipo_batchnorm_nhwc_workspace_bytes(1, 3, 3, 20) == 1 * 20 * 8
+    assert lib.hipo_batchnorm_nhwc_workspace_bytes(0, 3, 3, 20) == 0
+    assert lib.hipo_batchnorm_nchw_mean_workspace_bytes(128, 1024, 49) == 32 * 1024 * 8
+    assert lib.hipo_batchnorm_nchw_mean_workspace_bytes(5, 8, 9) == 2 * 8 * 8
+    assert lib.hipo_batchnorm_nchw_mean_workspace_bytes(5, 8, 0) == 0
 
 
 def test_batchnorm_workspace_bytes(lib):

@@ -479,6 +479,114 @@ def test_spatial_mean_layouts(rocm_device):
                        torch.full((2, 512, 1, 1), 1.25, dtype=bf))
 
 
+def _bn_bf16_ref(x, gamma, beta, rm, rv, eps, momentum, var_scale, act):
+    """CPU eager-order reference of the bf16 BatchNorm kernels: (mean, rstd,
+    y before the epilogue's layout step, running_mean, running_var)."""
+    var, mean = torch.var_mean(x.float(), [0, 2, 3], correction=0, keepdim=True)
+    rstd = torch.rsqrt(var + eps)
+    t = (((x.float() - mean) * rstd) * gamma.view(-1, 1, 1) + beta.view(-1, 1, 1)).to(torch.bfloat16)
+    if act == "relu":
+        t = torch.relu(t)
+    elif act == "silu":
+        tf = t.float()
+        t = (tf / (1 + torch.exp(-tf))).to(torch.bfloat16)
+    new_rm = mean.flatten() * momentum + rm * (1 - momentum)
+    new_rv = var.flatten() * var_scale * momentum + rv * (1 - momentum)
+    return mean, rstd, t, new_rm, new_rv
+
+
+def _bn_bf16_inputs(n, c, h, w, seed, channels_last):
+    g = torch.Generator().manual_seed(seed)
+    x = (2 * torch.randn(n, c, h, w, generator=g) + 0.5).to(torch.bfloat16)
+    if channels_last:
+        x = x.contiguous(memory_format=torch.channels_last)
+    params = [torch.randn(c, generator=g), 0.1 * torch.randn(c, generator=g),
+              torch.randn(c, generator=g), torch.rand(c, generator=g) + 0.5]
+    return x, params
+
+
+BN_NHWC_CASES = [  # n, c, h, w, pad_bottom, pad_right, act
+    (3, 240, 28, 28, 1, 1, "silu"), (2, 96, 9, 9, 0, 0, "relu"), (1, 8, 3, 3, 2, 3, None),
+    (2, 20, 5, 5, 1, 1, "silu"), (4, 8192, 2, 2, 1, 0, "relu"), (2, 8200, 2, 2, 0, 1, None),
+    (16, 64, 40, 40, 1, 1, "silu"), (5, 24, 17, 3, 0, 2, "silu"),
+]
+
+
+@pytest.mark.parametrize("n,c,h,w,pb,pr,act", BN_NHWC_CASES,
+                         ids=[f"{s[0]}x{s[1]}x{s[2]}x{s[3]}" for s in BN_NHWC_CASES])
+def test_batchnorm_nhwc_act_pad(n, c, h, w, pb, pr, act, rocm_device):
+    import hip_oracles
+    print(f"[bn-nhwc] {n}x{c}x{h}x{w} pad {pb},{pr} act {act}", flush=True)
+    x, (gm, bt, rm, rv) = _bn_bf16_inputs(n, c, h, w, n * c + h, True)
+    d = [t.to(rocm_device) for t in (x, gm, bt, rm, rv)]
+    mean, rstd, out = hip_oracles.batchnorm_nhwc_act_pad(
+        d[0], d[1], d[2], d[3], d[4], momentum=0.1, eps=1e-3, var_scale=1.25, act=act,
+        pad_bottom=pb, pad_right=pr)
+    wm, wr, wy, wrm, wrv = _bn_bf16_ref(x, gm, bt, rm, rv, 1e-3, 0.1, 1.25, act)
+    assert out.shape == (n, c, h + pb, w + pr) and out.is_contiguous(memory_format=torch.channels_last)
+    assert_close(mean, wm, F32_TOL, "save_mean")
+    assert_close(rstd, wr, F32_TOL, "save_rstd")
+    assert_close(d[3], wrm, F32_TOL, "running_mean")
+    assert_close(d[4], wrv, F32_TOL, "running_var")
+    got = out.cpu()
+    assert_close(got[:, :, :h, :w], wy, BF16_TOL, "y")
+    assert (got[:, :, h:, :] == 0).all() and (got[:, :, :, w:] == 0).all(), "padding must be zeros"
+
+
+BN_NCHW_CASES = [  # n, c, h, w, act
+    (5, 72, 7, 7, "relu"), (3, 20, 7, 7, "relu"), (4, 16, 10, 10, "silu"), (2, 64, 1, 1, None),
+    (9, 128, 3, 5, "relu"), (8, 1024, 7, 7, "relu"),
+]
+
+
+@pytest.mark.parametrize("n,c,h,w,act", BN_NCHW_CASES,
+                         ids=[f"{s[0]}x{s[1]}x{s[2]}x{s[3]}" for s in BN_NCHW_CASES])
+def test_batchnorm_nchw_act_mean(n, c, h, w, act, rocm_device):
+    import hip_oracles
+    print(f"[bn-nchw] {n}x{c}x{h}x{w} act {act}", flush=True)
+    x, (gm, bt, rm, rv) = _bn_bf16_inputs(n, c, h, w, n * c + h, False)
+    d = [t.to(rocm_device) for t in (x, gm, bt, rm, rv)]
+    mean, rstd, out = hip_oracles.batchnorm_nchw_act_mean(
+        d[0], d[1], d[2], d[3], d[4], momentum=0.1, eps=1e-5, var_scale=1.5, act=act)
+    wm, wr, wy, wrm, wrv = _bn_bf16_ref(x, gm, bt, rm, rv, 1e-5, 0.1, 1.5, act)
+    assert_close(mean, wm, F32_TOL, "save_mean")
+    assert_close(rstd, wr, F32_TOL * max(1.0, float(wr.abs().max())), "save_rstd")
+    assert_close(d[3], wrm, F32_TOL, "running_mean")
+    assert_close(d[4], wrv, F32_TOL, "running_var")
+    assert out.shape == (n, c) and out.dtype == torch.bfloat16
+    assert_close(out, wy.mean((2, 3)), BF16_TOL, "spatial mean")
+
+
+def test_batchnorm_bf16_closed_forms(rocm_device):
+    """A constant channel: mean = the constant, var = 0, rstd = 1/sqrt(eps),
+    y = act(bf16(beta)); running_var decays by 1 - momentum."""
+    import hip_oracles
+    bf = torch.bfloat16
+    c = 16
+    x = torch.full((4, c, 6, 6), 1.5, dtype=bf)
+    beta = torch.linspace(-2, 2, c)
+    for layout in ("nhwc", "nchw"):
+        rm, rv = torch.zeros(c), torch.ones(c)
+        d = [t.to(rocm_device) for t in (torch.ones(c), beta, rm, rv)]
+        if layout == "nhwc":
+            xd = x.contiguous(memory_format=torch.channels_last).to(rocm_device)
+            mean, rstd, out = hip_oracles.batchnorm_nhwc_act_pad(
+                xd, *d, momentum=0.1, eps=1e-3, var_scale=2.0, act="relu", pad_bottom=1, pad_right=1)
+            y = out.cpu()[:, :, :6, :6]
+            eps = 1e-3
+        else:
+            mean, rstd, out = hip_oracles.batchnorm_nchw_act_mean(
+                x.to(rocm_device), *d, momentum=0.1, eps=1e-5, var_scale=2.0, act="relu")
+            y = out.cpu().view(4, c, 1, 1)
+            eps = 1e-5
+        assert torch.equal(mean.cpu().flatten(), torch.full((c,), 1.5)), layout
+        assert_close(rstd, torch.full((1, c, 1, 1), 1 / math.sqrt(eps)), F32_TOL / math.sqrt(eps), layout)
+        want = torch.relu(beta.to(bf)).view(1, c, 1, 1).expand_as(y)
+        assert torch.equal(y, want), layout
+        assert_close(d[2], torch.full((c,), 0.15), F32_TOL, layout + " running_mean")
+        assert_close(d[3], torch.full((c,), 0.9), F32_TOL, layout + " running_var")
+
+
 def test_batchnorm_closed_forms_and_edges(rocm_device):
     import hip_oracles
     import oracle as ref

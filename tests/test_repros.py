@@ -159,3 +159,52 @@ def test_family_repro_contract(rid):
     hashes = {p["shape_hash"] for p in json.loads((CANONICAL / rid / "shapes.json").read_text())["points"]}
     assert {e["point"] for e in entries if e["point"]} == hashes
     assert any(e["shape"] is None and e["hardware"] == "MI355X" for e in entries)
+
+
+def _bn_inputs(shape, memory_format, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(*shape, generator=g) * 2 + 0.5).to(bf).contiguous(memory_format=memory_format)
+    c = shape[1]
+    rm, rv = torch.randn(c, generator=g), torch.rand(c, generator=g) + 0.5
+    gamma, beta = torch.randn(c, generator=g), torch.randn(c, generator=g)
+    return x, rm, rv, gamma, beta
+
+
+def test_bn_silu_pad_family_repro():
+    x, rm, rv, gamma, beta = _bn_inputs((3, 16, 5, 6), torch.channels_last, 10)
+    rm0, rv0 = rm.clone(), rv.clone()
+    mean, rstd, out, rm_out, rv_out = get_repro_instance(CANONICAL / "var_mean_ceb5c315290a")(
+        x, rm, rv, gamma, beta)
+    assert rm_out is rm and rv_out is rv
+    assert out.shape == (3, 16, 6, 7) and out.is_contiguous(memory_format=torch.channels_last)
+    y = F.batch_norm(x.float(), None, None, gamma, beta, training=True, eps=1e-3).to(bf)
+    assert torch.equal(out, F.pad(F.silu(y.float()).to(bf), (0, 1, 0, 1)))
+    var, m = torch.var_mean(x.float(), [0, 2, 3], correction=0)
+    assert mean.shape == rstd.shape == (1, 16, 1, 1)
+    assert torch.allclose(mean.flatten(), m) and torch.allclose(rstd.flatten(), torch.rsqrt(var + 1e-3))
+    # the graph's Bessel constant, not N/(N-1) of this shape
+    assert torch.allclose(rm, m * 0.1 + rm0 * 0.9)
+    assert torch.allclose(rv, var * 1.00000996502277 * 0.1 + rv0 * 0.9)
+
+
+def test_bn_relu_mean_family_repro():
+    x, rm, rv, gamma, beta = _bn_inputs((5, 12, 7, 7), torch.contiguous_format, 11)
+    rm0, rv0 = rm.clone(), rv.clone()
+    mean, rstd, out, rm_out, rv_out = get_repro_instance(CANONICAL / "var_mean_mean_19ffdb35cc67")(
+        x, rm, rv, gamma, beta)
+    assert rm_out is rm and rv_out is rv
+    y = F.batch_norm(x.float(), None, None, gamma, beta, training=True, eps=1e-5).to(bf)
+    want = torch.relu(y).mean((2, 3))
+    assert out.shape == (5, 12) and out.dtype == bf
+    assert torch.equal(out, want)
+    var, m = torch.var_mean(x.float(), [0, 2, 3], correction=0)
+    assert torch.allclose(rm, m * 0.1 + rm0 * 0.9)
+    assert torch.allclose(rv, var * 1.0001594642002871 * 0.1 + rv0 * 0.9)
+
+
+def test_bn_family_repros_compute_in_fp64_for_the_gate():
+    for rid, fmt in (("var_mean_ceb5c315290a", torch.channels_last),
+                     ("var_mean_mean_19ffdb35cc67", torch.contiguous_format)):
+        inp = [t.double() for t in _bn_inputs((2, 8, 4, 4), fmt, 12)]
+        outs = get_repro_instance(CANONICAL / rid).double()(*inp)
+        assert all(o.dtype == torch.float64 for o in outs), rid
