@@ -430,13 +430,14 @@ int64_t gcd64(int64_t a, int64_t b) {
 
 // Channels-last plan: threads per workgroup (0: scalar kernels), rows per
 // slice and slice count.  Slices of a multiple of 512 rows, at most about
-// 1024 of them; the slicing does not depend on the kernel choice, so the
+// 512 of them; the slicing does not depend on the kernel choice, so the
 // workspace size is a function of the shape alone.  The workspace traffic
-// (8 B per channel per slice) stays under 2 % of x for the corpus shapes.
+// (8 B per channel per slice) stays under 1 % of x for the corpus shapes.
 // Measured on MI355X (statistics kernel, [128, 240, 28, 28] / [128, 96,
-// 112, 112]): 512-row slices with 8 non-temporal loads in flight per thread
-// 15.1 / 55-60 us, against 21-27 / 55-64 us for 256-row slices, 4 or 16
-// loads, or cached loads.
+// 112, 112]): 512-row slices, at most 512 of them, 8 non-temporal loads in
+// flight per thread: 15.2 / 49.9 us; at most 1024 / 256 / 128 slices:
+// 61.8 / 53.6 / 84.8 us on the second shape; 256-row slices, 4 or 16 loads,
+// or cached loads: 21-27 / 55-64 us.
 struct NhwcPlan {
   int threads = 0;
   int64_t slice_len = 0;
@@ -444,6 +445,7 @@ struct NhwcPlan {
 };
 
 constexpr int64_t kNhwcSliceStep = 512;
+constexpr int64_t kNhwcMaxSlices = 512;
 
 NhwcPlan nhwc_plan(int64_t M, int64_t C, bool vec_ok) {
   NhwcPlan plan;
@@ -453,7 +455,7 @@ NhwcPlan nhwc_plan(int64_t M, int64_t C, bool vec_ok) {
     const int64_t lcm = G / gcd64(G, kWave) * kWave;
     plan.threads = static_cast<int>(lcm <= kMaxThreads ? lcm * std::max<int64_t>(1, 512 / lcm) : G);
   }
-  const int64_t want = (M + 1023) / 1024;
+  const int64_t want = (M + kNhwcMaxSlices - 1) / kNhwcMaxSlices;
   plan.slice_len = (want + kNhwcSliceStep - 1) / kNhwcSliceStep * kNhwcSliceStep;
   plan.slices = (M + plan.slice_len - 1) / plan.slice_len;
   return plan;

@@ -110,10 +110,10 @@ def test_spatial_mean_workspace_bytes(lib):
 
 def test_bf16_batchnorm_workspace_bytes(lib):
     """(mean, M2) fp32 pairs per slice and channel.  Channels-last: slices of
-    a multiple of 512 rows, at most about 1024 of them; NCHW: one slice per 4
+    a multiple of 512 rows, at most about 512 of them; NCHW: one slice per 4
     images."""
     assert lib.hipo_batchnorm_nhwc_workspace_bytes(128, 28, 28, 240) == 196 * 240 * 8
-    assert lib.hipo_batchnorm_nhwc_workspace_bytes(128, 112, 112, 96) == 784 * 96 * 8
+    assert lib.hipo_batchnorm_nhwc_workspace_bytes(128, 112, 112, 96) == 448 * 96 * 8
     assert lib.hipo_batchnorm_nhwc_workspace_bytes(1, 3, 3, 20) == 1 * 20 * 8
     assert lib.hipo_batchnorm_nhwc_workspace_bytes(0, 3, 3, 20) == 0
     assert lib.hipo_batchnorm_nchw_mean_workspace_bytes(128, 1024, 49) == 32 * 1024 * 8
