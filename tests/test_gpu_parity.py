@@ -709,6 +709,47 @@ def test_graph_capture_replays_match_eager(rocm_device):
                     f"{rid} replay {rep} out{i} differs from eager"
 
 
+def test_family_graph_capture_replays_match_eager(rocm_device):
+    """The corpus-family oracles (their smallest shapes.json point) under
+    hipGraph capture: workspaces come from the capture's memory pool, BN
+    updates running stats in place; every replay equals the eager call."""
+    import math as _m
+    from oracle_harness import _normalize_outputs, resolve_oracle
+    from repro_harness import make_inputs_from_config
+    for rid in VARIANT_IDS:
+        fn, _ = _load(rid)
+        pts = _points(rid)
+
+        def numel(cfg):
+            torch.manual_seed(1)
+            ins = make_inputs_from_config(cfg, device="meta")
+            return sum(_m.prod(t.shape) for t in ins if isinstance(t, torch.Tensor))
+        label, cfg = min(pts.items(), key=lambda kv: numel(kv[1]))
+        print(f"[graph] {rid} {label}", flush=True)
+        torch.manual_seed(1)
+        dev_in = make_inputs_from_config(cfg, device=rocm_device)
+        tensors = [t for t in dev_in if isinstance(t, torch.Tensor)]
+        impl, _ = resolve_oracle(fn, dev_in)
+        snapshot = [t.clone() for t in tensors]
+        eager = [t.clone() for t in _normalize_outputs(impl(dev_in))]
+        for t, s in zip(tensors, snapshot):
+            t.copy_(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            captured = _normalize_outputs(impl(dev_in))
+        for rep in range(3):
+            for t, s in zip(tensors, snapshot):
+                t.copy_(s)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            _ = torch.randn(1000, device=rocm_device).sum().item()  # eager work between
+            for i, (a, e) in enumerate(zip(captured, eager)):
+                assert torch.equal(a, e) or torch.allclose(a.float(), e.float(), atol=0, rtol=0,
+                                                           equal_nan=True), \
+                    f"{rid} replay {rep} out{i} differs from eager"
+
+
 def test_deterministic(rocm_device):
     import hip_oracles
     x = torch.randn(128, 256, 14, 14, device=rocm_device) * 2 + 0.5
