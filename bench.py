@@ -8,7 +8,7 @@ NHWC [128,256,56,56]); a step is one oracle_forward over one batch of
 inputs already resident in HBM.
 
 Steady-state timing: R rotating input sets (together >= 1 GiB, four times
-the 256 MB Infinity Cache) and one output buffer per step slot.  L steps
+the 256 MB Infinity Cache) and one output buffer per step slot.  L ~ 64 steps
 (cycling through the sets) are captured in one hipGraph, so consecutive
 kernels run back to back as in a real pipeline (a separate graph per step
 would add the ~8 us idle gap a ROCm graph launch costs); no step finds its
@@ -124,6 +124,13 @@ def cpu_baseline(rid, cpu_inputs, nbytes, budget_s: float = 10.0) -> dict:
             "us": round(best * 1e6, 1)}
 
 
+# Steps captured per hipGraph (rounded up to a multiple of the input sets):
+# each graph replay leaves the GPU idle for ~8 us on ROCm, so longer graphs
+# amortise it (64 steps: ~0.13 us per step).  Every step keeps its own
+# output buffers: at most ~55 GB of HBM for config 3.
+STEPS_PER_GRAPH = 64
+
+
 def steady_state(rid, steps, warmup):
     """Back-to-back steps over rotating input sets (see module docstring)."""
     import torch
@@ -139,7 +146,7 @@ def steady_state(rid, steps, warmup):
     nbytes = oh.effective_bytes(instance, cpu_inputs)
     in_bytes = sum(t.numel() * t.element_size() for t in cpu_inputs if isinstance(t, torch.Tensor))
     sets = min(16, max(2, math.ceil((1 << 30) / max(in_bytes, 1))))
-    per_graph = sets * max(1, math.ceil(16 / sets))
+    per_graph = sets * max(1, math.ceil(STEPS_PER_GRAPH / sets))
     input_sets = [[t.to(dev) if isinstance(t, torch.Tensor) else t for t in cpu_inputs]
                   for _ in range(sets)]
     impl, info = oh.resolve_oracle(fn, input_sets[0])
