@@ -124,9 +124,10 @@ def cpu_baseline(rid, cpu_inputs, nbytes, budget_s: float = 10.0) -> dict:
             "us": round(best * 1e6, 1)}
 
 
-# Steps captured per hipGraph (rounded up to a multiple of the input sets):
-# each graph replay leaves the GPU idle for ~8 us on ROCm, so longer graphs
-# amortise it (64 steps: ~0.13 us per step).  Every step keeps its own
+# Steps captured per hipGraph (a multiple of the input sets, at most the
+# timed steps): each graph replay leaves the GPU idle for ~8 us on ROCm, so
+# longer graphs amortise it (64 steps: ~0.13 us per step); the timed run's
+# remainder steps are one more graph.  Every captured step keeps its own
 # output buffers: at most ~55 GB of HBM for config 3.
 STEPS_PER_GRAPH = 64
 
@@ -146,7 +147,8 @@ def steady_state(rid, steps, warmup):
     nbytes = oh.effective_bytes(instance, cpu_inputs)
     in_bytes = sum(t.numel() * t.element_size() for t in cpu_inputs if isinstance(t, torch.Tensor))
     sets = min(16, max(2, math.ceil((1 << 30) / max(in_bytes, 1))))
-    per_graph = sets * max(1, math.ceil(STEPS_PER_GRAPH / sets))
+    per_graph = sets * max(1, min(STEPS_PER_GRAPH, steps) // sets)
+    tail_steps = steps % per_graph
     input_sets = [[t.to(dev) if isinstance(t, torch.Tensor) else t for t in cpu_inputs]
                   for _ in range(sets)]
     impl, info = oh.resolve_oracle(fn, input_sets[0])
@@ -160,6 +162,12 @@ def steady_state(rid, steps, warmup):
     with torch.cuda.graph(cycle):
         for k in range(per_graph):
             keep.append(impl(input_sets[k % sets]))
+    tail = None  # the timed run's remainder steps, one graph
+    if tail_steps:
+        tail = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(tail):
+            for k in range(tail_steps):
+                keep.append(impl(input_sets[k % sets]))
     singles = []
     for s in range(sets):
         g = torch.cuda.CUDAGraph()
@@ -172,8 +180,11 @@ def steady_state(rid, steps, warmup):
         full, rem = divmod(n, per_graph)
         for _ in range(full):
             cycle.replay()
-        for k in range(rem):
-            singles[k % sets].replay()
+        if rem and rem == tail_steps:
+            tail.replay()
+        else:
+            for k in range(rem):
+                singles[k % sets].replay()
 
     run(warmup)
     torch.cuda.synchronize()
@@ -198,7 +209,7 @@ def steady_state(rid, steps, warmup):
         "value": round(nbytes / wall_s / 1e9, 1),
         "achieved": round(nbytes / device_s / 1e9, 1),
     }
-    del cycle, singles, keep, input_sets
+    del cycle, tail, singles, keep, input_sets
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return out, cpu_inputs

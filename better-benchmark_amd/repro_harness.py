@@ -39,20 +39,37 @@ def point_label(point: dict) -> str:
     return f"{short}_{shape_hash}" if short else shape_hash
 
 
-def shape_hash_of(entries: list) -> str:
-    """8-hex identity of a point: md5 over each tensor's shape:stride:dtype.
+def _is_contiguous(shape, stride) -> bool:
+    """torch's row-major contiguity: strides of size-1 dims are free, an
+    empty tensor is contiguous."""
+    if any(d == 0 for d in shape):
+        return True
+    expected = 1
+    for d, s in zip(reversed(shape), reversed(stride)):
+        if d != 1 and s != expected:
+            return False
+        expected *= d
+    return True
 
-    Same idea as the reference's capture-time shape hash
-    (capture_hook.py:759-774): sorted per-input descriptors, md5, 8 hex.
-    """
+
+def shape_hash_of(entries: list) -> str:
+    """8-hex identity of a point, the reference's capture-time shape hash
+    (capture_hook.py:759-774 over the placeholder info of :331-336): for every
+    tensor input the string "<shape list>:<stride list>:<torch dtype>", the
+    stride spelled [] when the tensor is contiguous; the strings sorted,
+    JSON-encoded, md5, first 8 hex digits.  Shape-parameter inputs are not
+    part of it.  The reference's corpus points reproduce under this function
+    (tested on every transcribed shapes.json point)."""
     parts = []
-    for i, e in enumerate(entries):
+    for e in entries:
         spec = spec_from_compact(e)
-        if spec["kind"] == "tensor":
-            parts.append(f"{i}:{spec['shape']}:{spec['stride']}:{spec['dtype']}")
-        else:
-            parts.append(f"{i}:{spec['kind']}:{spec.get('dims', spec.get('value'))}")
-    return hashlib.md5("|".join(sorted(parts)).encode()).hexdigest()[:8]
+        if spec["kind"] != "tensor":
+            continue
+        shape = [int(d) for d in spec["shape"]]
+        stride = spec.get("stride")
+        stride = [] if stride is None or _is_contiguous(shape, stride) else [int(s) for s in stride]
+        parts.append(f"{shape}:{stride}:torch.{spec['dtype']}")
+    return hashlib.md5(json.dumps(sorted(parts)).encode()).hexdigest()[:8]
 
 
 def load_shape_configs(repro_file: str, symbol_bindings: dict | None = None) -> dict:
@@ -151,7 +168,9 @@ def make_inputs_from_config(config: dict, *, device=None) -> list:
 
     Tensors are generated on the CPU (global torch RNG) and copied to the
     spec's device, or to `device` when given (e.g. "cpu" for a host run).
-    Shape params become lists, symints ints, scalars their value.
+    On the "meta" device only the layout is built (no values, the RNG is
+    not drawn from).  Shape params become lists, symints ints, scalars their
+    value.
     """
     group_nbytes = config.get("alias_group_nbytes") or []
     groups: dict[int, torch.Tensor] = {}
@@ -171,6 +190,10 @@ def make_inputs_from_config(config: dict, *, device=None) -> list:
         dtype = getattr(torch, spec["dtype"].replace("torch.", ""))
         stride = [int(s) for s in (spec.get("stride") or [])] or None
         dev = _resolve_device(spec.get("device", "cuda"), device)
+        if dev.type == "meta" and spec.get("alias_group") is None:
+            result.append(torch.empty_strided(shape, stride or _contig(shape), dtype=dtype,
+                                              device=dev))
+            continue
         if spec.get("alias_group") is not None:
             g = int(spec["alias_group"])
             if g not in groups:

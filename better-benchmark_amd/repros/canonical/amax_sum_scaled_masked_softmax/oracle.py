@@ -20,7 +20,7 @@ from oracle_harness import oracle_impl  # noqa: E402
 SCALE = 0.125  # the graph constant of repro.py
 
 
-@oracle_impl(hardware="MI355X", point="dec743da", description="masked softmax, rows in registers")
+@oracle_impl(hardware="MI355X", point="134a1d74", description="masked softmax, rows in registers")
 @oracle_impl(hardware="MI355X", description="masked softmax, shape-general")
 def oracle_forward(inputs):
     x, mask = inputs

@@ -15,7 +15,7 @@ import hip_oracles  # noqa: E402
 from oracle_harness import oracle_impl  # noqa: E402
 
 
-@oracle_impl(hardware="MI355X", point="a45be573", description="row mean, waves per row")
+@oracle_impl(hardware="MI355X", point="b84ae979", description="row mean, waves per row")
 @oracle_impl(hardware="MI355X", description="row mean, shape-general")
 def oracle_forward(inputs):
     (x,) = inputs

@@ -18,7 +18,7 @@ from oracle_harness import oracle_impl  # noqa: E402
 EPS = 1e-05  # the graph constant of repro.py
 
 
-@oracle_impl(hardware="MI355X", point="0c98d8d1", description="RMSNorm, rows in registers")
+@oracle_impl(hardware="MI355X", point="0390a437", description="RMSNorm, rows in registers")
 @oracle_impl(hardware="MI355X", description="RMSNorm, shape-general")
 def oracle_forward(inputs):
     x, gamma = inputs

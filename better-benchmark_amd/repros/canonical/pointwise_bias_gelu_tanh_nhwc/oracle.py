@@ -19,7 +19,7 @@ import hip_oracles  # noqa: E402
 from oracle_harness import oracle_impl  # noqa: E402
 
 
-@oracle_impl(hardware="MI355X", point="fa7f85a9", description="bias+gelu NCHW->NHWC, register transpose")
+@oracle_impl(hardware="MI355X", point="8d22dcbf", description="bias+gelu NCHW->NHWC, register transpose")
 @oracle_impl(hardware="MI355X", description="bias+gelu NCHW->NHWC, shape-general")
 def oracle_forward(inputs):
     x, bias = inputs

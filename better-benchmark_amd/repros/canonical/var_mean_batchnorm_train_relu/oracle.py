@@ -23,7 +23,7 @@ MOMENTUM = 0.1  # graph constants of repro.py
 EPS = 1e-05
 
 
-@oracle_impl(hardware="MI355X", point="7b860eea", description="BN train fwd + ReLU, single pass")
+@oracle_impl(hardware="MI355X", point="ce16d05d", description="BN train fwd + ReLU, single pass")
 @oracle_impl(hardware="MI355X", description="BN train fwd + ReLU, shape-general")
 def oracle_forward(inputs):
     x, gamma, beta, running_mean, running_var = inputs

@@ -20,7 +20,7 @@ from oracle_harness import oracle_impl  # noqa: E402
 EPS = 1e-05  # the graph constant of repro.py
 
 
-@oracle_impl(hardware="MI355X", point="bd27ce78", description="residual LN, rows in registers")
+@oracle_impl(hardware="MI355X", point="fe9bbcba", description="residual LN, rows in registers")
 @oracle_impl(hardware="MI355X", description="residual LN, shape-general")
 def oracle_forward(inputs):
     x, residual, gamma, beta = inputs

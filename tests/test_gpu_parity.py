@@ -799,8 +799,8 @@ def test_bench_parallel_oracles_end_to_end(rocm_device, tmp_path):
     assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-2000:]
     timed = json.loads(out.read_text())
     assert "__failures__" not in timed
-    for name, baseline, ragged in (("mean_lastdim_f32", "a45be573", {"1ca01377", "12f6573e"}),
-                                   ("mean_rmsnorm", "0c98d8d1", {"984fcc7b", "5f1f5109"})):
+    for name, baseline, ragged in (("mean_lastdim_f32", "b84ae979", {"752b1fe9", "ca2d844f"}),
+                                   ("mean_rmsnorm", "0390a437", {"2af004bd", "1c70d57a"})):
         entry = timed[name]
         assert set(entry["points_by_shape"]) == {baseline} | ragged
         assert entry["n_points"] == 3
@@ -815,8 +815,8 @@ def test_bench_parallel_oracles_end_to_end(rocm_device, tmp_path):
     assert mga.main(["--all", "--json", "--timings", str(out), "--output",
                      str(report_path)]) == 0
     reports = {r["model_name"]: r for r in json.loads(report_path.read_text())}
-    for model, name, baseline in (("baseline/config1_row_mean", "mean_lastdim_f32", "a45be573"),
-                                  ("baseline/config4b_rmsnorm", "mean_rmsnorm", "0c98d8d1")):
+    for model, name, baseline in (("baseline/config1_row_mean", "mean_lastdim_f32", "b84ae979"),
+                                  ("baseline/config4b_rmsnorm", "mean_rmsnorm", "0390a437")):
         rep = reports[model]
         assert rep["projection_complete"] and rep["matched_occurrences"] == 1
         assert rep["fusible_oracle_us_total"] == timed[name]["points_by_shape"][baseline]["oracle_us"]

@@ -95,14 +95,33 @@ def test_instantiate_point():
         instantiate_point(point, symbols, guards=["s0 > 5"])
 
 
-def test_every_build_repro_has_consistent_shapes_json():
-    from conftest import CANONICAL, REPRO_IDS
-    for rid in REPRO_IDS:
+def test_shape_hash_is_the_capture_time_identity():
+    """Contiguous strides count as "no stride" (torch's rule: size-1 dims
+    are free), layouts differ, shape parameters are not part of it."""
+    plain = [[[4, 1, 8], "bf16"], [[8], "f32"]]
+    assert shape_hash_of(plain) == shape_hash_of([[[4, 1, 8], "bf16", {"st": [8, 8, 1]}], [[8], "f32"]])
+    assert shape_hash_of(plain) == shape_hash_of([[[4, 1, 8], "bf16", {"st": [8, 99, 1]}], [[8], "f32"]])
+    assert shape_hash_of(plain) == shape_hash_of(plain + [["S", [4, 8]]])
+    cl = [[[2, 3, 4, 5], "bf16", {"st": [60, 1, 15, 3]}]]
+    assert shape_hash_of(cl) != shape_hash_of([[[2, 3, 4, 5], "bf16"]])
+    assert shape_hash_of(plain) == shape_hash_of(list(reversed(plain)))  # sorted descriptors
+
+
+def test_every_canonical_dir_has_consistent_shapes_json():
+    """Every point's hash recomputes from its inputs -- for the corpus
+    families this checks the transcription against the reference's own
+    capture-time hashes."""
+    from conftest import CANONICAL, REPRO_IDS, VARIANT_IDS
+    for rid in REPRO_IDS + VARIANT_IDS:
         data = json.loads((CANONICAL / rid / "shapes.json").read_text())
         for p in data["points"]:
             assert p["shape_hash"] == shape_hash_of(p["inputs"]), (rid, p["shape_hash"])
         cfgs = load_shape_configs(str(CANONICAL / rid / "repro.py"))
         assert list(cfgs) == [point_label(p) for p in data["points"]]
-        assert next(iter(cfgs)).startswith("config"), "BASELINE point first"
         meta = json.loads((CANONICAL / rid / "meta.json").read_text())
-        assert meta["pattern_hash"] == rid and meta["origin_ops"]
+        assert meta["origin_ops"]
+        if rid in REPRO_IDS:
+            assert next(iter(cfgs)).startswith("config"), "BASELINE point first"
+            assert meta["pattern_hash"] == rid
+        else:
+            assert rid.endswith("_" + meta["pattern_hash"])
