@@ -1237,6 +1237,81 @@ _INVALID_STATUSES = frozenset({
 })
 
 
+def oracle_main(oracle_file, oracle_forward, argv=None) -> int:
+    """The standalone CLI of one oracle.py (`python oracle.py [--check]
+    [--bench] ...`), the flags of the reference's oracle template
+    (scripts/oracle_template.py:147-237): with neither --check nor --bench
+    both run; --check compares with the eager Repro on the default inputs
+    (every shapes.json point with --all-shapes) and exits 1 on a mismatch;
+    --bench times through bench_oracle (locked, graph-captured).  Used as
+
+        if __name__ == "__main__":
+            raise SystemExit(oracle_main(__file__, oracle_forward))
+    """
+    import argparse
+    repro_dir = Path(oracle_file).resolve().parent
+    repro_id = repro_dir.name
+    ap = argparse.ArgumentParser(description=f"Oracle for {repro_id}")
+    ap.add_argument("--check", action="store_true", help="verify against the eager Repro")
+    ap.add_argument("--bench", action="store_true", help="benchmark the oracle")
+    ap.add_argument("--rtol", type=float, default=1e-2)
+    ap.add_argument("--atol", type=float, default=1e-2)
+    ap.add_argument("--warmup", type=int, default=25)
+    ap.add_argument("--rep", type=int, default=200)
+    ap.add_argument("--no-skip-stochastic", action="store_true")
+    ap.add_argument("--all-shapes", action="store_true",
+                    help="every shapes.json point instead of the default one")
+    ap.add_argument("--disable-gpu-lock", action="store_true")
+    ap.add_argument("--no-compile", action="store_true",
+                    help="skip the torch.compile comparator (status ORACLE_ONLY)")
+    ap.add_argument("--cpu-eager", action="store_true",
+                    help="also time the eager repro on the host CPU")
+    ap.add_argument("--show-hw", action="store_true", help="print device info and exit")
+    ap.add_argument("--device", default=None,
+                    help="override the input device of --check (e.g. cpu)")
+    args = ap.parse_args(argv)
+    if args.show_hw:
+        print(json.dumps(get_hardware_info(), indent=2))
+        return 0
+    if not args.check and not args.bench:
+        args.check = args.bench = True
+    skip = not args.no_skip_stochastic
+    if args.check:
+        if args.all_shapes:
+            res = check_oracle_all_shapes(oracle_forward, repro_dir, repro_id,
+                                          skip_stochastic=skip, atol=args.atol, rtol=args.rtol,
+                                          device=args.device)
+            ok = not any(v in ("fail", False) for v in res.values())
+        else:
+            _seed_input_generation(1)
+            if args.device is None:
+                inputs = get_inputs(repro_dir)
+            else:
+                from repro_harness import load_shape_configs, make_inputs_from_config
+                cfg = next(iter(load_shape_configs(str(repro_dir / "repro.py")).values()))
+                inputs = make_inputs_from_config(cfg, device=args.device)
+            ok = check_oracle(oracle_forward, get_repro_instance(repro_dir), inputs,
+                              atol=args.atol, rtol=args.rtol, skip_stochastic=skip)
+        print(f"Correctness: {'PASS' if ok else 'FAIL'}")
+        if not ok:
+            return 1
+    if args.bench:
+        kw = dict(warmup=args.warmup, rep=args.rep, disable_gpu_lock=args.disable_gpu_lock,
+                  compare_compile=not args.no_compile, cpu_eager=args.cpu_eager,
+                  numerics_optout=load_numerics_optout(repro_dir))
+        if args.all_shapes:
+            results = bench_oracle_all_shapes(oracle_forward, repro_dir, repro_id, **kw)
+        else:
+            _seed_input_generation(1)
+            results = [bench_oracle(oracle_forward, get_repro_instance(repro_dir),
+                                    get_inputs(repro_dir), repro_id, **kw)]
+        for r in results:
+            print(json.dumps(r, default=str))
+        if any(isinstance(r, dict) and r.get("status", "") in _INVALID_STATUSES for r in results):
+            return 1
+    return 0
+
+
 def _runner_main(argv=None):
     import argparse
     ap = argparse.ArgumentParser(prog="python -m oracle_harness",

@@ -15,7 +15,7 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
 
 
 @oracle_impl(hardware="MI355X", point="38831ee4", description="bias softmax, rows in registers")
@@ -25,3 +25,7 @@ def oracle_forward(inputs):
     groups, heads, q, k = grouped_shape
     x = scores.reshape(flat_shape)
     return hip_oracles.scaled_bias_softmax(x, bias.reshape(bias.shape[0], q, k), 1.0, heads)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

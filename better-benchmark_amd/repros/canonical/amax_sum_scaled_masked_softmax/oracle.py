@@ -15,7 +15,7 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
 
 SCALE = 0.125  # the graph constant of repro.py
 
@@ -25,3 +25,7 @@ SCALE = 0.125  # the graph constant of repro.py
 def oracle_forward(inputs):
     x, mask = inputs
     return hip_oracles.scaled_masked_softmax(x, mask, SCALE)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

@@ -14,7 +14,7 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
 
 EPS = 1e-06
 SCALE = 0.04419417382415922
@@ -28,3 +28,7 @@ def oracle_forward(inputs):
     y = hip_oracles.rmsnorm_ex(x.reshape(-1, cols), gamma, EPS,
                                residual=residual.reshape(-1, cols), scale=SCALE, mode=1)
     return y.view(out_shape)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

@@ -15,7 +15,7 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
 
 _POINTS = ("69db7514", "280fa7d2", "2645a53e", "4ca56f88", "d1686c77", "333b11d0",
            "547c8164", "f0a667e3", "44f1e75f", "4784273d", "3cf84b69", "2150fa2c",
@@ -32,3 +32,7 @@ for _point in _POINTS:
                                  description="channels-last spatial mean")(oracle_forward)
 oracle_forward = oracle_impl(hardware="MI355X",
                              description="channels-last spatial mean, shape-general")(oracle_forward)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

@@ -12,7 +12,7 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
 
 
 @oracle_impl(hardware="MI355X", point="b84ae979", description="row mean, waves per row")
@@ -20,3 +20,7 @@ from oracle_harness import oracle_impl  # noqa: E402
 def oracle_forward(inputs):
     (x,) = inputs
     return hip_oracles.row_mean(x)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

@@ -13,7 +13,7 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
 
 EPS = 1e-05  # the graph constant of repro.py
 
@@ -23,3 +23,7 @@ EPS = 1e-05  # the graph constant of repro.py
 def oracle_forward(inputs):
     x, gamma = inputs
     return hip_oracles.rmsnorm(x, gamma, EPS)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

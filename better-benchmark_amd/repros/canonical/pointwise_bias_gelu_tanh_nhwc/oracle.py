@@ -16,7 +16,7 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
 
 
 @oracle_impl(hardware="MI355X", point="8d22dcbf", description="bias+gelu NCHW->NHWC, register transpose")
@@ -24,3 +24,7 @@ from oracle_harness import oracle_impl  # noqa: E402
 def oracle_forward(inputs):
     x, bias = inputs
     return hip_oracles.bias_gelu_nchw_to_nhwc(x, bias)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

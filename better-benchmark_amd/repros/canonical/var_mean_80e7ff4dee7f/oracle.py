@@ -14,7 +14,7 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
 
 EPS = 1e-05
 
@@ -27,3 +27,7 @@ def oracle_forward(inputs):
     y = hip_oracles.residual_layernorm(x.reshape(-1, cols), residual.reshape(-1, cols),
                                        gamma, beta, EPS, outputs="y")
     return y.view(shape)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

@@ -17,7 +17,7 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
 
 MOMENTUM = 0.1  # graph constants of repro.py
 EPS = 1e-05
@@ -30,3 +30,7 @@ def oracle_forward(inputs):
     y, save_mean, save_invstd = hip_oracles.batchnorm_train(
         x, gamma, beta, running_mean, running_var, momentum=MOMENTUM, eps=EPS, relu=True)
     return (y, save_mean, save_invstd, running_mean, running_var)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

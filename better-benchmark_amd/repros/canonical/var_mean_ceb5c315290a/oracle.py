@@ -17,7 +17,7 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
 
 EPS = 1e-3  # graph constants of repro.py
 MOMENTUM = 0.1
@@ -33,3 +33,7 @@ def oracle_forward(inputs):
         x, gamma, beta, running_mean, running_var, momentum=MOMENTUM, eps=EPS,
         var_scale=VAR_SCALE, act="silu", pad_bottom=1, pad_right=1)
     return (mean, rstd, out, running_mean, running_var)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

@@ -750,6 +750,26 @@ def test_family_graph_capture_replays_match_eager(rocm_device):
                     f"{rid} replay {rep} out{i} differs from eager"
 
 
+def test_oracle_py_runs_standalone(rocm_device):
+    """`python oracle.py --check --all-shapes` / `--bench` of a canonical
+    dir, in its own process (the reference template's CLI)."""
+    import os
+    import subprocess
+    import sys
+    import json as _json
+    d = CANONICAL / "pointwise_bias_gelu_tanh_nhwc"
+    env = dict(os.environ)
+    r = subprocess.run([sys.executable, str(d / "oracle.py"), "--check", "--all-shapes"],
+                       capture_output=True, text=True, env=env, timeout=240)
+    assert r.returncode == 0 and "Correctness: PASS" in r.stdout, r.stderr[-3000:]
+    r = subprocess.run([sys.executable, str(d / "oracle.py"), "--bench", "--no-compile",
+                        "--rep", "20", "--warmup", "5"],
+                       capture_output=True, text=True, env=env, timeout=240)
+    assert r.returncode == 0, r.stderr[-3000:]
+    line = _json.loads(r.stdout.strip().splitlines()[-1])
+    assert line["status"] == "ORACLE_ONLY" and line["hardware"] == "MI355X" and line["oracle_us"] > 0
+
+
 def test_deterministic(rocm_device):
     import hip_oracles
     x = torch.randn(128, 256, 14, 14, device=rocm_device) * 2 + 0.5

@@ -8,6 +8,7 @@ import ast
 import json
 import os
 import re
+import sys
 import textwrap
 from pathlib import Path
 
@@ -291,3 +292,33 @@ def test_product_never_imports_the_cpu_oracle():
         assert not pat.search(path.read_text()), f"{path} imports the test oracle"
     for path in PKG.rglob("*.hip"):
         assert "hipo_ref" not in path.read_text()
+
+
+MAIN_HOOK = '''
+if __name__ == "__main__":
+    from oracle_harness import oracle_main
+    raise SystemExit(oracle_main(__file__, oracle_forward))
+'''
+
+
+def test_oracle_py_standalone_cli(tmp_path):
+    """`python oracle.py [--check] [--bench] [--all-shapes]`: the reference
+    template's CLI (scripts/oracle_template.py:147-237), run as __main__."""
+    import os
+    import subprocess
+    pkg = Path(oh.__file__).resolve().parent
+    env = dict(os.environ, PYTHONPATH=str(pkg))
+    ok = fake_dir(tmp_path / "ok", ORACLE_OK + MAIN_HOOK)
+    bad = fake_dir(tmp_path / "bad", ORACLE_BAD + MAIN_HOOK)
+
+    def run(d, *args):
+        return subprocess.run([sys.executable, str(d / "oracle.py"), *args],
+                              capture_output=True, text=True, env=env, timeout=300)
+    r = run(ok, "--check")
+    assert r.returncode == 0 and "Correctness: PASS" in r.stdout, r.stderr[-2000:]
+    r = run(bad, "--check", "--all-shapes")
+    assert r.returncode == 1 and "Correctness: FAIL" in r.stdout
+    r = run(ok, "--bench", "--rep", "3", "--warmup", "1", "--disable-gpu-lock", "--no-compile")
+    assert r.returncode == 0, r.stderr[-2000:]
+    line = json.loads(r.stdout.strip().splitlines()[-1])
+    assert line["oracle_us"] > 0 and line["repro_id"] == "fake_pattern"
