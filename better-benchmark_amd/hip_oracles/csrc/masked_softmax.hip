@@ -22,12 +22,14 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <int U, bool ROUND_SCALE>
+template <int U, int WT, bool ROUND_SCALE>
 __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
     uint16_t* __restrict__ out, int64_t rows, int64_t Q, int64_t K,
     int64_t mask_stride, int64_t mask_batch_stride, int64_t heads, float scale,
-    int waves_per_row, int rows_per_block) {
+    int w_arg, int rpb_arg) {
+  const int waves_per_row = WT > 0 ? WT : w_arg;
+  const int rows_per_block = WT > 0 ? kRowMaxWaves / WT : rpb_arg;
   __shared__ float pmax[kRowMaxWaves], psum[kRowMaxWaves];
   const RowPlace p = row_place(waves_per_row, rows_per_block, rows);
   const int64_t b = p.row / Q;
@@ -247,18 +249,18 @@ bool is_power_of_two(float v) {
   return __builtin_frexpf(v, &e) == 0.5f;
 }
 
-template <int U>
+template <int U, int WT>
 void launch_vec(bool round_scale, dim3 grid, const RowPlan& plan, hipStream_t stream,
                 const uint16_t* x, const uint16_t* mask, uint16_t* out,
                 int64_t rows, int64_t Q, int64_t K, int64_t ms, int64_t mbs,
                 int64_t heads, float scale) {
   const dim3 block(plan.threads());
   if (round_scale) {
-    masked_softmax_rows<U, true><<<grid, block, 0, stream>>>(
+    masked_softmax_rows<U, WT, true><<<grid, block, 0, stream>>>(
         x, mask, out, rows, Q, K, ms, mbs, heads, scale, plan.waves_per_row,
         plan.rows_per_block);
   } else {
-    masked_softmax_rows<U, false><<<grid, block, 0, stream>>>(
+    masked_softmax_rows<U, WT, false><<<grid, block, 0, stream>>>(
         x, mask, out, rows, Q, K, ms, mbs, heads, scale, plan.waves_per_row,
         plan.rows_per_block);
   }
@@ -307,12 +309,11 @@ int softmax_impl(const uint16_t* x, const uint16_t* mask, uint16_t* out, int64_t
     const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);
     const dim3 grid(static_cast<unsigned>(blocks));
-    switch (plan.groups) {
-      case 1: launch_vec<1>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale); break;
-      case 2: launch_vec<2>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale); break;
-      case 4: launch_vec<4>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale); break;
-      default: launch_vec<8>(round_scale, grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale); break;
-    }
+#define HIPO_SOFTMAX(U_, W_)                                                            \
+  launch_vec<U_, W_>(round_scale, grid, plan, stream, x, mask, out, rows, q, k,          \
+                     mask_row_stride, mask_batch_stride, heads, scale)
+    HIPO_ROW_DISPATCH(plan, HIPO_SOFTMAX);
+#undef HIPO_SOFTMAX
   } else {
     const int64_t blocks = (rows + 3) / 4;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);

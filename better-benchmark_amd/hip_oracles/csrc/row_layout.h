@@ -150,6 +150,41 @@ struct RowPlan {
   int threads() const { return waves_per_row * rows_per_block * kWave; }
 };
 
+// Launch LAUNCH(U, WT) for a row plan.  WT > 0 fixes the waves per row
+// (and so the rows per workgroup, kRowMaxWaves / WT) at compile time for
+// the (W, U) pairs row_plan produces with W a power of two; WT = 0 takes
+// both from the kernel arguments.  Measured on MI355X (RMSNorm [16384,
+// 4096], W = 4, U = 2): 45.0 us with runtime W, 43.8 us with WT = 4 -- the
+// constant folds the row placement and the fixed-order LDS combine of the
+// per-row sums.
+#define HIPO_ROW_DISPATCH(plan, LAUNCH)                            \
+  do {                                                             \
+    const int w_ = (plan).waves_per_row, u_ = (plan).groups;       \
+    if (w_ == 1 && u_ == 1) {                                      \
+      LAUNCH(1, 1);                                                \
+    } else if (w_ == 1 && u_ == 2) {                               \
+      LAUNCH(2, 1);                                                \
+    } else if (w_ == 2 && u_ == 2) {                               \
+      LAUNCH(2, 2);                                                \
+    } else if (w_ == 4 && u_ == 2) {                               \
+      LAUNCH(2, 4);                                                \
+    } else if (w_ == 8 && u_ == 2) {                               \
+      LAUNCH(2, 8);                                                \
+    } else if (w_ == 8 && u_ == 4) {                               \
+      LAUNCH(4, 8);                                                \
+    } else if (w_ == 8 && u_ == 8) {                               \
+      LAUNCH(8, 8);                                                \
+    } else if (u_ == 1) {                                          \
+      LAUNCH(1, 0);                                                \
+    } else if (u_ == 2) {                                          \
+      LAUNCH(2, 0);                                                \
+    } else if (u_ == 4) {                                          \
+      LAUNCH(4, 0);                                                \
+    } else {                                                       \
+      LAUNCH(8, 0);                                                \
+    }                                                              \
+  } while (0)
+
 inline bool row_plan(int64_t cols, RowPlan& plan) {
   // About 2 groups (2 KiB) per wave of each streamed tensor, 8 waves per
   // workgroup.

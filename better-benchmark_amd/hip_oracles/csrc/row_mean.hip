@@ -23,10 +23,14 @@ namespace {
 constexpr int kMaxWaves = 8;  // per workgroup
 constexpr int kMaxThreads = kMaxWaves * kWave;
 
-template <int U>
+// WT > 0: waves per row (and rows per workgroup, kMaxWaves / WT) fixed at
+// compile time; WT = 0: both from the arguments.
+template <int U, int WT>
 __global__ __launch_bounds__(kMaxThreads) void row_mean_f32_vec4(
     const float* __restrict__ x, float* __restrict__ out, int64_t rows,
-    int64_t cols, int64_t row_stride, int waves_per_row, int rows_per_block) {
+    int64_t cols, int64_t row_stride, int w_arg, int rpb_arg) {
+  const int waves_per_row = WT > 0 ? WT : w_arg;
+  const int rows_per_block = WT > 0 ? kMaxWaves / WT : rpb_arg;
   __shared__ float part[kMaxWaves];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
@@ -109,13 +113,26 @@ extern "C" int hipo_row_mean_f32(const float* x, float* out, int64_t rows,
     const int64_t blocks = (rows + rpb - 1) / rpb;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "row_mean: too many rows");
     const dim3 grid(static_cast<unsigned>(blocks)), block(waves * rpb * kWave);
+#define HIPO_MEAN(U_, W_)                                                            \
+  row_mean_f32_vec4<U_, W_><<<grid, block, 0, stream>>>(x, out, rows, cols, row_stride, \
+                                                        waves, rpb)
+#define HIPO_MEAN_W(U_)                                  \
+  switch (waves) {                                       \
+    case 1: HIPO_MEAN(U_, 1); break;                     \
+    case 2: HIPO_MEAN(U_, 2); break;                     \
+    case 4: HIPO_MEAN(U_, 4); break;                     \
+    case 8: HIPO_MEAN(U_, 8); break;                     \
+    default: HIPO_MEAN(U_, 0); break;                    \
+  }
     if (per_lane <= 1) {
-      row_mean_f32_vec4<1><<<grid, block, 0, stream>>>(x, out, rows, cols, row_stride, waves, rpb);
+      HIPO_MEAN_W(1);
     } else if (per_lane <= 2) {
-      row_mean_f32_vec4<2><<<grid, block, 0, stream>>>(x, out, rows, cols, row_stride, waves, rpb);
+      HIPO_MEAN_W(2);
     } else {
-      row_mean_f32_vec4<4><<<grid, block, 0, stream>>>(x, out, rows, cols, row_stride, waves, rpb);
+      HIPO_MEAN_W(4);
     }
+#undef HIPO_MEAN_W
+#undef HIPO_MEAN
   } else {
     const int64_t blocks = (rows + 3) / 4;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "row_mean: too many rows");

@@ -15,19 +15,23 @@
 // HBM-bound.  Algorithmic bytes per row (cols = C):
 //   residual LayerNorm: 2C (x) + 2C (residual) + 2C (h) + 2C (y) + 8
 //   RMSNorm:            2C (x) + 2C (y) + 4
+#include <type_traits>
+
 #include "row_layout.h"
 #include "welford.h"
 
 namespace hipo {
 namespace {
 
-template <int U>
+template <int U, int WT>
 __global__ __launch_bounds__(kRowMaxThreads) void residual_layernorm_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
     const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
     uint16_t* __restrict__ h, uint16_t* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t rows,
-    int64_t cols, float eps, int waves_per_row, int rows_per_block) {
+    int64_t cols, float eps, int w_arg, int rpb_arg) {
+  const int waves_per_row = WT > 0 ? WT : w_arg;
+  const int rows_per_block = WT > 0 ? kRowMaxWaves / WT : rpb_arg;
   __shared__ Welford part[kRowMaxWaves];
   const RowPlace p = row_place(waves_per_row, rows_per_block, rows);
   const int64_t base = p.row * cols;
@@ -105,12 +109,14 @@ __global__ __launch_bounds__(kRowMaxThreads) void residual_layernorm_rows(
 // MODE 1 (HF T5 op order): t = bf16(h * rstd); u = bf16(gamma * t);
 //                          y = scale == 1 ? u : bf16(u * scale).
 // With a residual, h = bf16(x + residual) (the eager bf16 add), else h = x.
-template <int U, bool RES, int MODE>
+template <int U, int WT, bool RES, int MODE>
 __global__ __launch_bounds__(kRowMaxThreads) void rmsnorm_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
     const uint16_t* __restrict__ gamma, uint16_t* __restrict__ y,
     float* __restrict__ rstd_out, int64_t rows, int64_t cols, float eps,
-    float scale, int waves_per_row, int rows_per_block) {
+    float scale, int w_arg, int rpb_arg) {
+  const int waves_per_row = WT > 0 ? WT : w_arg;
+  const int rows_per_block = WT > 0 ? kRowMaxWaves / WT : rpb_arg;
   __shared__ float part[kRowMaxWaves];
   const RowPlace p = row_place(waves_per_row, rows_per_block, rows);
   const int64_t base = p.row * cols;
@@ -151,30 +157,40 @@ __global__ __launch_bounds__(kRowMaxThreads) void rmsnorm_rows(
   }
   const float rstd = 1.0f / __builtin_sqrtf(sq / static_cast<float>(cols) + eps);
 
+  // The scale test is hoisted out of the per-element loop (one uniform
+  // branch, two copies of the store loop).
+  auto store = [&](auto scaled) {
+    constexpr bool kScaled = decltype(scaled)::value;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t col = row_group_col(u, waves_per_row, p);
-    const u32x4_t gv = row_load_cached(gamma, col, cols);
-    u32x4_t o;
+    for (int u = 0; u < U; ++u) {
+      const int64_t col = row_group_col(u, waves_per_row, p);
+      const u32x4_t gv = row_load_cached(gamma, col, cols);
+      u32x4_t o;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      float a = bf16lo(xv[u][d]) * rstd, b = bf16hi(xv[u][d]) * rstd;
-      if (MODE == 0) {
-        a *= bf16lo(gv[d]);
-        b *= bf16hi(gv[d]);
-        if (scale != 1.0f) {
-          a *= scale;
-          b *= scale;
+      for (int d = 0; d < 4; ++d) {
+        float a = bf16lo(xv[u][d]) * rstd, b = bf16hi(xv[u][d]) * rstd;
+        if constexpr (MODE == 0) {
+          a *= bf16lo(gv[d]);
+          b *= bf16hi(gv[d]);
+          if constexpr (kScaled) {
+            a *= scale;
+            b *= scale;
+          }
+          o[d] = pack_bf16x2(a, b);
+        } else {
+          const uint32_t t = pack_bf16x2(a, b);
+          uint32_t w = pack_bf16x2(bf16lo(gv[d]) * bf16lo(t), bf16hi(gv[d]) * bf16hi(t));
+          if constexpr (kScaled) w = pack_bf16x2(bf16lo(w) * scale, bf16hi(w) * scale);
+          o[d] = w;
         }
-        o[d] = pack_bf16x2(a, b);
-      } else {
-        const uint32_t t = pack_bf16x2(a, b);
-        uint32_t w = pack_bf16x2(bf16lo(gv[d]) * bf16lo(t), bf16hi(gv[d]) * bf16hi(t));
-        if (scale != 1.0f) w = pack_bf16x2(bf16lo(w) * scale, bf16hi(w) * scale);
-        o[d] = w;
       }
+      if (p.valid && col < cols) row_store_stream(y + base, col, o);
     }
-    if (p.valid && col < cols) row_store_stream(y + base, col, o);
+  };
+  if (scale != 1.0f) {
+    store(std::true_type{});
+  } else {
+    store(std::false_type{});
   }
   if (rstd_out != nullptr && p.valid && p.w == 0 && p.lane == 0) rstd_out[p.row] = rstd;
 }
@@ -257,14 +273,6 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_scalar(
 }  // namespace
 }  // namespace hipo
 
-// Launch KERNEL (an expression naming U_) with U_ = plan.groups.
-#define HIPO_ROW_SWITCH(plan, KERNEL, grid, stream, ...)                          \
-  switch ((plan).groups) {                                                        \
-    case 1: { constexpr int U_ = 1; KERNEL<<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; } \
-    case 2: { constexpr int U_ = 2; KERNEL<<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; } \
-    case 4: { constexpr int U_ = 4; KERNEL<<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; } \
-    default: { constexpr int U_ = 8; KERNEL<<<grid, dim3((plan).threads()), 0, stream>>>(__VA_ARGS__); break; } \
-  }
 
 extern "C" int hipo_residual_layernorm_bf16(
     const uint16_t* x, const uint16_t* residual, const uint16_t* gamma,
@@ -285,9 +293,13 @@ extern "C" int hipo_residual_layernorm_bf16(
     const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "residual_layernorm: too many rows");
     const dim3 grid(static_cast<unsigned>(blocks));
-    HIPO_ROW_SWITCH(plan, residual_layernorm_rows<U_>, grid, stream, x, residual,
-                    gamma, beta, h, y, mean, rstd, rows, cols, eps,
-                    plan.waves_per_row, plan.rows_per_block);
+    const dim3 block(plan.threads());
+#define HIPO_LN(U_, W_)                                                              \
+  residual_layernorm_rows<U_, W_><<<grid, block, 0, stream>>>(                       \
+      x, residual, gamma, beta, h, y, mean, rstd, rows, cols, eps, plan.waves_per_row, \
+      plan.rows_per_block)
+    HIPO_ROW_DISPATCH(plan, HIPO_LN);
+#undef HIPO_LN
   } else {
     const int64_t blocks = (rows + 3) / 4;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "residual_layernorm: too many rows");
@@ -307,12 +319,11 @@ void launch_rmsnorm(const RowPlan& plan, dim3 grid, hipStream_t stream,
                     int64_t rows, int64_t cols, float eps, float scale) {
   const dim3 block(plan.threads());
   const int w = plan.waves_per_row, r = plan.rows_per_block;
-  switch (plan.groups) {
-    case 1: rmsnorm_rows<1, RES, MODE><<<grid, block, 0, stream>>>(x, residual, gamma, y, rstd, rows, cols, eps, scale, w, r); break;
-    case 2: rmsnorm_rows<2, RES, MODE><<<grid, block, 0, stream>>>(x, residual, gamma, y, rstd, rows, cols, eps, scale, w, r); break;
-    case 4: rmsnorm_rows<4, RES, MODE><<<grid, block, 0, stream>>>(x, residual, gamma, y, rstd, rows, cols, eps, scale, w, r); break;
-    default: rmsnorm_rows<8, RES, MODE><<<grid, block, 0, stream>>>(x, residual, gamma, y, rstd, rows, cols, eps, scale, w, r); break;
-  }
+#define HIPO_RMS(U_, W_)                                            \
+  rmsnorm_rows<U_, W_, RES, MODE><<<grid, block, 0, stream>>>(      \
+      x, residual, gamma, y, rstd, rows, cols, eps, scale, w, r)
+  HIPO_ROW_DISPATCH(plan, HIPO_RMS);
+#undef HIPO_RMS
 }
 
 int rmsnorm_impl(const uint16_t* x, const uint16_t* residual, const uint16_t* gamma,
