@@ -8,8 +8,9 @@
 //
 // LayerNorm statistics are over the bf16-rounded h (the eager op order).
 // Each wave computes an exact two-pass (count, mean, M2) over its own
-// values in registers; the W triples of a row are merged with Chan's
-// formula through LDS in a fixed order (deterministic).  RMSNorm adds the
+// values in registers; the W triples of a row are merged through LDS in
+// closed form (the k-group form of Chan's formula: one division), in a
+// fixed order (deterministic).  RMSNorm adds the
 // W wave sums of squares in a fixed order.
 //
 // HBM-bound.  Algorithmic bytes per row (cols = C):
@@ -74,11 +75,24 @@ __global__ __launch_bounds__(kRowMaxThreads) void residual_layernorm_rows(
   }
   Welford t{n, wmean, wave_sum(sq)};
   if (waves_per_row > 1) {
+    // The W wave triples of the row merged in closed form, in wave order:
+    // N = sum n_k, mean = sum n_k mean_k / N, M2 = sum M2_k + n_k (mean_k -
+    // mean)^2 (one division; waves without values add zero).
     if (p.lane == 0) part[p.wave] = t;
     __syncthreads();
     const int first = p.wave - p.w;
-    t = part[first];
-    for (int k = 1; k < waves_per_row; ++k) t = welford_merge(t, part[first + k]);
+    float nn = 0.f, s1 = 0.f;
+    for (int k = 0; k < waves_per_row; ++k) {
+      nn += part[first + k].n;
+      s1 = __builtin_fmaf(part[first + k].n, part[first + k].mean, s1);
+    }
+    const float mu = s1 / nn;
+    float m2 = 0.f;
+    for (int k = 0; k < waves_per_row; ++k) {
+      const float d = part[first + k].mean - mu;
+      m2 += __builtin_fmaf(part[first + k].n * d, d, part[first + k].m2);
+    }
+    t = Welford{nn, mu, m2};
   }
   const float mean = t.mean;
   const float rstd = 1.0f / __builtin_sqrtf(t.m2 / static_cast<float>(cols) + eps);
