@@ -1,4 +1,4 @@
-"""CPU oracle for the six HIP kernels -- TEST INFRASTRUCTURE ONLY.
+"""CPU oracle for the HIP kernels -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
 import this package, and only as the checker (or as the timed CPU baseline),
@@ -38,7 +38,16 @@ _SIGS = {
     "ref_residual_layernorm_bf16": (None, [_p] * 8 + [_i64, _i64, _f, _i]),
     "ref_rmsnorm_bf16": (None, [_p] * 4 + [_i64, _i64, _f, _i]),
     "ref_batchnorm_train_f32": (None, [_p] * 8 + [_i64, _i64, _i64, _f, _f, _i, _i]),
+    "ref_scaled_bias_softmax_bf16": (
+        None, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f, _i]),
+    "ref_spatial_mean_nhwc_bf16": (None, [_p, _p, _i64, _i64, _i64, _i]),
+    "ref_rmsnorm_ex_bf16": (None, [_p] * 5 + [_i64, _i64, _f, _f, _i, _i]),
+    "ref_batchnorm_nhwc_act_pad_bf16": (
+        None, [_p] * 8 + [_i64] * 6 + [_f, _f, _f, _i, _i]),
+    "ref_batchnorm_nchw_act_mean_bf16": (None, [_p] * 8 + [_i64] * 3 + [_f, _f, _f, _i, _i]),
 }
+
+_ACTS = {None: 0, "none": 0, "relu": 1, "silu": 2}
 
 
 def load():
@@ -144,3 +153,85 @@ def batchnorm_train(x, gamma, beta, running_mean, running_var, *, momentum: floa
         y.data_ptr(), sm.data_ptr(), si.data_ptr(), n, c, h * w,
         float(momentum), float(eps), 1 if relu else 0, _th(threads))
     return y, sm, si, rm, rv
+
+
+def scaled_bias_softmax(x, bias, scale: float, heads: int, threads=None):
+    """softmax(x * scale + bias[b / heads]) for x [B, Q, K], bias [B / heads, Q, K]."""
+    x = _cpu(x, torch.bfloat16)
+    bias = _cpu(bias, torch.bfloat16)
+    b, q, k = x.shape
+    assert b % heads == 0 and tuple(bias.shape) == (b // heads, q, k)
+    out = torch.empty_like(x)
+    load().ref_scaled_bias_softmax_bf16(x.data_ptr(), bias.data_ptr(), out.data_ptr(),
+                                        b, q, k, k, q * k, heads, float(scale), _th(threads))
+    return out
+
+
+def spatial_mean_nhwc(x, threads=None):
+    """Mean over H, W of a bf16 [N, C, H, W] tensor -> [N, C, 1, 1]."""
+    assert x.dtype == torch.bfloat16
+    n, c, h, w = x.shape
+    xl = x.detach().to("cpu").contiguous(memory_format=torch.channels_last)
+    out = torch.empty((n, c, 1, 1), dtype=torch.bfloat16)
+    load().ref_spatial_mean_nhwc_bf16(xl.data_ptr(), out.data_ptr(), n, h * w, c, _th(threads))
+    return out
+
+
+def rmsnorm_ex(x, gamma, eps: float, *, residual=None, scale: float = 1.0, mode: int = 0,
+               threads=None):
+    """(y, rstd) of the RMSNorm with an optional residual, scale and rounding
+    order (mode 0: torch rms_norm, mode 1: HF T5)."""
+    x, gamma = _cpu(x, torch.bfloat16), _cpu(gamma, torch.bfloat16)
+    res = None if residual is None else _cpu(residual, torch.bfloat16)
+    rows, cols = x.shape
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, dtype=torch.float32)
+    load().ref_rmsnorm_ex_bf16(x.data_ptr(), None if res is None else res.data_ptr(),
+                               gamma.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, cols,
+                               float(eps), float(scale), int(mode), _th(threads))
+    return y, rstd
+
+
+def _bn_params(c, gamma, beta, running_mean, running_var):
+    gamma, beta = _cpu(gamma, torch.float32), _cpu(beta, torch.float32)
+    rm = _cpu(running_mean, torch.float32).clone()
+    rv = _cpu(running_var, torch.float32).clone()
+    assert gamma.numel() == beta.numel() == rm.numel() == rv.numel() == c
+    return gamma, beta, rm, rv
+
+
+def batchnorm_nhwc_act_pad(x, gamma, beta, running_mean, running_var, *, momentum: float,
+                           eps: float, var_scale: float, act=None, pad_bottom: int = 0,
+                           pad_right: int = 0, threads=None):
+    """bf16 BatchNorm-train + activation + bottom/right zero pad.  Returns
+    (save_mean [1,C,1,1], save_rstd [1,C,1,1], out channels-last, rm', rv')."""
+    assert x.dtype == torch.bfloat16
+    n, c, h, w = x.shape
+    xl = x.detach().to("cpu").contiguous(memory_format=torch.channels_last)
+    gamma, beta, rm, rv = _bn_params(c, gamma, beta, running_mean, running_var)
+    out = torch.empty((n, c, h + pad_bottom, w + pad_right), dtype=torch.bfloat16,
+                      memory_format=torch.channels_last)
+    sm = torch.empty((1, c, 1, 1), dtype=torch.float32)
+    sr = torch.empty((1, c, 1, 1), dtype=torch.float32)
+    load().ref_batchnorm_nhwc_act_pad_bf16(
+        xl.data_ptr(), gamma.data_ptr(), beta.data_ptr(), rm.data_ptr(), rv.data_ptr(),
+        sm.data_ptr(), sr.data_ptr(), out.data_ptr(), n, h, w, c, int(pad_bottom),
+        int(pad_right), float(momentum), float(eps), float(var_scale), _ACTS[act], _th(threads))
+    return sm, sr, out, rm, rv
+
+
+def batchnorm_nchw_act_mean(x, gamma, beta, running_mean, running_var, *, momentum: float,
+                            eps: float, var_scale: float, act=None, threads=None):
+    """bf16 NCHW BatchNorm-train + activation + mean over H, W.  Returns
+    (save_mean [1,C,1,1], save_rstd [1,C,1,1], out [N, C], rm', rv')."""
+    x = _cpu(x, torch.bfloat16)
+    n, c, h, w = x.shape
+    gamma, beta, rm, rv = _bn_params(c, gamma, beta, running_mean, running_var)
+    out = torch.empty((n, c), dtype=torch.bfloat16)
+    sm = torch.empty((1, c, 1, 1), dtype=torch.float32)
+    sr = torch.empty((1, c, 1, 1), dtype=torch.float32)
+    load().ref_batchnorm_nchw_act_mean_bf16(
+        x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), rm.data_ptr(), rv.data_ptr(),
+        sm.data_ptr(), sr.data_ptr(), out.data_ptr(), n, c, h * w, float(momentum),
+        float(eps), float(var_scale), _ACTS[act], _th(threads))
+    return sm, sr, out, rm, rv

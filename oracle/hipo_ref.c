@@ -1,5 +1,5 @@
 /*
- * CPU restatement of the six oracle patterns -- TEST INFRASTRUCTURE ONLY.
+ * CPU restatement of the oracle patterns -- TEST INFRASTRUCTURE ONLY.
  *
  * This file is the checker, never the product: only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
@@ -14,6 +14,12 @@
  *   residual LayerNorm  repros/canonical/var_mean_80e7ff4dee7f/repro.py:23-39
  *   RMSNorm             repros/canonical/mean_4462ce967d63/repro.py:23-38
  *   BatchNorm train     repros/canonical/var_mean_mean_19ffdb35cc67/repro.py:23-54
+ * and the corpus families the kernels generalise to:
+ *   spatial mean, channels-last   repros/canonical/mean_c9e1a8113328/repro.py:26
+ *   per-group bias softmax        repros/canonical/amax_sum_20ccc18dda60/repro.py:23-35
+ *   T5 residual RMSNorm           repros/canonical/mean_4462ce967d63/repro.py:23-38
+ *   bf16 BN + SiLU + pad (NHWC)   repros/canonical/var_mean_ceb5c315290a/repro.py:27-58
+ *   bf16 BN + ReLU + mean (NCHW)  repros/canonical/var_mean_mean_19ffdb35cc67/repro.py:23-54
  * (paths relative to the reference tree).  Every rounding that the eager
  * graph performs on a bf16 tensor is reproduced (float arithmetic, then
  * round-to-nearest-even to bf16); reductions and transcendental functions
@@ -127,14 +133,16 @@ void ref_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x, const uint16_t* bias,
 }
 
 /*
- * s = bf16(bf16(x * scale) + mask[q, :]); out = bf16(softmax(s)) with the
- * max, exp and sum in fp64.  x/out [batch, q, k]; mask row stride in
- * elements.
+ * s = bf16(bf16(x * scale) + bias[b / heads, q, :]); out = bf16(softmax(s))
+ * with the max, exp and sum in fp64.  x/out [batch, q, k]; the bias row of
+ * (b, q) starts at (b / heads) * bias_batch_stride + q * bias_row_stride
+ * elements.  The masked softmax is the case batch_stride = 0, heads = 1.
  */
-void ref_scaled_masked_softmax_bf16(const uint16_t* x, const uint16_t* mask,
-                                    uint16_t* out, int64_t batch, int64_t q,
-                                    int64_t k, int64_t mask_stride, float scale,
-                                    int threads) {
+void ref_scaled_bias_softmax_bf16(const uint16_t* x, const uint16_t* mask,
+                                  uint16_t* out, int64_t batch, int64_t q,
+                                  int64_t k, int64_t mask_stride,
+                                  int64_t mask_batch_stride, int64_t heads,
+                                  float scale, int threads) {
   const int64_t rows = batch * q;
   if (k <= 0) return;
 #pragma omp parallel num_threads(threads)
@@ -143,7 +151,8 @@ void ref_scaled_masked_softmax_bf16(const uint16_t* x, const uint16_t* mask,
 #pragma omp for schedule(static)
     for (int64_t r = 0; r < rows; ++r) {
       const uint16_t* xr = x + r * k;
-      const uint16_t* mr = mask + (r % q) * mask_stride;
+      const uint16_t* mr =
+          mask + ((r / q) / heads) * mask_batch_stride + (r % q) * mask_stride;
       double m = -INFINITY;
       for (int64_t j = 0; j < k; ++j) {
         const float a = round_bf16(bf16_to_f32(xr[j]) * scale);
@@ -165,6 +174,14 @@ void ref_scaled_masked_softmax_bf16(const uint16_t* x, const uint16_t* mask,
     }
     free(s);
   }
+}
+
+void ref_scaled_masked_softmax_bf16(const uint16_t* x, const uint16_t* mask,
+                                    uint16_t* out, int64_t batch, int64_t q,
+                                    int64_t k, int64_t mask_stride, float scale,
+                                    int threads) {
+  ref_scaled_bias_softmax_bf16(x, mask, out, batch, q, k, mask_stride, 0, 1, scale,
+                               threads);
 }
 
 /*
@@ -272,4 +289,165 @@ void ref_batchnorm_train_f32(const float* x, const float* gamma,
     running_mean[ch] = (float)(mom * mean + (1.0 - mom) * running_mean[ch]);
     running_var[ch] = (float)(mom * unbiased + (1.0 - mom) * running_var[ch]);
   }
+}
+
+/*
+ * Spatial mean of a channels-last bf16 tensor, physical [n, p, c]:
+ * out[n, c] = bf16(sum_p x / p), the sum in fp64.
+ */
+void ref_spatial_mean_nhwc_bf16(const uint16_t* x, uint16_t* out, int64_t n,
+                                int64_t p, int64_t c, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t i = 0; i < n * c; ++i) {
+    const int64_t img = i / c, ch = i % c;
+    const uint16_t* src = x + img * p * c + ch;
+    double s = 0.0;
+    for (int64_t j = 0; j < p; ++j) s += bf16_to_f32(src[j * c]);
+    out[i] = f64_to_bf16(s / (double)p);
+  }
+}
+
+/*
+ * RMSNorm with an optional residual and output scale, in the two eager op
+ * orders:  h = residual ? bf16(x + residual) : x;  rstd = 1/sqrt(mean(h^2)
+ * + eps) (fp64);  mode 0: y = bf16(h * rstd * gamma * scale) (one rounding,
+ * torch rms_norm);  mode 1 (HF T5): t = bf16(h * rstd); u = bf16(gamma * t);
+ * y = scale == 1 ? u : bf16(u * scale).  residual may be NULL.
+ */
+void ref_rmsnorm_ex_bf16(const uint16_t* x, const uint16_t* res, const uint16_t* gamma,
+                         uint16_t* y, float* rstd_out, int64_t rows, int64_t cols,
+                         float eps, float scale, int mode, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t base = r * cols;
+    double q = 0.0;
+    for (int64_t j = 0; j < cols; ++j) {
+      const float a = bf16_to_f32(x[base + j]);
+      const double h = res ? round_bf16(a + bf16_to_f32(res[base + j])) : a;
+      q += h * h;
+    }
+    const double rstd = 1.0 / sqrt(q / (double)cols + (double)eps);
+    for (int64_t j = 0; j < cols; ++j) {
+      const float a = bf16_to_f32(x[base + j]);
+      const double h = res ? round_bf16(a + bf16_to_f32(res[base + j])) : a;
+      const double g = bf16_to_f32(gamma[j]);
+      if (mode == 0) {
+        y[base + j] = f64_to_bf16(h * rstd * g * (double)scale);
+      } else {
+        const double t = bf16_to_f32(f64_to_bf16(h * rstd));
+        const double u = bf16_to_f32(f64_to_bf16(g * t));
+        y[base + j] = scale == 1.0f ? f64_to_bf16(u) : f64_to_bf16(u * (double)scale);
+      }
+    }
+    if (rstd_out) rstd_out[r] = (float)rstd;
+  }
+}
+
+/* act(bf16(((x - mean) * rstd) * gamma + beta)) of the bf16 BN graphs, in
+ * fp64 with the graph's bf16 rounding; act 0 none, 1 ReLU, 2 SiLU (rounded
+ * to bf16 again). */
+static inline double bn_bf16_act(double xv, double mean, double rstd, double g, double b,
+                                 int act) {
+  double t = bf16_to_f32(f64_to_bf16((xv - mean) * rstd * g + b));
+  if (act == 1) {
+    t = t < 0.0 ? 0.0 : t;
+  } else if (act == 2) {
+    t = bf16_to_f32(f64_to_bf16(t / (1.0 + exp(-t))));
+  }
+  return t;
+}
+
+/* Per-channel statistics, save_* and running statistics of the bf16 BN
+ * graphs: var with correction 0 in fp64; save_rstd = 1/sqrt(float(var) +
+ * eps); running_mean = mean*m + rm*(1-m); running_var = var*var_scale*m +
+ * rv*(1-m).  at(i, j) addresses channel element j of channel i's `cnt`. */
+static void bn_bf16_stats(const uint16_t* x, int64_t cnt, int64_t c, int nhwc, int64_t n,
+                          int64_t hw, float momentum, float eps, float var_scale,
+                          float* running_mean, float* running_var, float* save_mean,
+                          float* save_rstd, double* mean_out, double* rstd_out, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t ch = 0; ch < c; ++ch) {
+    double s = 0.0;
+    for (int64_t i = 0; i < cnt; ++i) {
+      const int64_t idx = nhwc ? i * c + ch : ((i / hw) * c + ch) * hw + i % hw;
+      s += bf16_to_f32(x[idx]);
+    }
+    const double mean = s / (double)cnt;
+    double q = 0.0;
+    for (int64_t i = 0; i < cnt; ++i) {
+      const int64_t idx = nhwc ? i * c + ch : ((i / hw) * c + ch) * hw + i % hw;
+      const double d = bf16_to_f32(x[idx]) - mean;
+      q += d * d;
+    }
+    const double var = q / (double)cnt;
+    const double rstd = 1.0 / sqrt((double)(float)var + (double)eps);
+    save_mean[ch] = (float)mean;
+    save_rstd[ch] = (float)rstd;
+    mean_out[ch] = (float)mean;
+    rstd_out[ch] = (float)rstd;
+    const double m = momentum;
+    running_mean[ch] = (float)(mean * m + running_mean[ch] * (1.0 - m));
+    running_var[ch] = (float)(var * var_scale * m + running_var[ch] * (1.0 - m));
+  }
+  (void)n;
+}
+
+/*
+ * Channels-last bf16 BatchNorm training forward + activation + zero pad of
+ * the bottom / right border: x physical [n, h, w, c]; out physical
+ * [n, h + pad_bottom, w + pad_right, c].
+ */
+void ref_batchnorm_nhwc_act_pad_bf16(const uint16_t* x, const float* gamma,
+                                     const float* beta, float* running_mean,
+                                     float* running_var, float* save_mean,
+                                     float* save_rstd, uint16_t* out, int64_t n,
+                                     int64_t h, int64_t w, int64_t c, int64_t pad_bottom,
+                                     int64_t pad_right, float momentum, float eps,
+                                     float var_scale, int act, int threads) {
+  double* mean = (double*)malloc(sizeof(double) * (size_t)c);
+  double* rstd = (double*)malloc(sizeof(double) * (size_t)c);
+  bn_bf16_stats(x, n * h * w, c, 1, n, h * w, momentum, eps, var_scale, running_mean,
+                running_var, save_mean, save_rstd, mean, rstd, threads);
+  const int64_t ho = h + pad_bottom, wo = w + pad_right;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t o = 0; o < n * ho * wo; ++o) {
+    const int64_t img = o / (ho * wo), rem = o % (ho * wo), y = rem / wo, xw = rem % wo;
+    for (int64_t ch = 0; ch < c; ++ch) {
+      double v = 0.0;
+      if (y < h && xw < w) {
+        const double xv = bf16_to_f32(x[((img * h + y) * w + xw) * c + ch]);
+        v = bn_bf16_act(xv, mean[ch], rstd[ch], gamma[ch], beta[ch], act);
+      }
+      out[o * c + ch] = f64_to_bf16(v);
+    }
+  }
+  free(mean);
+  free(rstd);
+}
+
+/*
+ * NCHW bf16 BatchNorm training forward + activation + mean over H, W:
+ * out[n, c] = bf16(mean_hw act(...)) (fp64 sum).
+ */
+void ref_batchnorm_nchw_act_mean_bf16(const uint16_t* x, const float* gamma,
+                                      const float* beta, float* running_mean,
+                                      float* running_var, float* save_mean,
+                                      float* save_rstd, uint16_t* out, int64_t n,
+                                      int64_t c, int64_t hw, float momentum, float eps,
+                                      float var_scale, int act, int threads) {
+  double* mean = (double*)malloc(sizeof(double) * (size_t)c);
+  double* rstd = (double*)malloc(sizeof(double) * (size_t)c);
+  bn_bf16_stats(x, n * hw, c, 0, n, hw, momentum, eps, var_scale, running_mean,
+                running_var, save_mean, save_rstd, mean, rstd, threads);
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t i = 0; i < n * c; ++i) {
+    const int64_t ch = i % c;
+    const uint16_t* seg = x + i * hw;
+    double s = 0.0;
+    for (int64_t j = 0; j < hw; ++j)
+      s += bn_bf16_act(bf16_to_f32(seg[j]), mean[ch], rstd[ch], gamma[ch], beta[ch], act);
+    out[i] = f64_to_bf16(s / (double)hw);
+  }
+  free(mean);
+  free(rstd);
 }

@@ -82,6 +82,65 @@ def main() -> None:
         "save_mean": floats(sm), "save_invstd": floats(si),
         "running_mean": floats(rm), "running_var": floats(rv)}
 
+    # --- corpus families (appended: the cases above keep their inputs) ---
+    x = (torch.randn(2, 24, 3, 5, generator=g) + 0.3).to(bf).contiguous(
+        memory_format=torch.channels_last)
+    cases["spatial_mean_nhwc"] = {"x_nhwc": bits(x.permute(0, 2, 3, 1)), "shape": [2, 24, 3, 5],
+                                  "out": bits(torch.ops.aten.mean.dim(x, [2, 3], True))}
+
+    x = torch.randn(6, 4, 12, generator=g).to(bf)          # 2 bias groups x 3 heads
+    bias = torch.randn(2, 4, 12, generator=g).to(bf)
+    s4 = torch.ops.aten.add.Tensor(torch.ops.aten.mul.Tensor(x, 0.5).view(2, 3, 4, 12),
+                                   bias.view(2, 1, 4, 12))
+    y = torch.softmax(s4.float(), -1).to(bf).view(6, 4, 12)
+    cases["bias_softmax"] = {"x": bits(x), "bias": bits(bias), "shape": [6, 4, 12], "heads": 3,
+                             "scale": 0.5, "out": bits(y)}
+
+    x = torch.randn(6, 32, generator=g).to(bf)
+    r = torch.randn(6, 32, generator=g).to(bf)
+    gm = (1 + 0.1 * torch.randn(32, generator=g)).to(bf)
+    h = r + x
+    rs = torch.rsqrt(h.float().pow(2).mean(-1, keepdim=True) + 1e-6)
+    t5 = (gm * (h.float() * rs).to(bf)) * 0.04419417382415922
+    cases["rmsnorm_t5"] = {"x": bits(x), "residual": bits(r), "gamma": bits(gm), "shape": [6, 32],
+                           "eps": 1e-6, "scale": 0.04419417382415922, "y": bits(t5),
+                           "rstd": floats(rs.squeeze(-1)),
+                           "y_residual_rms_norm": bits(F.rms_norm(h, [32], gm, 1e-6))}
+
+    def bn_bf16(x, rm, rv, w, b, eps, var_scale):
+        var, mean = torch.var_mean(x.float(), [0, 2, 3], correction=0, keepdim=True)
+        rstd = torch.rsqrt(var + eps)
+        t = ((x - mean) * rstd * w.view(-1, 1, 1) + b.view(-1, 1, 1)).to(bf)
+        rm2 = mean.flatten() * 0.1 + rm * 0.9
+        rv2 = var.flatten() * var_scale * 0.1 + rv * 0.9
+        return mean, rstd, t, rm2, rv2
+
+    x = (2 * torch.randn(3, 8, 4, 5, generator=g) + 0.5).to(bf).contiguous(
+        memory_format=torch.channels_last)
+    rm, rv = torch.randn(8, generator=g), torch.rand(8, generator=g) + 0.5
+    w, b = 1 + 0.1 * torch.randn(8, generator=g), 0.1 * torch.randn(8, generator=g)
+    mean, rstd, t, rm2, rv2 = bn_bf16(x, rm, rv, w, b, 1e-3, 1.25)
+    tf = t.float()
+    silu = (tf / (1 + torch.exp(-tf))).to(bf)
+    out = torch.ops.aten.constant_pad_nd.default(silu, [0, 1, 0, 1], 0.0)
+    cases["bn_nhwc_silu_pad"] = {
+        "x_nhwc": bits(x.permute(0, 2, 3, 1)), "shape": [3, 8, 4, 5], "running_mean": floats(rm),
+        "running_var": floats(rv), "gamma": floats(w), "beta": floats(b), "eps": 1e-3,
+        "momentum": 0.1, "var_scale": 1.25, "pad": [1, 1], "save_mean": floats(mean),
+        "save_rstd": floats(rstd), "out_nhwc": bits(out.permute(0, 2, 3, 1)),
+        "running_mean_out": floats(rm2), "running_var_out": floats(rv2)}
+
+    x = (2 * torch.randn(5, 8, 3, 3, generator=g) + 0.5).to(bf)
+    rm, rv = torch.randn(8, generator=g), torch.rand(8, generator=g) + 0.5
+    w, b = 1 + 0.1 * torch.randn(8, generator=g), 0.1 * torch.randn(8, generator=g)
+    mean, rstd, t, rm2, rv2 = bn_bf16(x, rm, rv, w, b, 1e-5, 1.5)
+    out = torch.ops.aten.mean.dim(torch.relu(t), [2, 3])
+    cases["bn_nchw_relu_mean"] = {
+        "x": bits(x), "shape": [5, 8, 3, 3], "running_mean": floats(rm), "running_var": floats(rv),
+        "gamma": floats(w), "beta": floats(b), "eps": 1e-5, "momentum": 0.1, "var_scale": 1.5,
+        "save_mean": floats(mean), "save_rstd": floats(rstd), "out": bits(out),
+        "running_mean_out": floats(rm2), "running_var_out": floats(rv2)}
+
     doc = {"generator": "tests/golden/make_golden.py",
            "producer": f"torch {torch.__version__} eager ATen CPU kernels",
            "cases": cases}

@@ -91,11 +91,35 @@ def test_all_points_vs_oracle_and_eager(rid, rocm_device):
         del cpu_in, dev_in, got, want, eager
 
 
+def _family_oracle(rid, i):
+    """The C oracle's outputs for a family point's CPU inputs."""
+    import oracle as ref
+    if rid == "mean_c9e1a8113328":
+        return [ref.spatial_mean_nhwc(i[0])]
+    if rid == "mean_4462ce967d63":
+        x, r, g = i[0], i[1].reshape(i[0].shape), i[2]
+        return [ref.rmsnorm_ex(x, g, 1e-6, residual=r, scale=0.04419417382415922, mode=1)[0]]
+    if rid == "amax_sum_20ccc18dda60":
+        heads = i[2][1]
+        return [ref.scaled_bias_softmax(i[0], i[1].reshape(-1, *i[0].shape[1:]), 1.0, heads)]
+    if rid == "var_mean_80e7ff4dee7f":
+        x, r, g, b = i[0], i[1].reshape(i[0].shape), i[2], i[3]
+        return [ref.residual_layernorm(x, r, g, b, 1e-5)[1].reshape(i[4])]
+    if rid == "var_mean_ceb5c315290a":
+        x, rm, rv, g, b = i
+        return list(ref.batchnorm_nhwc_act_pad(x, g, b, rm, rv, momentum=0.1, eps=1e-3,
+                                               var_scale=1.00000996502277, act="silu",
+                                               pad_bottom=1, pad_right=1))
+    x, rm, rv, g, b = i
+    return list(ref.batchnorm_nchw_act_mean(x, g, b, rm, rv, momentum=0.1, eps=1e-5,
+                                            var_scale=1.0001594642002871, act="relu"))
+
+
 @pytest.mark.parametrize("rid", VARIANT_IDS)
 def test_family_points_vs_eager(rid, rocm_device):
     """The reference's corpus families at their transcribed shapes.json
-    points, against the eager repro on the CPU (the reference harness's own
-    gate) and, for the bf16 outputs, against the fp64 eager result."""
+    points, against the CPU oracle, the eager repro on the CPU (the
+    reference harness's own gate) and the same repro in fp64."""
     from oracle_harness import _normalize_outputs, resolve_oracle
     from repro_harness import make_inputs_from_config
     fn, inst = _load(rid)
@@ -115,13 +139,16 @@ def test_family_points_vs_eager(rid, rocm_device):
                                              for t in cpu_in]))
             exact = _normalize_outputs(inst64(*[t.double() if isinstance(t, torch.Tensor) else t
                                                for t in cpu_in]))
-        assert len(got) == len(eager)
-        for i, (g, e, x) in enumerate(zip(got, eager, exact)):
+        oracle_out = _family_oracle(rid, [t.clone() if isinstance(t, torch.Tensor) else t
+                                          for t in cpu_in])
+        assert len(got) == len(eager) == len(oracle_out)
+        for i, (g, e, x, o) in enumerate(zip(got, eager, exact, oracle_out)):
             assert g.dtype == e.dtype and g.shape == e.shape, f"{label} out{i}"
             assert g.stride() == e.stride(), f"{label} out{i} strides {g.stride()} vs {e.stride()}"
+            assert_close(g, o.reshape(e.shape), _tol(e), f"{rid}/{label} out{i} vs oracle")
             assert_close(g, e, _tol(e), f"{rid}/{label} out{i} vs eager")
             assert_close(g, x, _tol(e), f"{rid}/{label} out{i} vs fp64")
-        del cpu_in, dev_in, got, eager, exact
+        del cpu_in, dev_in, got, eager, exact, oracle_out
 
 
 # ---------------------------------------------------------------------------

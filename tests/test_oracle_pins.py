@@ -176,6 +176,128 @@ def check_batchnorm(fn):
     assert torch.allclose(rm, torch.full((2,), 0.5)) and torch.allclose(rv, torch.full((2,), 0.9))
 
 
+def from_nhwc_bits(bits, shape):
+    n, c, h, w = shape
+    return from_bits(bits, [n, h, w, c]).permute(0, 3, 1, 2)
+
+
+def exact_fraction(a, b):
+    return (a.float() == b.float()).float().mean().item()
+
+
+def check_spatial_mean(fn):
+    c = GOLDEN["spatial_mean_nhwc"]
+    x = from_nhwc_bits(c["x_nhwc"], c["shape"])
+    got = fn(x)
+    want = from_bits(c["out"], [c["shape"][0], c["shape"][1], 1, 1])
+    assert close(got, want, 1.6e-2) and exact_fraction(got, want) > 0.9, "golden"
+    # brute force: fp64 sum over positions of each (image, channel)
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(2, 5, 3, 7, generator=g) * 3).to(BF)
+    got = fn(x)
+    for i in range(2):
+        for ch in range(5):
+            v = math.fsum(x[i, ch].float().flatten().tolist()) / 21
+            assert abs(got[i, ch, 0, 0].item() - bf16_round(v)) <= 1e-2 * abs(v) + 1e-6, "brute force"
+    const = torch.full((3, 16, 4, 4), 0.625, dtype=BF)
+    assert torch.equal(fn(const), torch.full((3, 16, 1, 1), 0.625, dtype=BF)), "constant"
+
+
+def check_bias_softmax(fn):
+    c = GOLDEN["bias_softmax"]
+    b_, q, k = c["shape"]
+    heads = c["heads"]
+    x, bias = from_bits(c["x"], c["shape"]), from_bits(c["bias"], [b_ // heads, q, k])
+    got = fn(x, bias, c["scale"], heads)
+    assert close(got, from_bits(c["out"], c["shape"]), 1.6e-2), "golden"
+    # brute force, batch entry 4 (group 1), row 2
+    s = [bf16_round(bf16_round(v * c["scale"]) + bv)
+         for v, bv in zip(x[4, 2].float().tolist(), bias[4 // heads, 2].float().tolist())]
+    mx = max(s)
+    e = [math.exp(v - mx) for v in s]
+    tot = math.fsum(e)
+    assert close(got[4, 2], torch.tensor([bf16_round(v / tot) for v in e]), 1e-2), "brute force"
+    # group mapping: bias group j is -inf except column j -> out[b] one-hot at b // heads
+    groups, hh = 3, 4
+    onehot_bias = torch.full((groups, 2, 8), float("-inf"))
+    for j in range(groups):
+        onehot_bias[j, :, j] = 0
+    out = fn(torch.randn(groups * hh, 2, 8).to(BF), onehot_bias.to(BF), 1.0, hh).float()
+    for bb in range(groups * hh):
+        want = torch.zeros(2, 8)
+        want[:, bb // hh] = 1
+        assert torch.equal(out[bb], want), f"batch {bb} uses bias group {bb // hh}"
+
+
+def check_rmsnorm_ex(fn):
+    c = GOLDEN["rmsnorm_t5"]
+    rows, cols = c["shape"]
+    x, r = from_bits(c["x"], [rows, cols]), from_bits(c["residual"], [rows, cols])
+    gm = from_bits(c["gamma"], [cols])
+    y, rstd = fn(x, gm, c["eps"], residual=r, scale=c["scale"], mode=1)
+    want = from_bits(c["y"], [rows, cols])
+    assert close(y, want, 1.6e-2), "golden T5 y"
+    assert exact_fraction(y, want) > 0.97, f"golden T5 exact {exact_fraction(y, want)}"
+    assert close(rstd, f32(c["rstd"], [rows]), 1e-5), "golden rstd"
+    y0, _ = fn(x, gm, c["eps"], residual=r, mode=0)
+    want0 = from_bits(c["y_residual_rms_norm"], [rows, cols])
+    assert close(y0, want0, 1.6e-2) and exact_fraction(y0, want0) > 0.97, "golden rms_norm(x + r)"
+    # brute force row 3, T5 order
+    h = [bf16_round(a + b) for a, b in zip(x[3].float().tolist(), r[3].float().tolist())]
+    rs = 1 / math.sqrt(math.fsum(v * v for v in h) / cols + c["eps"])
+    for j in range(cols):
+        u = bf16_round(gm[j].item() * bf16_round(h[j] * rs))
+        assert abs(y[3, j].item() - bf16_round(u * c["scale"])) <= 1e-2 * abs(u * c["scale"]) + 1e-6
+    # constant rows: rstd = 1/sqrt(c^2 + eps); gamma = 1 -> y = bf16(c * rstd) * scale
+    yc, rc = fn(torch.full((2, 16), 3.0, dtype=BF), torch.ones(16, dtype=BF), 1e-6,
+                scale=0.5, mode=1)
+    assert abs(rc[0].item() - 1 / math.sqrt(9 + 1e-6)) < 1e-7
+    assert torch.equal(yc, torch.full((2, 16), 0.5, dtype=BF))
+
+
+def check_bn_nhwc(fn):
+    c = GOLDEN["bn_nhwc_silu_pad"]
+    n, ch, h, w = c["shape"]
+    x = from_nhwc_bits(c["x_nhwc"], c["shape"])
+    sm, sr, out, rm, rv = fn(x, f32(c["gamma"], [ch]), f32(c["beta"], [ch]),
+                             f32(c["running_mean"], [ch]), f32(c["running_var"], [ch]),
+                             momentum=c["momentum"], eps=c["eps"], var_scale=c["var_scale"],
+                             act="silu", pad_bottom=1, pad_right=1)
+    want = from_nhwc_bits(c["out_nhwc"], [n, ch, h + 1, w + 1])
+    assert out.shape == want.shape and out.is_contiguous(memory_format=torch.channels_last)
+    assert close(out, want, 1.6e-2), "golden out"
+    for key, v in (("save_mean", sm), ("save_rstd", sr), ("running_mean_out", rm),
+                   ("running_var_out", rv)):
+        assert close(v.flatten(), f32(c[key], [ch]), 1e-5), f"golden {key}"
+    assert (out[:, :, h:, :].float() == 0).all() and (out[:, :, :, w:].float() == 0).all(), "pad"
+    # constant channel: var 0 -> y = silu(bf16(beta)); running_var decays
+    x = torch.full((2, 4, 3, 3), 1.5, dtype=BF).contiguous(memory_format=torch.channels_last)
+    beta = torch.tensor([-1.0, 0.0, 0.5, 2.0])
+    sm, sr, out, rm, rv = fn(x, torch.ones(4), beta, torch.zeros(4), torch.ones(4), momentum=0.1,
+                             eps=1e-3, var_scale=2.0, act="silu", pad_bottom=1, pad_right=1)
+    silu = [bf16_round(v / (1 + math.exp(-v))) for v in beta.tolist()]
+    assert torch.allclose(out[:, :, :3, :3].float(), torch.tensor(silu).view(1, 4, 1, 1).expand(2, 4, 3, 3))
+    assert torch.allclose(rv, torch.full((4,), 0.9)) and torch.allclose(rm, torch.full((4,), 0.15))
+
+
+def check_bn_nchw(fn):
+    c = GOLDEN["bn_nchw_relu_mean"]
+    n, ch, h, w = c["shape"]
+    x = from_bits(c["x"], c["shape"])
+    sm, sr, out, rm, rv = fn(x, f32(c["gamma"], [ch]), f32(c["beta"], [ch]),
+                             f32(c["running_mean"], [ch]), f32(c["running_var"], [ch]),
+                             momentum=c["momentum"], eps=c["eps"], var_scale=c["var_scale"],
+                             act="relu")
+    assert close(out, from_bits(c["out"], [n, ch]), 1.6e-2), "golden out"
+    for key, v in (("save_mean", sm), ("save_rstd", sr), ("running_mean_out", rm),
+                   ("running_var_out", rv)):
+        assert close(v.flatten(), f32(c[key], [ch]), 1e-5), f"golden {key}"
+    x = torch.full((3, 2, 2, 2), -4.0, dtype=BF)
+    sm, sr, out, rm, rv = fn(x, torch.ones(2), torch.tensor([-0.5, 0.75]), torch.zeros(2),
+                             torch.ones(2), momentum=0.1, eps=1e-5, var_scale=1.5, act="relu")
+    assert torch.equal(out.float(), torch.tensor([[0.0, 0.75]] * 3)), "relu(beta) on constant channels"
+
+
 CHECKS = {
     "row_mean": (check_row_mean, ref.row_mean),
     "bias_gelu": (check_bias_gelu, ref.bias_gelu_nchw_to_nhwc),
@@ -183,6 +305,11 @@ CHECKS = {
     "residual_layernorm": (check_residual_layernorm, ref.residual_layernorm),
     "rmsnorm": (check_rmsnorm, ref.rmsnorm),
     "batchnorm": (check_batchnorm, ref.batchnorm_train),
+    "spatial_mean": (check_spatial_mean, ref.spatial_mean_nhwc),
+    "bias_softmax": (check_bias_softmax, ref.scaled_bias_softmax),
+    "rmsnorm_ex": (check_rmsnorm_ex, ref.rmsnorm_ex),
+    "bn_nhwc": (check_bn_nhwc, ref.batchnorm_nhwc_act_pad),
+    "bn_nchw": (check_bn_nchw, ref.batchnorm_nchw_act_mean),
 }
 
 
@@ -243,7 +370,45 @@ def _bn_no_relu(x, g, b, rm, rv, *, momentum, eps, relu=True):
     return ref.batchnorm_train(x, g, b, rm, rv, momentum=momentum, eps=eps, relu=False)
 
 
+def _spatial_mean_wrong_divisor(x):
+    p = x.shape[2] * x.shape[3]
+    return (ref.spatial_mean_nhwc(x).float() * p / (p - 1)).to(BF)
+
+
+def _bias_softmax_groups_reversed(x, bias, scale, heads):
+    return ref.scaled_bias_softmax(x, bias.flip(0).contiguous(), scale, heads)
+
+
+def _rmsnorm_ex_t5_order_dropped(x, g, eps, *, residual=None, scale=1.0, mode=0):
+    return ref.rmsnorm_ex(x, g, eps, residual=residual, scale=scale, mode=0)
+
+
+def _rmsnorm_ex_no_residual(x, g, eps, *, residual=None, scale=1.0, mode=0):
+    return ref.rmsnorm_ex(x, g, eps, residual=None, scale=scale, mode=mode)
+
+
+def _bn_nhwc_pad_top_left(x, *a, **k):
+    sm, sr, out, rm, rv = ref.batchnorm_nhwc_act_pad(x, *a, **k)
+    return sm, sr, out.roll((1, 1), (2, 3)).contiguous(memory_format=torch.channels_last), rm, rv
+
+
+def _bn_nhwc_true_bessel(x, g, b, rm, rv, *, var_scale, **k):
+    n = x.numel() / x.shape[1]
+    return ref.batchnorm_nhwc_act_pad(x, g, b, rm, rv, var_scale=n / (n - 1), **k)
+
+
+def _bn_nchw_mean_before_relu(x, *a, act=None, **k):
+    return ref.batchnorm_nchw_act_mean(x, *a, act=None, **k)
+
+
 MUTANTS = [
+    ("spatial_mean", _spatial_mean_wrong_divisor),
+    ("bias_softmax", _bias_softmax_groups_reversed),
+    ("rmsnorm_ex", _rmsnorm_ex_t5_order_dropped),
+    ("rmsnorm_ex", _rmsnorm_ex_no_residual),
+    ("bn_nhwc", _bn_nhwc_pad_top_left),
+    ("bn_nhwc", _bn_nhwc_true_bessel),
+    ("bn_nchw", _bn_nchw_mean_before_relu),
     ("row_mean", _mean_wrong_divisor),
     ("bias_gelu", _gelu_drops_bias),
     ("bias_gelu", _gelu_wrong_layout),
@@ -290,3 +455,39 @@ def test_oracle_matches_repro_eager_modules():
             for i, (g, w) in enumerate(zip(got, want)):
                 tol = 1.6e-2 if w.dtype == BF else 1e-5
                 assert close(g, w, tol), f"{rid}/{label} out{i}"
+
+
+def test_oracle_matches_family_repros():
+    """The oracle's family functions against the family repro modules (eager
+    ATen, the reference graphs' op order) on small inputs of each family's
+    structure."""
+    from conftest import CANONICAL
+    from oracle_harness import get_repro_instance
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(3, 40, 5, 6, generator=g).to(BF).contiguous(memory_format=torch.channels_last)
+    want = get_repro_instance(CANONICAL / "mean_c9e1a8113328")(x)
+    assert close(ref.spatial_mean_nhwc(x), want, 1.6e-2)
+    x, r = torch.randn(6, 64, generator=g).to(BF), torch.randn(2, 3, 64, generator=g).to(BF)
+    gm = torch.randn(64, generator=g).to(BF)
+    want = get_repro_instance(CANONICAL / "mean_4462ce967d63")(x, r, gm, [2, 3, 64], [6, 64])
+    y, _ = ref.rmsnorm_ex(x, gm, 1e-6, residual=r.view(6, 64), scale=0.04419417382415922, mode=1)
+    assert close(y, want, 1.6e-2) and exact_fraction(y, want) > 0.97
+    x, bias = torch.randn(8, 5, 12, generator=g).to(BF), torch.randn(2, 1, 5, 12, generator=g).to(BF)
+    want = get_repro_instance(CANONICAL / "amax_sum_20ccc18dda60")(x, bias, [2, 4, 5, 12], [8, 5, 12])
+    assert close(ref.scaled_bias_softmax(x, bias.view(2, 5, 12), 1.0, 4), want, 1.6e-2)
+    for rid, fmt, call in (
+            ("var_mean_ceb5c315290a", torch.channels_last,
+             lambda x, rm, rv, w, b: ref.batchnorm_nhwc_act_pad(
+                 x, w, b, rm, rv, momentum=0.1, eps=1e-3, var_scale=1.00000996502277,
+                 act="silu", pad_bottom=1, pad_right=1)),
+            ("var_mean_mean_19ffdb35cc67", torch.contiguous_format,
+             lambda x, rm, rv, w, b: ref.batchnorm_nchw_act_mean(
+                 x, w, b, rm, rv, momentum=0.1, eps=1e-5, var_scale=1.0001594642002871,
+                 act="relu"))):
+        x = (2 * torch.randn(3, 8, 5, 4, generator=g) + 0.5).to(BF).contiguous(memory_format=fmt)
+        rm, rv, w, b = (torch.randn(8, generator=g), torch.rand(8, generator=g) + 0.5,
+                        torch.randn(8, generator=g), torch.randn(8, generator=g))
+        got = call(x, rm, rv, w, b)
+        want = get_repro_instance(CANONICAL / rid)(x, rm.clone(), rv.clone(), w, b)
+        for i, (a_, b_) in enumerate(zip(got, want)):
+            assert close(a_, b_, 1.6e-2 if b_.dtype == BF else 1e-5), f"{rid} out{i}"
