@@ -14,12 +14,13 @@
 // var_scale is the graph's Bessel constant (N/(N-1) of the shape the graph
 // was captured at), passed through unchanged.
 //
-// Three launches, no atomics, deterministic:
+// Three launches (two for NCHW), no atomics, deterministic:
 //   1. partial statistics per slice of the reduction axis -> workspace
 //      (mean, M2) per (slice, channel);
-//   2. one wave per channel merges the slices (Chan's formula in fp64, a
-//      fixed butterfly order) and writes save_mean, save_rstd and the running
-//      statistics;
+//   2. a per-channel merge of the slices in fp64 (a fixed order) that writes
+//      save_mean, save_rstd and the running statistics -- its own launch for
+//      channels-last; folded into the epilogue's workgroups for NCHW, whose
+//      64 channels each workgroup merges itself;
 //   3. the normalise + activation pass (padded store / spatial mean).
 // HBM-bound: x is read twice and the output written once.
 #include <algorithm>
@@ -267,7 +268,20 @@ __global__ __launch_bounds__(256) void bn_nhwc_apply_pad_scalar(
 // ---------------------------------------------------------------------------
 constexpr int kNchwImages = 4;
 constexpr int kNchwChannels = 64;
-constexpr int64_t kNchwMaxStagedHw = 92;  // LDS: 4 x 64 x 92 x 2 B + 2 KiB < 48 KiB
+constexpr int64_t kNchwMaxStagedHw = 80;  // LDS: 4 x 64 x 80 x 2 B + 6 KiB < 48 KiB
+
+// What the NCHW epilogue pass needs to merge its channels' slice statistics
+// itself (the statistics pass wrote (mean, M2) per (channel, slice of
+// kNchwImages images), channel-major).
+struct NchwMerge {
+  const float2* part;
+  int64_t slices;
+  float* running_mean;
+  float* running_var;
+  float* save_mean;
+  float* save_rstd;
+  float momentum, eps, var_scale;
+};
 
 template <bool STAGED, bool LAST_USE>
 __device__ __forceinline__ const uint16_t* nchw_stage(const uint16_t* __restrict__ x,
@@ -293,13 +307,16 @@ __device__ __forceinline__ const uint16_t* nchw_stage(const uint16_t* __restrict
 // MODE 0: per (channel, slice of kNchwImages images) partial (mean, M2),
 //         exact two-pass statistics of each (image, channel) segment merged
 //         over the images in order.
-// MODE 1: out[n, c] = bf16(sum_hw act(bn(x[n, c, hw])) / HW).
+// MODE 1: the workgroup first merges the slice partials of its 64 channels
+//         (fp64 sums about the shift m_0, slices strided over the waves, the
+//         waves added in order: the same result in every workgroup; the
+//         workgroups of the first image group write save_* and the running
+//         statistics), then out[n, c] = bf16(sum_hw act(bn(x[n, c, hw])) / HW).
 template <int MODE, bool STAGED>
 __global__ __launch_bounds__(kNchwImages * kWave) void bn_nchw_small_hw(
-    const uint16_t* __restrict__ x, float2* __restrict__ part, const float* __restrict__ mean,
-    const float* __restrict__ rstd, const float* __restrict__ gamma,
-    const float* __restrict__ beta, uint16_t* __restrict__ out, int64_t N, int64_t C,
-    int64_t HW, int act) {
+    const uint16_t* __restrict__ x, float2* __restrict__ part, NchwMerge mg,
+    const float* __restrict__ gamma, const float* __restrict__ beta,
+    uint16_t* __restrict__ out, int64_t N, int64_t C, int64_t HW, int act) {
   extern __shared__ uint16_t slab[];  // [kNchwImages][64 * HW] when STAGED
   __shared__ float2 stats[kNchwImages][kNchwChannels];
   const int lane = threadIdx.x & (kWave - 1);
@@ -334,8 +351,47 @@ __global__ __launch_bounds__(kNchwImages * kWave) void bn_nchw_small_hw(
       part[c * static_cast<int64_t>(gridDim.y) + blockIdx.y] = make_float2(mm, mq);
     }
   } else {
+    __shared__ double red[kNchwImages][kNchwChannels][3];
+    const float2* pc = mg.part + (c < C ? c : C - 1) * mg.slices;
+    const double K = static_cast<double>(pc[0].x);
+    {
+      double n = 0.0, s1 = 0.0, s2 = 0.0;
+      for (int64_t s = w; s < mg.slices; s += kNchwImages) {
+        const double cnt = static_cast<double>(
+            (std::min<int64_t>(N, (s + 1) * kNchwImages) - s * kNchwImages) * HW);
+        const float2 pv = pc[s];
+        const double d = static_cast<double>(pv.x) - K;
+        n += cnt;
+        s1 = __builtin_fma(cnt, d, s1);
+        s2 += __builtin_fma(cnt * d, d, static_cast<double>(pv.y));
+      }
+      red[w][lane][0] = n;
+      red[w][lane][1] = s1;
+      red[w][lane][2] = s2;
+    }
+    __syncthreads();
+    double n = 0.0, s1 = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int k = 0; k < kNchwImages; ++k) {
+      n += red[k][lane][0];
+      s1 += red[k][lane][1];
+      s2 += red[k][lane][2];
+    }
+    const double dm = s1 / n;
+    const float mc = static_cast<float>(K + dm);
+    const float var_f = static_cast<float>(std::max(0.0, s2 - s1 * dm) / n);
+    const float rc = 1.0f / __builtin_sqrtf(__fadd_rn(var_f, mg.eps));
+    if (blockIdx.y == 0 && w == 0 && c < C) {
+      mg.save_mean[c] = mc;
+      mg.save_rstd[c] = rc;
+      const float keep = 1.0f - mg.momentum;
+      mg.running_mean[c] =
+          __fadd_rn(__fmul_rn(mc, mg.momentum), __fmul_rn(mg.running_mean[c], keep));
+      mg.running_var[c] = __fadd_rn(__fmul_rn(__fmul_rn(var_f, mg.var_scale), mg.momentum),
+                                    __fmul_rn(mg.running_var[c], keep));
+    }
     if (!valid) return;
-    const float mc = mean[c], rc = rstd[c], gc = gamma[c], bc = beta[c];
+    const float gc = gamma[c], bc = beta[c];
     float sum = 0.f;
     for (int64_t j = 0; j < HW; ++j) sum += bn_act(bf16_to_f32(seg[j]), mc, rc, gc, bc, act);
     out[img * C + c] = static_cast<uint16_t>(pack_bf16x2(sum / static_cast<float>(HW), 0.f) & 0xffffu);
@@ -564,22 +620,19 @@ extern "C" int hipo_batchnorm_nchw_act_mean_bf16(
                   static_cast<unsigned>(slices));
   const dim3 block(kNchwImages * kWave);
   const size_t lds = staged ? static_cast<size_t>(kNchwImages * kNchwChannels * hw) * 2 : 0;
+  const NchwMerge none{};
+  const NchwMerge mg{part, slices, running_mean, running_var, save_mean, save_rstd,
+                     momentum, eps, var_scale};
   if (staged) {
-    bn_nchw_small_hw<0, true><<<grid, block, lds, stream>>>(x, part, nullptr, nullptr, nullptr,
-                                                            nullptr, nullptr, n, c, hw, act);
+    bn_nchw_small_hw<0, true><<<grid, block, lds, stream>>>(x, part, none, nullptr, nullptr,
+                                                            nullptr, n, c, hw, act);
+    bn_nchw_small_hw<1, true><<<grid, block, lds, stream>>>(x, nullptr, mg, gamma, beta, out,
+                                                            n, c, hw, act);
   } else {
-    bn_nchw_small_hw<0, false><<<grid, block, 0, stream>>>(x, part, nullptr, nullptr, nullptr,
-                                                           nullptr, nullptr, n, c, hw, act);
-  }
-  bn_finalize<<<dim3(static_cast<unsigned>(c)), dim3(kFinalThreads), 0, stream>>>(
-      part, slices, n, kNchwImages, hw, running_mean, running_var, save_mean, save_rstd,
-      momentum, eps, var_scale);
-  if (staged) {
-    bn_nchw_small_hw<1, true><<<grid, block, lds, stream>>>(x, nullptr, save_mean, save_rstd,
-                                                            gamma, beta, out, n, c, hw, act);
-  } else {
-    bn_nchw_small_hw<1, false><<<grid, block, 0, stream>>>(x, nullptr, save_mean, save_rstd,
-                                                           gamma, beta, out, n, c, hw, act);
+    bn_nchw_small_hw<0, false><<<grid, block, 0, stream>>>(x, part, none, nullptr, nullptr,
+                                                           nullptr, n, c, hw, act);
+    bn_nchw_small_hw<1, false><<<grid, block, 0, stream>>>(x, nullptr, mg, gamma, beta, out,
+                                                           n, c, hw, act);
   }
   return check_launch(what);
 }
