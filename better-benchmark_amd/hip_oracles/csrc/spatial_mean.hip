@@ -8,8 +8,9 @@
 // see spatial_plan).  A workgroup of T threads (T a multiple of G) reduces
 // the positions [p0, p1) of one image: thread t
 // owns group t % G and positions p0 + t / G + k * (T / G), so each load
-// instruction of the workgroup covers T / G whole rows, T * 16 contiguous
-// bytes, and each thread keeps 4 loads in flight.  The T / G partial sums of
+// instruction of the workgroup covers T / G rows -- whole rows (T * 16
+// contiguous bytes), or each row's 1 KiB of the channel block -- and each
+// thread keeps 4 loads in flight.  The T / G partial sums of
 // a group meet in LDS and the first G threads add them in a fixed order.
 // With one position slice per image the result is written as bf16 directly;
 // with S > 1 slices (more workgroups than images alone give) each slice
