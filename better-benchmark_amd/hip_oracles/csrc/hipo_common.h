@@ -52,6 +52,7 @@ typedef float float2_t __attribute__((ext_vector_type(2)));
 // 16-byte vectors as native clang vectors (the non-temporal load/store
 // builtins accept these, not HIP's struct vector types).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 inline bool aligned16(const void* p) {

@@ -6,15 +6,20 @@
 // When `scale` is a power of two, x * scale is exact in fp32 and the first
 // rounding is the identity, so it is skipped.
 //
-// Layout (row_layout.h): W waves per row (W = 1 for K = 1024: one wave
-// holds a 2 KiB row), rows held in registers, non-temporal 16-byte
-// streaming accesses for x and out; the mask row (mask[q, :], q = row % Q)
-// is re-read by every batch entry and stays cache-resident.  Row max and
-// row sum: DPP within a wave, then a fixed-order combine of the W wave
-// results through LDS.  Rows of K <= 512 take the short-row kernel: L lanes
-// per row, 64 / L rows per access instruction, 2 KiB of x per wave,
-// reductions within lane segments, no LDS.  HBM-bound: algorithmic
-// bytes per element = 2 (read) + 2 (write), plus the mask once.
+// Layout: rows held in registers, non-temporal 16-byte streaming accesses
+// for x and out; the mask row (mask[q, :], q = row % Q) is re-read by every
+// batch entry and stays cache-resident.  Row max and row sum: DPP within a
+// wave, then a fixed-order combine of the wave results through LDS.  Three
+// kernels by row length:
+//   K <= 512: L lanes per row, 64 / L rows per access instruction, 2 KiB of
+//     x per wave, reductions within lane segments, no LDS;
+//   K = 1024 or 2048 (config [384, 1024, 1024]): 1 KiB of x per wave, the
+//     rows of one q for 4 / W consecutive batch entries in a 256-thread
+//     workgroup, their shared mask row loaded once and staged through LDS;
+//   otherwise (or a per-batch mask the grouping cannot share): the
+//     row_layout.h plan, W waves per row, 2 KiB per wave.
+// HBM-bound: algorithmic bytes per element = 2 (read) + 2 (write), plus the
+// mask once.
 #include "row_layout.h"
 
 namespace hipo {
@@ -207,6 +212,162 @@ void launch_short(bool round_scale, dim3 grid, hipStream_t stream, const uint16_
   }
 }
 
+// Rows of exactly K = 1024 or 2048 (KC, a compile-time constant):
+// 256-thread workgroups, W = KC / 512 waves per row (one 16-byte group per
+// lane: 1 KiB of x per wave, no idle lanes), NR = 4 / W rows per workgroup.
+// Workgroup (q, y, z) of the 3-D grid takes the rows (b0 + i) * Q + q,
+// i < NR, b0 = (z * gy + y) * NR: the same q of NR consecutive batch
+// entries, which share one mask row.  z is the mask's batch group (offset
+// z * mask_batch_stride; a single z when the mask is broadcast over batch)
+// and gy its workgroups along y, so the kernel does no integer division; x
+// is fastest, so dispatch order walks q in memory order.  The mask row
+// (2 KC bytes, 2 KC / 256 per thread) is loaded once per workgroup, issued
+// before the x load, and staged through LDS; row max and sum combine the W
+// wave results through LDS in a fixed order.  Rows past the batch end (NR
+// not dividing a broadcast batch) re-read the last batch entry and store
+// nothing.
+// Measured on MI355X (graph loop, rotating buffers, 2 B read + 2 B written
+// per element, % of 8 TB/s), [384, 1024, 1024]: one wave per row with every
+// wave reading its own mask row (the row-plan kernel) 261.6-263.5 us
+// (76.6-77.0 %); this layout with the block index split by division 272.2
+// us, with a 3-D grid and a runtime K 252.7-255.0 us, with K fixed 245.4
+// us = a flat copy of the same bytes; 512-thread workgroups (NR = 4 or 8)
+// 260-267 us.  [192, 1024, 2048]: 258.7-260.1 us against 253.3 us.  With a
+// runtime K and idle lanes (K = 776, 1032) the layout lost 8-15 % to the
+// row-plan kernel, so other row lengths stay there.
+template <int KC, bool ROUND_SCALE>
+__global__ __launch_bounds__(256) void masked_softmax_shared_mask(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
+    uint16_t* __restrict__ out, uint32_t batch, uint32_t Q, uint32_t gy,
+    int64_t mask_stride, int64_t mask_batch_stride, float scale) {
+  constexpr int W = KC / 512;
+  constexpr int NR = 4 / W;
+  static_assert(W * NR * kWave == 256 && W * kWave * kRowGroup == KC, "full rows");
+  constexpr int kStageWords = KC / 512;  // 32-bit words of the mask row per thread
+  __shared__ uint32_t mrow[KC / 2];
+  __shared__ float pmax[W * NR], psum[W * NR];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int w = wave % W;
+  const int rr = wave / W;
+  const uint32_t q = blockIdx.x;
+  const uint32_t b = (blockIdx.z * gy + blockIdx.y) * NR + rr;
+  const bool row_ok = b < batch;
+  const int64_t row = static_cast<int64_t>(row_ok ? b : batch - 1) * Q + q;
+
+  const uint16_t* mr = mask + blockIdx.z * mask_batch_stride +
+                       static_cast<int64_t>(q) * mask_stride;
+  const int st = static_cast<int>(threadIdx.x) * kStageWords;  // first word staged
+  uint32_t mval[kStageWords];
+  if constexpr (kStageWords == 2) {
+    const u32x2_t v = *reinterpret_cast<const u32x2_t*>(mr + 2 * st);
+    mval[0] = v[0];
+    mval[1] = v[1];
+  } else {
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(mr + 2 * st);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mval[i] = v[i];
+  }
+  const int col = (w * kWave + lane) * kRowGroup;
+  const u32x4_t xv =
+      __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + row * KC + col));
+#pragma unroll
+  for (int i = 0; i < kStageWords; ++i) mrow[st + i] = mval[i];
+  __syncthreads();
+  const u32x4_t mv = *reinterpret_cast<const u32x4_t*>(&mrow[col / 2]);
+
+  float s[8];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    float a0 = bf16lo(xv[d]) * scale;
+    float a1 = bf16hi(xv[d]) * scale;
+    if (ROUND_SCALE) {
+      const uint32_t r = pack_bf16x2(a0, a1);
+      a0 = bf16lo(r);
+      a1 = bf16hi(r);
+    }
+    const uint32_t t = pack_bf16x2(a0 + bf16lo(mv[d]), a1 + bf16hi(mv[d]));
+    s[2 * d] = bf16lo(t);
+    s[2 * d + 1] = bf16hi(t);
+    m = fmaxf(m, fmaxf(s[2 * d], s[2 * d + 1]));
+  }
+  m = wave_max(m);
+  if (lane == 0) pmax[wave] = m;
+  __syncthreads();
+  m = pmax[rr * W];
+#pragma unroll
+  for (int k = 1; k < W; ++k) m = fmaxf(m, pmax[rr * W + k]);
+
+  // (-inf) - (-inf) gives NaN for an all-masked row, as the eager formula.
+  const float ml = m * kLog2e;
+  float sum = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    s[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], kLog2e, -ml));
+    sum += s[e];
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) psum[wave] = sum;
+  __syncthreads();
+  sum = psum[rr * W];
+#pragma unroll
+  for (int k = 1; k < W; ++k) sum += psum[rr * W + k];
+  const float inv = 1.0f / sum;
+
+  u32x4_t o;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) o[d] = pack_bf16x2(s[2 * d] * inv, s[2 * d + 1] * inv);
+  if (row_ok) __builtin_nontemporal_store(o, reinterpret_cast<u32x4_t*>(out + row * KC + col));
+}
+
+// Launch shape of the shared-mask kernel: its row length (1024 or 2048; 0
+// when the kernel does not apply) and the 3-D grid.  It does not apply to
+// other K, to a per-batch mask whose heads groups NR = 4 / W does not
+// divide, or to grids beyond the y / z limits.
+struct SharedMaskPlan {
+  int k = 0;
+  uint32_t gy = 0;  // workgroups along y per mask batch group
+  dim3 grid;
+};
+
+SharedMaskPlan shared_mask_plan(int64_t batch, int64_t Q, int64_t K, int64_t mbs,
+                                int64_t heads) {
+  SharedMaskPlan plan;
+  if ((K != 1024 && K != 2048) || Q > 0x7fffffff) return plan;
+  const int nr = K == 1024 ? 2 : 1;
+  int64_t gy, gz;
+  if (mbs == 0) {
+    gy = (batch + nr - 1) / nr;
+    gz = 1;
+  } else {
+    if (heads % nr != 0) return plan;
+    gy = heads / nr;
+    gz = batch / heads;
+  }
+  if (gy > 65535 || gz > 65535) return plan;
+  plan.k = static_cast<int>(K);
+  plan.gy = static_cast<uint32_t>(gy);
+  plan.grid = dim3(static_cast<unsigned>(Q), static_cast<unsigned>(gy),
+                   static_cast<unsigned>(gz));
+  return plan;
+}
+
+template <int KC>
+void launch_shared_mask(bool round_scale, const SharedMaskPlan& plan, hipStream_t stream,
+                        const uint16_t* x, const uint16_t* mask, uint16_t* out,
+                        int64_t batch, int64_t Q, int64_t ms, int64_t mbs, float scale) {
+  const auto bt = static_cast<uint32_t>(batch);
+  const auto q = static_cast<uint32_t>(Q);
+  if (round_scale) {
+    masked_softmax_shared_mask<KC, true><<<plan.grid, dim3(256), 0, stream>>>(
+        x, mask, out, bt, q, plan.gy, ms, mbs, scale);
+  } else {
+    masked_softmax_shared_mask<KC, false><<<plan.grid, dim3(256), 0, stream>>>(
+        x, mask, out, bt, q, plan.gy, ms, mbs, scale);
+  }
+}
+
 // Any K / alignment: one wave per row, three passes over the row (max, sum,
 // write) with scalar accesses.
 __global__ __launch_bounds__(256) void masked_softmax_rows_scalar(
@@ -305,6 +466,17 @@ int softmax_impl(const uint16_t* x, const uint16_t* mask, uint16_t* out, int64_t
       default: HIPO_SHORT(64); break;
     }
 #undef HIPO_SHORT
+  } else if (const SharedMaskPlan sp = vec && rows < (int64_t{1} << 31)
+                                            ? shared_mask_plan(batch, q, k, mask_batch_stride, heads)
+                                            : SharedMaskPlan{};
+             sp.k > 0) {
+    if (sp.k == 1024) {
+      launch_shared_mask<1024>(round_scale, sp, stream, x, mask, out, batch, q, mask_row_stride,
+                               mask_batch_stride, scale);
+    } else {
+      launch_shared_mask<2048>(round_scale, sp, stream, x, mask, out, batch, q, mask_row_stride,
+                               mask_batch_stride, scale);
+    }
   } else if (vec) {
     const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);

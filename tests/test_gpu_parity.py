@@ -304,6 +304,43 @@ def test_softmax_short_rows(rocm_device):
     assert_close(got.float().sum(-1), torch.ones(64, 256), 1e-2, "row sums")
 
 
+def test_softmax_mid_rows(rocm_device):
+    """512 < K <= 2048.  K = 1024 and 2048 take the shared-mask kernel (the
+    rows of one q for 2 or 1 batch entries per workgroup, their mask row
+    staged once through LDS), other K the row-plan kernel: odd batches that
+    leave the workgroup's last row empty, rounded scales, fully masked rows,
+    per-group biases that can share (heads even, or K = 2048) and that
+    cannot (heads odd at K = 1024: the row-plan kernel)."""
+    import hip_oracles
+    import oracle as ref
+    bf = torch.bfloat16
+    for k in (520, 640, 1000, 1024, 1032, 1536, 2040, 2048):
+        for b, q, scale in ((3, 7, 0.125), (1, 1, 1.0), (4, 33, 0.3)):
+            what = f"mid softmax b={b} q={q} k={k} scale={scale}"
+            print(f"[mid] {what}", flush=True)
+            g = torch.Generator().manual_seed(k * 100 + q)
+            x = (2 * torch.randn(b, q, k, generator=g)).to(bf)
+            m = torch.triu(torch.full((q, k), float("-inf")), 1 + k // 3).to(bf)
+            m[q // 2] = float("-inf")                      # one fully masked row -> NaN
+            got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), m.to(rocm_device), scale)
+            want = ref.scaled_masked_softmax(x, m, scale)
+            assert_close(got, want, BF16_TOL, what)
+            assert torch.isnan(got[:, q // 2].float()).all().item(), what + " masked row"
+    for b, heads, q, k in ((12, 4, 9, 768), (9, 3, 9, 768), (6, 1, 5, 1024), (4, 2, 6, 2048),
+                           (3, 3, 4, 1536), (8, 2, 7, 1024), (6, 6, 3, 1024), (3, 1, 5, 2048)):
+        what = f"mid bias softmax b={b} heads={heads} q={q} k={k}"
+        print(f"[mid] {what}", flush=True)
+        g = torch.Generator().manual_seed(b * heads + k)
+        x = torch.randn(b, q, k, generator=g).to(bf)
+        bias = torch.randn(b // heads, q, k, generator=g).to(bf)
+        got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), 1.0, heads)
+        assert_close(got, ref.scaled_bias_softmax(x, bias, 1.0, heads), BF16_TOL, what)
+        # each batch entry's rows against a direct fp32 softmax of its own bias group
+        want = torch.softmax((x.float().view(b // heads, heads, q, k) + bias.float().unsqueeze(1))
+                             .to(bf).float(), -1).to(bf).view(b, q, k)
+        assert_close(got, want, BF16_TOL, what + " vs torch")
+
+
 def test_norm_closed_forms(rocm_device):
     import hip_oracles
     bf = torch.bfloat16
