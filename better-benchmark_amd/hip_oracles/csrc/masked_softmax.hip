@@ -125,9 +125,9 @@ __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
 // Measured on MI355X (steady state, % of 8 TB/s): K = 256 with 16-head
 // bias groups 77.9 % (the long-row layout: 34 %), K = 512 79.6 %, K = 128
 // and 64 about 80 %; V = 1 or 4 and 512-thread workgroups were 1-7 points
-// lower.  For K = 1024 one wave per row with 2 groups per lane measured the
-// same as the long-row kernel (75.7-76.2 % against 76.6 %), so longer rows
-// stay there.
+// lower.  For K = 1024 this layout (one wave per row, 2 groups per lane)
+// measured the same as the row-plan kernel (75.7-76.2 % against 76.6 %), so
+// longer rows use the kernels below.
 constexpr int kShortV = 2;
 constexpr int kShortThreads = 256;
 
