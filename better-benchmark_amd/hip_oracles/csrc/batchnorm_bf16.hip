@@ -493,7 +493,10 @@ int64_t gcd64(int64_t a, int64_t b) {
 // 112, 112]): 512-row slices, at most 512 of them, 8 non-temporal loads in
 // flight per thread: 15.2 / 49.9 us; at most 1024 / 256 / 128 slices:
 // 61.8 / 53.6 / 84.8 us on the second shape; 256-row slices, 4 or 16 loads,
-// or cached loads: 21-27 / 55-64 us.
+// or cached loads: 21-27 / 55-64 us.  Whole call (three launches, graph
+// loop): 44.0 / 160.2 us as planned; 128- or 64-row slices with up to 1024
+// or 2048 of them 71-100 / 167-184 us; 2 or 1 rows per thread in the
+// epilogue instead of kApplyUnroll = 4: 44.1-51.2 / 168.6-203.5 us.
 struct NhwcPlan {
   int threads = 0;
   int64_t slice_len = 0;
