@@ -53,17 +53,33 @@ struct TileGeom {
   int c_tiles, hw_tiles, ntiles;  // ntiles < 2^31 (checked on the host)
 };
 
+// GRID3: the grid carries the tile coordinates (x = group of kWavesPerBlock
+// channel tiles, y = position tile, z = image), so a workgroup starts its
+// loads without integer divisions (66.1 against 66.6 us at config 2); the
+// dispatch order is the 1-D numbering's.  Otherwise (grids past the y / z
+// limits) the block index is split by division.
+template <bool GRID3>
 __global__ __launch_bounds__(kBlockThreads) void bias_gelu_nchw_to_nhwc_tiles(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ out, TileGeom g) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int t = __builtin_amdgcn_readfirstlane(
-      static_cast<int>(blockIdx.x) * kWavesPerBlock + static_cast<int>(threadIdx.x >> 6));
-  if (t >= g.ntiles) return;  // wave-uniform; the kernel has no barrier
-  const int ct = t % g.c_tiles;
-  const int rest = t / g.c_tiles;
-  const int ht = rest % g.hw_tiles;
-  const int64_t img = rest / g.hw_tiles;
+  int ct, ht;
+  int64_t img;
+  if constexpr (GRID3) {
+    ct = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * kWavesPerBlock +
+                                        static_cast<int>(threadIdx.x >> 6));
+    if (ct >= g.c_tiles) return;  // wave-uniform; the kernel has no barrier
+    ht = blockIdx.y;
+    img = blockIdx.z;
+  } else {
+    const int t = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(blockIdx.x) * kWavesPerBlock + static_cast<int>(threadIdx.x >> 6));
+    if (t >= g.ntiles) return;  // wave-uniform
+    ct = t % g.c_tiles;
+    const int rest = t / g.c_tiles;
+    ht = rest % g.hw_tiles;
+    img = rest / g.hw_tiles;
+  }
   const int64_t c0 = static_cast<int64_t>(ct) * kTileC + (lane >> 3) * 8;
   const int64_t p0 = static_cast<int64_t>(ht) * kTileHw + (lane & 7) * 8;
   // Lanes outside a partial tile load from the tile's first block (always in
@@ -149,9 +165,17 @@ extern "C" int hipo_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x,
     g.c_tiles = static_cast<int>(c_tiles);
     g.hw_tiles = static_cast<int>(hw_tiles);
     g.ntiles = static_cast<int>(ntiles);
-    const int64_t blocks = (ntiles + kWavesPerBlock - 1) / kWavesPerBlock;
-    bias_gelu_nchw_to_nhwc_tiles<<<dim3(static_cast<unsigned>(blocks)),
-                                   dim3(kBlockThreads), 0, stream>>>(x, bias, out, g);
+    const int64_t c_groups = (c_tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (hw_tiles <= 65535 && n <= 65535) {
+      const dim3 grid(static_cast<unsigned>(c_groups), static_cast<unsigned>(hw_tiles),
+                      static_cast<unsigned>(n));
+      bias_gelu_nchw_to_nhwc_tiles<true><<<grid, dim3(kBlockThreads), 0, stream>>>(x, bias, out,
+                                                                                  g);
+    } else {
+      const int64_t blocks = (ntiles + kWavesPerBlock - 1) / kWavesPerBlock;
+      bias_gelu_nchw_to_nhwc_tiles<false><<<dim3(static_cast<unsigned>(blocks)),
+                                            dim3(kBlockThreads), 0, stream>>>(x, bias, out, g);
+    }
   } else {
     const int64_t total = n * c * hw;
     int64_t blocks = (total + 255) / 256;

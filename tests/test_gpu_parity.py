@@ -195,7 +195,9 @@ def test_bias_gelu_edges(rocm_device):
     assert out[0, 0, 0, 4].item() == float("inf") and math.isnan(out[0, 0, 0, 5].float().item())
     assert_close(out[..., 6:], want[..., 6:], BF16_TOL, "gelu +-0.5")
     # shapes off the vector path (C % 8, HW % 8) and partial channel groups
-    for shape in [(2, 5, 3, 3), (1, 264, 2, 4), (3, 16, 1, 8)]:
+    # (65537, 8, 1, 8): more images than a grid's z dimension holds, so the
+    # tile kernel takes its 1-D numbering instead of the 3-D grid
+    for shape in [(2, 5, 3, 3), (1, 264, 2, 4), (3, 16, 1, 8), (65537, 8, 1, 8)]:
         g = torch.Generator().manual_seed(sum(shape))
         x = torch.randn(shape, generator=g).to(bf)
         b = (0.1 * torch.randn(shape[1], generator=g)).to(bf)
