@@ -83,6 +83,27 @@ __device__ __forceinline__ float round_bf16(float v) {
   return bf16lo(pack_bf16x2(v, 0.0f));
 }
 
+// Division of numerators n < 2^31 by a runtime divisor d >= 1 as
+// (n * magic) >> shift, shift = 31 + ceil(log2 d), magic = ceil(2^shift / d):
+// exact, since magic * d - 2^shift = e <= d and n * e < 2^shift.  The
+// hardware has no integer divide; this replaces a ~30-instruction sequence
+// with one 64-bit multiply where a kernel divides before its first load.
+struct DivMagic {
+  uint32_t magic;
+  int shift;
+};
+
+inline DivMagic div_magic(uint32_t d) {
+  int l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  const int shift = 31 + l;
+  return DivMagic{static_cast<uint32_t>(((uint64_t{1} << shift) + d - 1) / d), shift};
+}
+
+__device__ __forceinline__ uint32_t div_by(uint32_t n, DivMagic m) {
+  return static_cast<uint32_t>((static_cast<uint64_t>(n) * m.magic) >> m.shift);
+}
+
 // DPP controls (GFX9 encoding).
 constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]

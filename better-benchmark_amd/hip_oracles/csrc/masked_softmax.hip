@@ -121,7 +121,10 @@ __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
 // l / L, v = 0 .. V-1: V = 2 rows per lane keep 2 KiB of x per wave in
 // flight.  Rows past the last re-read the last row and store nothing; lanes
 // past K load the row's last group and score -inf.  32-bit row arithmetic
-// (the host checks rows < 2^31).
+// (the host checks rows < 2^31); row / Q and batch / heads by multiply-high
+// constants (TrOCR [1024, 256, 256]: 44.5 against 44.8-45.1 us with the
+// division sequences, median 44.8-46.1 against 47.3-47.9; K = 512 -0.4 %,
+// K = 128 +1.5 %).
 // Measured on MI355X (steady state, % of 8 TB/s): K = 256 with 16-head
 // bias groups 77.9 % (the long-row layout: 34 %), K = 512 79.6 %, K = 128
 // and 64 about 80 %; V = 1 or 4 and 512-thread workgroups were 1-7 points
@@ -134,8 +137,8 @@ constexpr int kShortThreads = 256;
 template <int L, bool ROUND_SCALE>
 __global__ __launch_bounds__(kShortThreads) void masked_softmax_short_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
-    uint16_t* __restrict__ out, uint32_t rows, uint32_t Q, int K,
-    int64_t mask_stride, int64_t mask_batch_stride, uint32_t heads, float scale) {
+    uint16_t* __restrict__ out, uint32_t rows, uint32_t Q, DivMagic q_div, int K,
+    int64_t mask_stride, int64_t mask_batch_stride, DivMagic heads_div, float scale) {
   constexpr int RI = kWave / L;
   const int lane = threadIdx.x & (kWave - 1);
   const uint32_t wave = blockIdx.x * (kShortThreads / kWave) + (threadIdx.x >> 6);
@@ -149,9 +152,9 @@ __global__ __launch_bounds__(kShortThreads) void masked_softmax_short_rows(
   for (int v = 0; v < kShortV; ++v) {
     row[v] = (wave * kShortV + v) * RI + lane / L;
     const uint32_t r = row[v] < rows ? row[v] : rows - 1;
-    const uint32_t b = r / Q;
+    const uint32_t b = div_by(r, q_div);
     const uint32_t q = r - b * Q;
-    const uint16_t* mr = mask + static_cast<int64_t>(b / heads) * mask_batch_stride +
+    const uint16_t* mr = mask + static_cast<int64_t>(div_by(b, heads_div)) * mask_batch_stride +
                          static_cast<int64_t>(q) * mask_stride;
     xv[v] = __builtin_nontemporal_load(
         reinterpret_cast<const u32x4_t*>(x + static_cast<int64_t>(r) * K + c));
@@ -201,14 +204,14 @@ void launch_short(bool round_scale, dim3 grid, hipStream_t stream, const uint16_
   const dim3 block(kShortThreads);
   const auto r = static_cast<uint32_t>(rows);
   const auto q = static_cast<uint32_t>(Q);
-  const auto h = static_cast<uint32_t>(heads);
+  const DivMagic qd = div_magic(q), hd = div_magic(static_cast<uint32_t>(heads));
   const int k = static_cast<int>(K);
   if (round_scale) {
-    masked_softmax_short_rows<L, true><<<grid, block, 0, stream>>>(x, mask, out, r, q, k, ms,
-                                                                   mbs, h, scale);
+    masked_softmax_short_rows<L, true><<<grid, block, 0, stream>>>(x, mask, out, r, q, qd, k, ms,
+                                                                   mbs, hd, scale);
   } else {
-    masked_softmax_short_rows<L, false><<<grid, block, 0, stream>>>(x, mask, out, r, q, k, ms,
-                                                                    mbs, h, scale);
+    masked_softmax_short_rows<L, false><<<grid, block, 0, stream>>>(x, mask, out, r, q, qd, k,
+                                                                    ms, mbs, hd, scale);
   }
 }
 
