@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kMaxThreads) void bn_nhwc_apply_pad(
     const uint16_t* __restrict__ x, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
     const float* __restrict__ beta, uint16_t* __restrict__ out, uint32_t rows_out, uint32_t H,
-    uint32_t W, uint32_t Ho, uint32_t Wo, int G, int act) {
+    uint32_t W, uint32_t Ho, uint32_t Wo, DivMagic image_div, DivMagic row_div, int G, int act) {
   const int T = blockDim.x;
   const int t = threadIdx.x;
   const int g = t % G;
@@ -189,9 +189,9 @@ __global__ __launch_bounds__(kMaxThreads) void bn_nhwc_apply_pad(
 #pragma unroll
   for (int u = 0; u < kApplyUnroll; ++u) {
     const uint32_t o = o0 + static_cast<uint32_t>(u * R);
-    const uint32_t img = o / (Ho * Wo);
+    const uint32_t img = div_by(o, image_div);  // o / (Ho Wo), the load depends on it
     const uint32_t rem = o - img * (Ho * Wo);
-    const uint32_t ho = rem / Wo;
+    const uint32_t ho = div_by(rem, row_div);   // rem / Wo
     const uint32_t wo = rem - ho * Wo;
     inside[u] = o < rows_out && ho < H && wo < W;
     // Padding and rows past the end read row 0 (in bounds) and store zeros.
@@ -581,7 +581,8 @@ extern "C" int hipo_batchnorm_nhwc_act_pad_bf16(
     bn_nhwc_apply_pad<<<dim3(static_cast<unsigned>(blocks)), dim3(plan.threads), 0, stream>>>(
         x, save_mean, save_rstd, gamma, beta, out, static_cast<uint32_t>(rows_out),
         static_cast<uint32_t>(h), static_cast<uint32_t>(w), static_cast<uint32_t>(Ho),
-        static_cast<uint32_t>(Wo), G, act);
+        static_cast<uint32_t>(Wo), div_magic(static_cast<uint32_t>(Ho * Wo)),
+        div_magic(static_cast<uint32_t>(Wo)), G, act);
   } else {
     const int64_t total = rows_out * c;
     HIPO_REQUIRE((total + 255) / 256 <= 0x7fffffff, "%s: too large", what);
