@@ -317,7 +317,7 @@ __global__ __launch_bounds__(kNchwImages * kWave) void bn_nchw_small_hw(
     const uint16_t* __restrict__ x, float2* __restrict__ part, NchwMerge mg,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     uint16_t* __restrict__ out, int64_t N, int64_t C, int64_t HW, int act) {
-  extern __shared__ uint16_t slab[];  // [kNchwImages][64 * HW] when STAGED
+  extern __shared__ __align__(16) uint16_t slab[];  // [kNchwImages][64 * HW] when STAGED
   __shared__ float2 stats[kNchwImages][kNchwChannels];
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x >> 6;

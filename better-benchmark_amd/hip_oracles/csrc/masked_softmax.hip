@@ -247,7 +247,7 @@ __global__ __launch_bounds__(256) void masked_softmax_shared_mask(
   constexpr int NR = 4 / W;
   static_assert(W * NR * kWave == 256 && W * kWave * kRowGroup == KC, "full rows");
   constexpr int kStageWords = KC / 512;  // 32-bit words of the mask row per thread
-  __shared__ uint32_t mrow[KC / 2];
+  __shared__ __align__(16) uint32_t mrow[KC / 2];  // read back as 16-byte groups
   __shared__ float pmax[W * NR], psum[W * NR];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
