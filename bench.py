@@ -19,6 +19,9 @@ stream, between two hipEvents (device time).
 
 value             = algorithmic bytes per step / (wall time per step)   [GB/s]
 roofline.achieved = algorithmic bytes / (device time per step)          [GB/s]
+roofline.memcopy_sol_us = the reference's memcopy SOL (fp32 add(src, 1,
+                    out=dst) over the same bytes) in the same loop;
+         vs_memcopy_sol = memcopy_sol_us / kernel_us (> 1: faster than it)
 cpu_baseline      = the CPU oracle (oracle/hipo_ref.c, OpenMP) on the same
                     workload on the host cores.
 configs           = every BASELINE config: the same steady-state loop, plus
@@ -230,6 +233,45 @@ def steady_state(rid, steps, warmup):
     return out, cpu_inputs
 
 
+def memcopy_sol_steady(nbytes: int, steps: int = 128) -> float:
+    """The reference's memcopy speed-of-light construction
+    (repro_harness.py:952-958: an fp32 add(src, 1, out=dst) moving nbytes,
+    half read, half written) timed in the steady-state loop (rotating
+    buffers >= 1 GiB between reuses, steps in one hipGraph, events on the
+    launch stream): device us per step.  It is ATen's elementwise kernel
+    with cached stores, not a bound -- a non-temporal copy of the same bytes
+    runs ~8 % faster on MI355X."""
+    import torch
+    import oracle_harness as oh
+    n = max(nbytes // 8, 1)
+    sets = min(16, max(2, math.ceil((1 << 30) / (4 * n))))
+    src = [torch.ones(n, dtype=torch.float32, device="cuda") for _ in range(sets)]
+    dst = [torch.empty_like(t) for t in src]
+    per_graph = sets * max(1, min(STEPS_PER_GRAPH, steps) // sets)
+    for k in range(sets):
+        torch.add(src[k], 1, out=dst[k])
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for k in range(per_graph):
+            torch.add(src[k % sets], 1, out=dst[k % sets])
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // per_graph)
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with oh._gpu_exclusive_lock("bench:memcopy_sol"):
+        ev0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / (reps * per_graph)
+    del g, src, dst
+    torch.cuda.empty_cache()
+    return round(us, 2)
+
+
 def per_config(want_cpu, steady_steps=64):
     import torch
     import oracle_harness as oh
@@ -326,6 +368,11 @@ def main(argv=None) -> int:
                      "traffic": pmc_traffic(rid), "kernel_us": h["device_us_per_step"]},
         "cpu_baseline": None,
     }
+    # The reference's own SOL yardstick on this box, in the same loop (boxes
+    # of the pool differ by 1-3 %); > 1 means faster than that copy.
+    sol_us = memcopy_sol_steady(h["nbytes"])
+    line["roofline"]["memcopy_sol_us"] = sol_us
+    line["roofline"]["vs_memcopy_sol"] = round(sol_us / h["device_us_per_step"], 4)
     if not args.no_cpu:
         log("cpu baseline (CPU oracle)")
         line["cpu_baseline"] = cpu_baseline(rid, cpu_inputs, h["nbytes"])
