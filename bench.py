@@ -291,6 +291,8 @@ def per_config(want_cpu, steady_steps=64):
                  "bytes": r.get("bytes"),
                  "steady_us": ss["device_us_per_step"], "steady_gbps": ss["achieved"],
                  "steady_sol_frac": round(ss["achieved"] / PEAK_GBPS, 4),
+                 "steady_vs_memcopy_sol": round(memcopy_sol_steady(ss["nbytes"])
+                                                / ss["device_us_per_step"], 4),
                  "traffic": pmc_traffic(rid),
                  "us": r.get("oracle_us"), "median_us": r.get("oracle_median_us"),
                  "graph_us": r.get("oracle_graph_us"),
