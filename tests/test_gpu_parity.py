@@ -341,6 +341,12 @@ def test_softmax_mid_rows(rocm_device):
         want = torch.softmax((x.float().view(b // heads, heads, q, k) + bias.float().unsqueeze(1))
                              .to(bf).float(), -1).to(bf).view(b, q, k)
         assert_close(got, want, BF16_TOL, what + " vs torch")
+        # the same bias as a padded view: row stride k + 8, batch stride q (k + 8)
+        padded = torch.randn(b // heads, q, k + 8, generator=g).to(bf)
+        got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), padded.to(rocm_device)[:, :, :k],
+                                              1.0, heads)
+        assert_close(got, ref.scaled_bias_softmax(x, padded[:, :, :k].contiguous(), 1.0, heads),
+                     BF16_TOL, what + " padded bias rows")
 
 
 def test_norm_closed_forms(rocm_device):
