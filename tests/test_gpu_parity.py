@@ -387,6 +387,35 @@ def test_norm_shapes_off_vector_path(rocm_device):
             assert_close(a, w, _tol(w), f"rms {rows}x{cols} {name}")
 
 
+def test_layernorm_k4096_kernel(rocm_device):
+    """cols = 4096 takes the row-length kernel (two rows per workgroup, gamma
+    and beta staged in LDS): odd row counts leave the last workgroup's second
+    row idle; y-only calls pass NULL h / mean / rstd."""
+    import hip_oracles
+    import oracle as ref
+    bf = torch.bfloat16
+    for rows in (1, 5, 33):
+        g = torch.Generator().manual_seed(rows)
+        x = (torch.randn(rows, 4096, generator=g) * 2 + 0.5).to(bf)
+        r = torch.randn(rows, 4096, generator=g).to(bf)
+        gm = (1 + 0.1 * torch.randn(4096, generator=g)).to(bf)
+        bt = (0.1 * torch.randn(4096, generator=g)).to(bf)
+        d = [t.to(rocm_device) for t in (x, r, gm, bt)]
+        want = ref.residual_layernorm(x, r, gm, bt, 1e-5)
+        for name, a, w in zip(("h", "y", "mean", "rstd"), hip_oracles.residual_layernorm(*d, 1e-5), want):
+            assert_close(a, w, _tol(w), f"ln k4096 rows {rows} {name}")
+        assert_close(hip_oracles.residual_layernorm(*d, 1e-5, outputs="y"), want[1], BF16_TOL,
+                     f"ln k4096 rows {rows} y-only")
+    # a constant row: mean c, rstd 1/sqrt(eps), y = beta
+    x = torch.full((3, 4096), 1.5, dtype=bf)
+    h, y, mean, rstd = hip_oracles.residual_layernorm(
+        x.to(rocm_device), torch.zeros_like(x).to(rocm_device),
+        torch.ones(4096, dtype=bf, device=rocm_device), bt.to(rocm_device), 1e-5)
+    assert torch.equal(mean.cpu(), torch.full((3,), 1.5))
+    assert_close(rstd, torch.full((3,), 1 / math.sqrt(1e-5)), F32_TOL, "rstd constant row")
+    assert_close(y, bt.expand(3, 4096), BF16_TOL, "y constant row = beta")
+
+
 def test_row_layouts_multiwave(rocm_device):
     """Row kernels with several waves per row: ragged last groups, waves with
     no valid group, rows not a multiple of rows-per-block, the largest row on
