@@ -22,12 +22,18 @@ roofline.achieved = algorithmic bytes / (device time per step)          [GB/s]
 roofline.memcopy_sol_us = the reference's memcopy SOL (fp32 add(src, 1,
                     out=dst) over the same bytes) in the same loop;
          vs_memcopy_sol = memcopy_sol_us / kernel_us (> 1: faster than it)
-cpu_baseline      = the CPU oracle (oracle/hipo_ref.c, OpenMP) on the same
-                    workload on the host cores.
-configs           = every BASELINE config: the same steady-state loop, plus
-                    oracle_harness.bench_oracle (single launch after a cache
-                    flush, fp64 numerics gate) with the eager repro timed
-                    on the host CPU beside it.
+roofline.flat_copy_us = a non-temporal flat copy (hipo_flat_copy) of the
+                    config's read and write bytes in the same loop: the
+                    ceiling of the access style; vs_flat_copy = flat_copy_us
+                    / kernel_us
+cpu_baseline      = the eager repro (ATen) on the host CPU, os.cpu_count()
+                    threads, warmup 1 + min of 5 (BASELINE.md's method); the
+                    CPU oracle (oracle/hipo_ref.c) time rides along.
+configs           = every BASELINE config: the same steady-state loop and
+                    flat copy, plus oracle_harness.bench_oracle (graph-replay
+                    timing after a cache flush, the Inductor comparator, the
+                    fp64 numerics gate) with the eager repro timed on the host
+                    CPU beside it.
 """
 from __future__ import annotations
 
@@ -109,10 +115,10 @@ def _cpu_oracle_call(rid, cpu_inputs, threads):
     return lambda: ref.batchnorm_train(*cpu_inputs, momentum=0.1, eps=1e-5, threads=threads)
 
 
-def cpu_baseline(rid, cpu_inputs, nbytes, budget_s: float = 10.0) -> dict:
-    """CPU oracle on the host cores: min over repeated full-workload runs
-    within ~budget_s of wall time (at least 2 runs)."""
-    threads = max(1, min(os.cpu_count() or 1, 16))
+def c_oracle_time(rid, cpu_inputs, budget_s: float = 5.0) -> dict:
+    """CPU oracle (oracle/hipo_ref.c, OpenMP, fp64 arithmetic) on the full
+    workload: min over repeated runs within ~budget_s (at least 2 runs)."""
+    threads = os.cpu_count() or 1
     fn = _cpu_oracle_call(rid, cpu_inputs, threads)
     fn()  # warm (page-in, thread pool)
     times = []
@@ -121,12 +127,23 @@ def cpu_baseline(rid, cpu_inputs, nbytes, budget_s: float = 10.0) -> dict:
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
-    best = min(times)
-    return {"value": round(nbytes / best / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"full {WORKLOAD[rid]} workload, min of {len(times)} runs "
-                      f"({best * 1e3:.1f} ms each) of oracle/hipo_ref.c, OpenMP",
-            "us": round(best * 1e6, 1)}
+    return {"us": round(min(times) * 1e6, 1), "threads": threads, "runs": len(times)}
+
+
+def cpu_baseline(rid, cpu_inputs, nbytes) -> dict:
+    """The eager repro on the host CPU (os.cpu_count() threads,
+    warmup 1 + min of 5 perf_counter runs), expressed in the metric's unit
+    over the same algorithmic bytes; the CPU oracle's time rides along."""
+    import oracle_harness as oh
+    _, _, d = oh._load_oracle_module(CANONICAL / rid)
+    eager = oh.time_cpu_eager(oh.get_repro_instance(d), cpu_inputs)
+    us = eager["cpu_eager_us"]
+    return {"value": round(nbytes / (us * 1e-6) / 1e9, 2), "unit": "GB/s",
+            "cores": eager["cpu_threads"], "kind": "port",
+            "sample": f"full {WORKLOAD[rid]} workload: the eager Repro (ATen on the CPU), "
+                      f"torch.set_num_threads(os.cpu_count()), warmup 1 + min of 5",
+            "us": us, "cpu_model": eager["cpu_model"], "cpu_affinity": eager.get("cpu_affinity"),
+            "c_oracle": c_oracle_time(rid, cpu_inputs)}
 
 
 # Steps captured per hipGraph (a multiple of the input sets, at most the
@@ -272,34 +289,113 @@ def memcopy_sol_steady(nbytes: int, steps: int = 128) -> float:
     return round(us, 2)
 
 
-def per_config(want_cpu, steady_steps=64):
+def flat_copy_steady(read_bytes: int, write_bytes: int, steps: int = 128) -> float:
+    """hipo_flat_copy of read_bytes -> write_bytes (rounded to 1 KiB) in the
+    steady-state loop (rotating buffers >= 1 GiB between reuses, steps in one
+    hipGraph, events on the launch stream): device us per step.  The ceiling
+    of the oracle kernels' access style at a config's bytes."""
+    import torch
+    import hip_oracles
+    import oracle_harness as oh
+    rb = max(1024, int(round(read_bytes / 1024)) * 1024)
+    wb = max(1024, int(round(write_bytes / 1024)) * 1024)
+    sets = min(16, max(2, math.ceil((1 << 30) / min(rb, wb))))
+    src = [torch.ones(rb // 4, dtype=torch.float32, device="cuda") for _ in range(sets)]
+    dst = [torch.empty(wb // 4, dtype=torch.float32, device="cuda") for _ in range(sets)]
+    per_graph = sets * max(1, min(STEPS_PER_GRAPH, steps) // sets)
+    for k in range(sets):
+        hip_oracles.flat_copy(src[k], dst[k])
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for k in range(per_graph):
+            hip_oracles.flat_copy(src[k % sets], dst[k % sets])
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // per_graph)
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with oh._gpu_exclusive_lock("bench:flat_copy"):
+        ev0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / (reps * per_graph)
+    del g, src, dst
+    torch.cuda.empty_cache()
+    return round(us, 2)
+
+
+def read_write_bytes(cpu_inputs, nbytes):
+    """(read, write) split of the algorithmic bytes: every tensor input is
+    read once, the rest is written."""
+    import torch
+    seen, rd = set(), 0
+    for t in cpu_inputs:
+        if isinstance(t, torch.Tensor) and id(t) not in seen:
+            seen.add(id(t))
+            rd += t.numel() * t.element_size()
+    return rd, max(nbytes - rd, 0)
+
+
+# Compile comparator budget: per-config torch.compile is skipped once the
+# run has spent this long, so the default bench stays within minutes.
+COMPILE_BUDGET_S = 420.0
+
+
+def per_config(want_cpu, steady_steps=64, compare_compile=True, coordinate_descent=True,
+               t_start=None):
     import torch
     import oracle_harness as oh
     from repro_harness import make_inputs_from_config
+    t_start = t_start or time.perf_counter()
     out = []
     for tag, rid in ALL_CONFIGS:
         label, cfg = _baseline_point(rid)
         log(f"config {tag}: {rid}")
-        ss, _ = steady_state(rid, steady_steps, 8)
+        ss, cpu_inputs = steady_state(rid, steady_steps, 8)
+        rd, wr = read_write_bytes(cpu_inputs, ss["nbytes"])
+        del cpu_inputs
+        flat_us = flat_copy_steady(rd, wr)
+        memcopy_us = memcopy_sol_steady(ss["nbytes"])
         _, fn, d = oh._load_oracle_module(CANONICAL / rid)
         oh._seed_input_generation(1)
         inputs = make_inputs_from_config(cfg, device="cuda")
+        elapsed = time.perf_counter() - t_start
+        use_compile = compare_compile and elapsed < COMPILE_BUDGET_S
+        log(f"config {tag}: bench_oracle (compile comparator: {use_compile}, "
+            f"{elapsed:.0f} s elapsed)")
         r = oh.bench_oracle(fn, oh.get_repro_instance(d), inputs, f"{rid}_{label}",
-                            warmup=10, rep=100, rounds=5, compare_compile=False,
-                            cpu_eager=want_cpu)
+                            warmup=10, rep=100, rounds=5, compare_compile=use_compile,
+                            coordinate_descent=coordinate_descent, cpu_eager=want_cpu)
         entry = {"config": tag, "repro": rid, "status": r.get("status"),
-                 "bytes": r.get("bytes"),
+                 "bytes": r.get("bytes"), "read_bytes": rd, "write_bytes": wr,
                  "steady_us": ss["device_us_per_step"], "steady_gbps": ss["achieved"],
                  "steady_sol_frac": round(ss["achieved"] / PEAK_GBPS, 4),
-                 "steady_vs_memcopy_sol": round(memcopy_sol_steady(ss["nbytes"])
-                                                / ss["device_us_per_step"], 4),
+                 "flat_copy_us": flat_us,
+                 "vs_flat_copy": round(flat_us / ss["device_us_per_step"], 4),
+                 "memcopy_sol_us": memcopy_us,
+                 "steady_vs_memcopy_sol": round(memcopy_us / ss["device_us_per_step"], 4),
                  "traffic": pmc_traffic(rid),
-                 "us": r.get("oracle_us"), "median_us": r.get("oracle_median_us"),
-                 "graph_us": r.get("oracle_graph_us"),
-                 "gbps": r.get("gbps"), "sol_frac": r.get("sol_frac")}
+                 "oracle_us": r.get("oracle_us"), "compile_us": r.get("compile_us"),
+                 "ratio": r.get("ratio"),
+                 "oracle_launch_us": r.get("oracle_launch_us"),
+                 "oracle_median_us": r.get("oracle_median_us"),
+                 "clean_cache_sol_frac": r.get("clean_cache_sol_frac")}
+        if not use_compile and compare_compile:
+            entry["compile_skipped"] = f"time budget ({COMPILE_BUDGET_S:.0f} s) spent"
+        for k in ("compile", "compile_error"):
+            if k in r:
+                entry[k] = r[k]
         gate = r.get("numerics_gate")
         if gate is not None:
             entry["numerics_gate_pass"] = gate.get("pass")
+            entry["numerics_gate_comparator"] = gate.get("comparator")
+            entry["numerics_gate"] = [
+                {k: v for k, v in o.items() if k in ("idx", "err_oracle", "err_compiled",
+                                                     "threshold", "pass")}
+                for o in gate.get("per_output", [])]
         for k in ("cpu_eager_us", "cpu_threads", "cpu_model"):
             if k in r:
                 entry[k] = r[k]
@@ -330,6 +426,10 @@ def main(argv=None) -> int:
     ap.add_argument("--config", default=HEADLINE, help="repro id of the headline workload")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-compile", action="store_true",
+                    help="skip the per-config torch.compile (Inductor) comparator")
+    ap.add_argument("--no-coordinate-descent", action="store_true",
+                    help="Inductor without coordinate-descent tuning")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
     args = ap.parse_args(argv)
 
@@ -347,6 +447,7 @@ def main(argv=None) -> int:
     import hip_oracles
     hip_oracles.load_library()
 
+    t_start = time.perf_counter()
     rid = args.config
     h, cpu_inputs = steady_state(rid, args.steps, args.warmup)
     line = {
@@ -375,12 +476,18 @@ def main(argv=None) -> int:
     sol_us = memcopy_sol_steady(h["nbytes"])
     line["roofline"]["memcopy_sol_us"] = sol_us
     line["roofline"]["vs_memcopy_sol"] = round(sol_us / h["device_us_per_step"], 4)
+    rd, wr = read_write_bytes(cpu_inputs, h["nbytes"])
+    flat_us = flat_copy_steady(rd, wr)
+    line["roofline"]["flat_copy_us"] = flat_us
+    line["roofline"]["vs_flat_copy"] = round(flat_us / h["device_us_per_step"], 4)
     if not args.no_cpu:
-        log("cpu baseline (CPU oracle)")
+        log("cpu baseline (eager repro on the host CPU)")
         line["cpu_baseline"] = cpu_baseline(rid, cpu_inputs, h["nbytes"])
     del cpu_inputs
     if not args.no_configs:
-        line["configs"] = per_config(not args.no_cpu)
+        line["configs"] = per_config(not args.no_cpu, compare_compile=not args.no_compile,
+                                     coordinate_descent=not args.no_coordinate_descent,
+                                     t_start=t_start)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -14,6 +14,7 @@ from __future__ import annotations
 import ctypes
 import re
 import threading
+import weakref
 from pathlib import Path
 
 import torch  # imported before the .so so the process has one HIP runtime
@@ -66,6 +67,7 @@ _SIGNATURES = {
         ctypes.c_int,
         [_c_ptr] * 8 + [_c_i64, _c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int,
                         _c_ptr, ctypes.c_size_t, _c_ptr]),
+    "hipo_flat_copy": (ctypes.c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
 }
 
 _lib = None
@@ -327,19 +329,38 @@ def batchnorm_workspace_bytes(n: int, c: int, hw: int) -> int:
 # One zero-filled BatchNorm workspace per device, kept for the process: the
 # single-pass kernel keeps its exchange state (completion count, epoch,
 # tagged slots) there between calls, so it must start zeroed and must not be
-# handed to two calls that can run at the same time.
+# handed to two calls that can run at the same time.  A workspace that is
+# replaced by a larger one is retired, never freed: a hipGraph captured
+# earlier holds its raw address (ctypes keeps no reference to the tensor),
+# and its replays keep using it, with their own epoch state, safely.
 _bn_workspaces: dict[int, torch.Tensor] = {}
+_bn_retired: dict[int, list[torch.Tensor]] = {}
+# Caller-provided workspaces seen by batchnorm_train, so their error words are
+# checked too (weak: the caller owns them).
+_bn_caller_workspaces: "weakref.WeakValueDictionary[int, torch.Tensor]" = (
+    weakref.WeakValueDictionary())
 _bn_ws_lock = threading.Lock()
+
+# Byte offset of the sticky error word in a BatchNorm workspace.
+BN_ERROR_WORD_OFFSET = 8
+
+
+class HipOraclesDeviceFault(RuntimeError):
+    """A kernel reported a fault through its error word (a bounded
+    cross-workgroup wait timed out; the affected outputs are NaN)."""
 
 
 def batchnorm_cached_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
-    """The device's shared workspace, grown (zero-filled) to at least nbytes."""
+    """The device's shared workspace, grown (zero-filled) to at least nbytes.
+    The workspace it replaces stays allocated for the rest of the process."""
     with _bn_ws_lock:
         ws = _bn_workspaces.get(dev.index)
         if ws is None or ws.numel() < nbytes:
             _require(not torch.cuda.is_current_stream_capturing(),
                      "batchnorm: the workspace is allocated on first use; call once "
                      "outside graph capture (or pass workspace=) before capturing")
+            if ws is not None:
+                _bn_retired.setdefault(dev.index, []).append(ws)
             ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=dev)
             _bn_workspaces[dev.index] = ws
         return ws
@@ -364,7 +385,11 @@ def batchnorm_train(x, gamma, beta, running_mean, running_var, *, momentum: floa
     need = int(lib.hipo_batchnorm_workspace_bytes(n, c, h * w))
     if workspace is None:
         workspace = batchnorm_cached_workspace(dev, need)
-    _require(workspace.device == dev and workspace.numel() * workspace.element_size() >= need,
+    else:
+        _require(workspace.device == dev and workspace.is_contiguous(),
+                 "batchnorm: workspace must be contiguous memory on x's device")
+        _bn_caller_workspaces[workspace.data_ptr()] = workspace
+    _require(workspace.numel() * workspace.element_size() >= need,
              "batchnorm: workspace too small")
     y = torch.empty_like(x)
     save_mean = torch.empty(c, dtype=torch.float32, device=dev)
@@ -377,6 +402,22 @@ def batchnorm_train(x, gamma, beta, running_mean, running_var, *, momentum: floa
             _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(dev)),
             "batchnorm_train")
     return y, save_mean, save_invstd
+
+
+def flat_copy(src: torch.Tensor, dst: torch.Tensor, read_bytes: int | None = None,
+              write_bytes: int | None = None) -> None:
+    """Measurement yardstick: read `read_bytes` of src and write `write_bytes`
+    of dst in one launch with the oracle kernels' access style (default: all
+    of each).  Sizes are multiples of 1024 bytes."""
+    lib = load_library()
+    dev = _require_rocm(src, dst)
+    _require(src.is_contiguous() and dst.is_contiguous(), "flat_copy: contiguous buffers")
+    rb = src.numel() * src.element_size() if read_bytes is None else int(read_bytes)
+    wb = dst.numel() * dst.element_size() if write_bytes is None else int(write_bytes)
+    _require(rb <= src.numel() * src.element_size() and wb <= dst.numel() * dst.element_size(),
+             "flat_copy: sizes exceed the buffers")
+    with torch.cuda.device(dev):
+        _check(lib.hipo_flat_copy(_ptr(src), rb, _ptr(dst), wb, _stream(dev)), "flat_copy")
 
 
 _BN_ACTS = {None: 0, "none": 0, "relu": 1, "silu": 2}
@@ -447,14 +488,57 @@ def batchnorm_nchw_act_mean(x, gamma, beta, running_mean, running_var, *, moment
     return save_mean, save_rstd, out
 
 
-def batchnorm_error_flag(dev: torch.device | None = None) -> int:
-    """Sticky error word of the device's shared BatchNorm workspace: nonzero
-    once an exchange wait of the single-pass kernel has timed out (that
-    channel's outputs are then NaN).  Synchronises the device."""
-    ws = _bn_workspaces.get((dev or torch.device("cuda", torch.cuda.current_device())).index)
-    if ws is None:
-        return 0
-    return int(ws[8:12].view(torch.int32).item())
+def _error_word(ws: torch.Tensor) -> torch.Tensor:
+    raw = ws.view(torch.uint8) if ws.dtype != torch.uint8 else ws
+    return raw[BN_ERROR_WORD_OFFSET:BN_ERROR_WORD_OFFSET + 4].view(torch.int32)
+
+
+def _known_workspaces(dev: torch.device | None):
+    with _bn_ws_lock:
+        found = list(_bn_workspaces.items())
+        found += [(d, w) for d, ws in _bn_retired.items() for w in ws]
+        found += [(w.device.index, w) for w in list(_bn_caller_workspaces.values())]
+    return [w for d, w in found if dev is None or d == dev.index]
+
+
+def batchnorm_error_flag(dev: torch.device | None = None, *,
+                         workspace: torch.Tensor | None = None) -> int:
+    """Sticky error word of a BatchNorm workspace: nonzero once an exchange
+    wait of the single-pass kernel has timed out (that channel's outputs and
+    running statistics are then NaN).  `workspace` selects a caller-provided
+    workspace; by default the device's shared one.  Synchronises."""
+    if workspace is None:
+        d = dev or torch.device("cuda", torch.cuda.current_device())
+        workspace = _bn_workspaces.get(d.index)
+        if workspace is None:
+            return 0
+    return int(_error_word(workspace).item())
+
+
+def device_faults(dev: torch.device | None = None, *, clear: bool = True) -> list[str]:
+    """Faults recorded by kernels in every BatchNorm workspace this process has
+    used on `dev` (all devices if None): the shared, retired and caller-provided
+    ones.  With `clear`, each reported word is reset to zero on the current
+    stream, so the next check sees only new faults.  Synchronises."""
+    out = []
+    for ws in _known_workspaces(dev):
+        word = _error_word(ws)
+        v = int(word.item())
+        if v:
+            out.append(f"batchnorm_train_fwd_f32: exchange wait timed out "
+                       f"(error word {v:#x}, workspace {ws.data_ptr():#x} on {ws.device}); "
+                       f"its outputs and running statistics are NaN")
+            if clear:
+                word.zero_()
+    return out
+
+
+def raise_on_device_faults(dev: torch.device | None = None) -> None:
+    """Raise HipOraclesDeviceFault if any kernel recorded a fault (see
+    device_faults); the words are cleared first."""
+    faults = device_faults(dev, clear=True)
+    if faults:
+        raise HipOraclesDeviceFault("; ".join(faults))
 
 
 __all__ = [
@@ -463,5 +547,6 @@ __all__ = [
     "residual_layernorm", "rmsnorm", "rmsnorm_ex", "scaled_bias_softmax", "spatial_mean_nhwc",
     "batchnorm_nhwc_act_pad", "batchnorm_nchw_act_mean",
     "batchnorm_workspace_bytes", "batchnorm_train",
-    "batchnorm_cached_workspace", "batchnorm_error_flag",
+    "batchnorm_cached_workspace", "batchnorm_error_flag", "BN_ERROR_WORD_OFFSET",
+    "HipOraclesDeviceFault", "device_faults", "raise_on_device_faults", "flat_copy",
 ]

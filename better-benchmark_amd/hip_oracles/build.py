@@ -36,6 +36,7 @@ SOURCES = [
     "batchnorm_fused.hip",
     "spatial_mean.hip",
     "batchnorm_bf16.hip",
+    "flat_copy.hip",
 ]
 
 # Packed-FP32 VALU forms are disabled for all device code (the compiler

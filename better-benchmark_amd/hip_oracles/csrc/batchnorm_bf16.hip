@@ -31,13 +31,13 @@ namespace hipo {
 namespace {
 
 constexpr int kMaxThreads = 1024;
-constexpr float kLog2e = 1.4426950408889634f;
 
 enum { kActNone = 0, kActRelu = 1, kActSilu = 2 };
 
 // act(bf16(((x - mean) * rstd) * gamma + beta)), fp32 ops in the eager order
-// (no contraction).  SiLU is t / (1 + e^-t) with the hardware exp2 and
-// reciprocal; the caller rounds the result to bf16.
+// (no contraction).  SiLU is t / (1 + exp(-t)) as eager, with the
+// extended-precision exp_f32 and an IEEE division; the caller rounds the
+// result to bf16.
 __device__ __forceinline__ float bn_act(float x, float mean, float rstd, float g, float b,
                                         int act) {
   float y = __fmul_rn(__fsub_rn(x, mean), rstd);
@@ -45,7 +45,7 @@ __device__ __forceinline__ float bn_act(float x, float mean, float rstd, float g
   if (act == kActRelu) {
     y = y < 0.f ? 0.f : y;
   } else if (act == kActSilu) {
-    y = y * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-y * kLog2e));
+    y = y / (1.f + exp_f32(exp_domain(-y)));
   }
   return y;
 }

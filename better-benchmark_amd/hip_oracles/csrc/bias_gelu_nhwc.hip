@@ -3,16 +3,24 @@
 // Semantics (the eager op order of gelu(x + bias) on bf16 tensors):
 //   t = bf16(x + bias[c])            (fp32 add, round to nearest even)
 //   y = bf16(GELU_tanh(t))           (fp32 arithmetic, one rounding)
-// GELU_tanh(t) = 0.5 t (1 + tanh(u)), u = sqrt(2/pi) (t + 0.044715 t^3), is
-// evaluated as the same function in the form
-//   t * sigmoid(2u) = t / (1 + 2^z),   z = t * (K0 + K1 t^2),
-//   K0 = -2 sqrt(2/pi) log2(e),  K1 = 0.044715 K0,
-// with the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32): one FMA,
-// three multiplies, one add and two transcendentals per value.  This form
-// keeps the small negative tail that 1 + tanh(u) cancels to zero, gives
-// +inf at +inf and NaN at -inf (as -inf * 0 in the tanh form), and rounds to
-// the same bf16 as the correctly rounded function except within a few fp32
-// ulps of a bf16 rounding boundary.
+// GELU_tanh(t) = 0.5 t (1 + tanh(u)), u = sqrt(2/pi) (t + 0.044715 t^3).
+// t is a bf16 value, so the output is a function of its 65536 bit patterns,
+// and the kernel returns the correctly rounded bf16 of the exact function:
+//   2^-10 <= |t| < 16 (3584 inputs): read from a table of the correctly
+//     rounded results (gelu_table.h, generated at 96-bit precision), staged
+//     once per workgroup in LDS;
+//   2^-125 <= |t| < 2^-10: t / 2, an exponent decrement (GELU(t) = t/2 (1 +
+//     u + ...) with |u| < 0.8 * 2^-10, less than half a bf16 ulp, and t / 2
+//     is a bf16 value);
+//   t >= 16: t (1 - GELU(t) / t < e^-300);  t <= -16: -0 (|GELU(t)| <
+//     e^-300 underflows);  +inf -> +inf, -inf -> NaN (as -inf * 0 in
+//     eager), NaN -> NaN;
+//   |t| < 2^-125 (bf16 subnormal t / 2): t / 2 rounded to nearest even.
+// gen_gelu_table.py --check verifies the whole mapping against the exact
+// function.  Eager and Inductor evaluate the tanh form in fp32 and differ
+// from it by one ulp within a few fp32 ulps of a rounding boundary and in
+// the far negative tail, where their 1 + tanh(u) cancels.  No
+// transcendental is evaluated on the device.
 //
 // Layout: one wave64 per tile of 64 channels x 64 spatial positions of one
 // image.  Lane l owns an 8x8 (channel x position) block: cb = l / 8 picks 8
@@ -30,6 +38,7 @@
 // version of this kernel with the GELU read from a 128 KiB LDS table.
 // Loads and stores are non-temporal.
 // HBM-bound: algorithmic bytes per element = 2 (read) + 2 (write).
+#include "gelu_table.h"
 #include "hipo_common.h"
 
 namespace hipo {
@@ -39,14 +48,44 @@ constexpr int kTileHw = 64;  // positions per wave tile
 constexpr int kTileC = 64;   // channels per wave tile
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlockThreads = kWavesPerBlock * kWave;
+constexpr int kTilesPerWave = 1;  // consecutive position tiles per wave (3-D grid)
 
-constexpr float kGeluK0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
-constexpr float kGeluK1 = kGeluK0 * 0.044715f;
+// bf16 bits of t -> bf16 bits of GELU(t); `lut` holds kGeluTable.
+constexpr uint32_t kGeluLo = static_cast<uint32_t>(kGeluTableExpLo) << 7;  // |t| = 2^-10
+constexpr uint32_t kGeluHi = static_cast<uint32_t>(kGeluTableExpHi + 1) << 7;  // |t| = 16
 
-__device__ __forceinline__ float gelu_tanh_f32(float t) {
-  const float z = t * __builtin_fmaf(kGeluK1, t * t, kGeluK0);
-  return t * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
+// The common inputs (2^-125 <= |t| < 16): the table or t / 2.  Branch-free:
+// the LDS index is clamped into the table, the read is unconditional, and a
+// select picks the result.
+__device__ __forceinline__ uint32_t gelu_bits_common(uint32_t tb, const uint16_t* lut) {
+  const uint32_t mag = tb & 0x7fffu;
+  const uint32_t off = mag - kGeluLo;  // wraps below the table
+  const uint32_t idx = __builtin_elementwise_min(off, static_cast<uint32_t>(kGeluTablePerSign - 1)) +
+                       (tb >> 15) * static_cast<uint32_t>(kGeluTablePerSign);
+  const uint32_t looked = lut[idx];
+  return off < static_cast<uint32_t>(kGeluTablePerSign) ? looked : tb - 0x80u;
 }
+
+// Inputs gelu_bits_common does not cover: |t| >= 16, inf, NaN, |t| <
+// 2^-125 (zero included).
+__device__ __forceinline__ bool gelu_rare(uint32_t tb) {
+  return ((tb & 0x7fffu) - 0x100u) >= (kGeluHi - 0x100u);
+}
+
+__device__ __forceinline__ uint32_t gelu_bits_rare(uint32_t tb) {
+  const uint32_t mag = tb & 0x7fffu;
+  if (mag < 0x100u)  // +-0 and subnormal results: t / 2 rounded to nearest even
+    return pack_bf16x2(0.5f * bf16_to_f32(static_cast<uint16_t>(tb)), 0.0f) & 0xffffu;
+  if ((tb & 0x8000u) == 0 || mag > 0x7f80u) return tb;  // t >= 16, +inf, NaN
+  return mag == 0x7f80u ? 0x7fc0u : 0x8000u;             // -inf -> NaN; t <= -16 -> -0
+}
+
+__device__ __forceinline__ uint32_t gelu_bits(uint32_t tb, const uint16_t* lut) {
+  return gelu_rare(tb) ? gelu_bits_rare(tb) : gelu_bits_common(tb, lut);
+}
+
+// The table's 16-byte chunks, staged into LDS by a workgroup.
+constexpr int kGeluTableChunks = kGeluTableSize * 2 / 16;
 
 struct TileGeom {
   int64_t C, HW;
@@ -58,70 +97,122 @@ struct TileGeom {
 // loads without integer divisions (66.1 against 66.6 us at config 2); the
 // dispatch order is the 1-D numbering's.  Otherwise (grids past the y / z
 // limits) the block index is split by division.
-template <bool GRID3>
+template <bool GRID3, int TPW>
 __global__ __launch_bounds__(kBlockThreads) void bias_gelu_nchw_to_nhwc_tiles(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ out, TileGeom g) {
+  __shared__ __align__(16) uint16_t lut[kGeluTableSize];
   const int lane = threadIdx.x & (kWave - 1);
-  int ct, ht;
+  int ct, ht0;
   int64_t img;
+  bool tile_ok;  // wave-uniform
   if constexpr (GRID3) {
     ct = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * kWavesPerBlock +
                                         static_cast<int>(threadIdx.x >> 6));
-    if (ct >= g.c_tiles) return;  // wave-uniform; the kernel has no barrier
-    ht = blockIdx.y;
+    tile_ok = ct < g.c_tiles;
+    if (!tile_ok) ct = 0;
+    ht0 = static_cast<int>(blockIdx.y) * TPW;
     img = blockIdx.z;
   } else {
-    const int t = __builtin_amdgcn_readfirstlane(
+    static_assert(GRID3 || TPW == 1, "the 1-D numbering takes one tile per wave");
+    int t = __builtin_amdgcn_readfirstlane(
         static_cast<int>(blockIdx.x) * kWavesPerBlock + static_cast<int>(threadIdx.x >> 6));
-    if (t >= g.ntiles) return;  // wave-uniform
+    tile_ok = t < g.ntiles;
+    if (!tile_ok) t = 0;
     ct = t % g.c_tiles;
     const int rest = t / g.c_tiles;
-    ht = rest % g.hw_tiles;
+    ht0 = rest % g.hw_tiles;
     img = rest / g.hw_tiles;
   }
   const int64_t c0 = static_cast<int64_t>(ct) * kTileC + (lane >> 3) * 8;
-  const int64_t p0 = static_cast<int64_t>(ht) * kTileHw + (lane & 7) * 8;
   // Lanes outside a partial tile load from the tile's first block (always in
   // bounds, no branch around the loads) and store nothing.
-  const bool ok = c0 < g.C && p0 < g.HW;
-  const int64_t cl = ok ? c0 : static_cast<int64_t>(ct) * kTileC;
-  const int64_t pl = ok ? p0 : static_cast<int64_t>(ht) * kTileHw;
-  const int64_t in_off = (img * g.C + cl) * g.HW + pl;
+  const bool c_ok = tile_ok && c0 < g.C;
+  const int64_t cl = c_ok ? c0 : static_cast<int64_t>(ct) * kTileC;
 
-  u32x4_t v[8];
+  auto load_tile = [&](int ht, u32x4_t (&v)[8]) {
+    const int64_t p0 = static_cast<int64_t>(ht) * kTileHw + (lane & 7) * 8;
+    const int64_t pl = p0 < g.HW ? p0 : static_cast<int64_t>(ht) * kTileHw;
+    const int64_t in_off = (img * g.C + cl) * g.HW + pl;
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    v[j] = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4_t*>(x + in_off + j * g.HW));
+    for (int j = 0; j < 8; ++j)
+      v[j] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(x + in_off + j * g.HW));
+  };
+
+  // Stage the GELU table (7 KiB, L2-resident) first: loads return in issue
+  // order, so its LDS writes and the barrier complete while the tile's HBM
+  // loads, issued after it, are still in flight.
+  u32x4_t tab[(kGeluTableChunks + kBlockThreads - 1) / kBlockThreads];
+#pragma unroll
+  for (int k = 0; k < (kGeluTableChunks + kBlockThreads - 1) / kBlockThreads; ++k) {
+    const int i = static_cast<int>(threadIdx.x) + k * kBlockThreads;
+    if (i < kGeluTableChunks) tab[k] = reinterpret_cast<const u32x4_t*>(kGeluTable)[i];
+  }
+  u32x4_t va[8], vb[8];
+  load_tile(ht0, va);
   const u32x4_t bw = *reinterpret_cast<const u32x4_t*>(bias + cl);
+#pragma unroll
+  for (int k = 0; k < (kGeluTableChunks + kBlockThreads - 1) / kBlockThreads; ++k) {
+    const int i = static_cast<int>(threadIdx.x) + k * kBlockThreads;
+    if (i < kGeluTableChunks) reinterpret_cast<u32x4_t*>(lut)[i] = tab[k];
+  }
+  __syncthreads();
   float b[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) b[j] = (j & 1) ? bf16hi(bw[j >> 1]) : bf16lo(bw[j >> 1]);
 
-  if (!ok) return;
-  const int64_t out_off = (img * g.HW + p0) * g.C + c0;
+  auto gelu_store = [&](int ht, const u32x4_t (&v)[8]) {
+    const int64_t p0 = static_cast<int64_t>(ht) * kTileHw + (lane & 7) * 8;
+    if (!c_ok || p0 >= g.HW) return;
+    const int64_t out_off = (img * g.HW + p0) * g.C + c0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    // Position p0 + i, channels c0 .. c0 + 7: round t for two channels into
-    // one word (v_cvt_pk_bf16_f32), GELU both halves, pack the results.
-    u32x4_t o;
+    for (int i = 0; i < 8; ++i) {
+      // Position p0 + i, channels c0 .. c0 + 7: round t for two channels
+      // into one word (v_cvt_pk_bf16_f32), map both halves, pack them.
+      u32x4_t o, tt;
+      bool rare = false;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t w0 = v[2 * k][i >> 1];
-      const uint32_t w1 = v[2 * k + 1][i >> 1];
-      const float x0 = (i & 1) ? bf16hi(w0) : bf16lo(w0);
-      const float x1 = (i & 1) ? bf16hi(w1) : bf16lo(w1);
-      const uint32_t tt = pack_bf16x2(x0 + b[2 * k], x1 + b[2 * k + 1]);
-      o[k] = pack_bf16x2(gelu_tanh_f32(bf16lo(tt)), gelu_tanh_f32(bf16hi(tt)));
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t w0 = v[2 * k][i >> 1];
+        const uint32_t w1 = v[2 * k + 1][i >> 1];
+        const float x0 = (i & 1) ? bf16hi(w0) : bf16lo(w0);
+        const float x1 = (i & 1) ? bf16hi(w1) : bf16lo(w1);
+        tt[k] = pack_bf16x2(x0 + b[2 * k], x1 + b[2 * k + 1]);
+        o[k] = gelu_bits_common(tt[k] & 0xffffu, lut) |
+               (gelu_bits_common(tt[k] >> 16, lut) << 16);
+        rare |= gelu_rare(tt[k] & 0xffffu) | gelu_rare(tt[k] >> 16);
+      }
+      if (rare) {  // one branch per 8 values, not taken for ordinary data
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = gelu_bits(tt[k] & 0xffffu, lut) |
+                                           (gelu_bits(tt[k] >> 16, lut) << 16);
+      }
+      __builtin_nontemporal_store(
+          o, reinterpret_cast<u32x4_t*>(out + out_off + static_cast<int64_t>(i) * g.C));
     }
-    __builtin_nontemporal_store(
-        o, reinterpret_cast<u32x4_t*>(out + out_off + static_cast<int64_t>(i) * g.C));
+  };
+
+  // TPW consecutive position tiles per wave: the next tile's loads are
+  // issued before the current one is mapped and stored.
+#pragma unroll
+  for (int r = 0; r < TPW; ++r) {
+    const int ht = ht0 + r;
+    if (ht >= g.hw_tiles) break;  // wave-uniform; no barrier follows
+    const bool next = r + 1 < TPW && ht + 1 < g.hw_tiles;
+    if (r % 2 == 0) {
+      if (next) load_tile(ht + 1, vb);
+      gelu_store(ht, va);
+    } else {
+      if (next) load_tile(ht + 1, va);
+      gelu_store(ht, vb);
+    }
   }
 }
 
 // Any shape: one thread per output element, NHWC order (coalesced stores,
-// strided loads); same arithmetic as the tile kernel.
+// strided loads); the same mapping as the tile kernel, from the table in
+// global memory.
 __global__ __launch_bounds__(256) void bias_gelu_nchw_to_nhwc_scalar(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ out, int64_t N, int64_t C, int64_t HW) {
@@ -131,9 +222,10 @@ __global__ __launch_bounds__(256) void bias_gelu_nchw_to_nhwc_scalar(
     const int64_t c = o % C;
     const int64_t p = (o / C) % HW;
     const int64_t img = o / (C * HW);
-    const float t =
-        round_bf16(bf16_to_f32(x[(img * C + c) * HW + p]) + bf16_to_f32(bias[c]));
-    out[o] = static_cast<uint16_t>(pack_bf16x2(gelu_tanh_f32(t), 0.0f) & 0xffffu);
+    const uint32_t tb =
+        pack_bf16x2(bf16_to_f32(x[(img * C + c) * HW + p]) + bf16_to_f32(bias[c]), 0.0f) &
+        0xffffu;
+    out[o] = static_cast<uint16_t>(gelu_bits(tb, kGeluTable));
   }
 }
 
@@ -166,15 +258,16 @@ extern "C" int hipo_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x,
     g.hw_tiles = static_cast<int>(hw_tiles);
     g.ntiles = static_cast<int>(ntiles);
     const int64_t c_groups = (c_tiles + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (hw_tiles <= 65535 && n <= 65535) {
-      const dim3 grid(static_cast<unsigned>(c_groups), static_cast<unsigned>(hw_tiles),
+    const int64_t hw_groups = (hw_tiles + kTilesPerWave - 1) / kTilesPerWave;
+    if (hw_groups <= 65535 && n <= 65535) {
+      const dim3 grid(static_cast<unsigned>(c_groups), static_cast<unsigned>(hw_groups),
                       static_cast<unsigned>(n));
-      bias_gelu_nchw_to_nhwc_tiles<true><<<grid, dim3(kBlockThreads), 0, stream>>>(x, bias, out,
-                                                                                  g);
+      bias_gelu_nchw_to_nhwc_tiles<true, kTilesPerWave>
+          <<<grid, dim3(kBlockThreads), 0, stream>>>(x, bias, out, g);
     } else {
       const int64_t blocks = (ntiles + kWavesPerBlock - 1) / kWavesPerBlock;
-      bias_gelu_nchw_to_nhwc_tiles<false><<<dim3(static_cast<unsigned>(blocks)),
-                                            dim3(kBlockThreads), 0, stream>>>(x, bias, out, g);
+      bias_gelu_nchw_to_nhwc_tiles<false, 1><<<dim3(static_cast<unsigned>(blocks)),
+                                               dim3(kBlockThreads), 0, stream>>>(x, bias, out, g);
     }
   } else {
     const int64_t total = n * c * hw;

@@ -144,6 +144,34 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// e^x in fp32 to about one ulp, for x in [-104, 89] (NaN propagates), by
+// the extended-precision reduction of the device library's expf: x*log2(e)
+// is the rounded product ph plus a residual pl carried to first order (the
+// product's exact rounding error from an FMA, plus x times the rounding
+// error of the constant), so e^x = 2^ph * 2^pl = r * (1 + pl * ln2) with
+// r = 2^ph from the hardware exp2 (|pl| <= 2^-17 here, so the dropped
+// second-order term is below 2^-35 relative; the product form keeps
+// r = inf and r = 0 exact).  Unlike the library routine
+// the result is not rescaled by ldexp: results below 2^-126 (x < -87.3) are
+// whatever the hardware exp2 gives there (denormal or zero) -- below any
+// bf16 rounding these kernels apply.  Callers clamp x first (exp_domain):
+// e^-104 rounds to 0, e^89 overflows to inf.
+constexpr float kLog2eHi = 1.4426950216293335f;   // log2(e) rounded to fp32
+constexpr float kLog2eLo = 1.9259629891e-8f;      // log2(e) - kLog2eHi
+constexpr float kLn2 = 0.6931471805599453f;
+__device__ __forceinline__ float exp_f32(float x) {
+  const float ph = x * kLog2eHi;
+  const float pl = __builtin_fmaf(x, kLog2eLo, __builtin_fmaf(x, kLog2eHi, -ph));
+  const float r = __builtin_amdgcn_exp2f(ph);
+  return r * __builtin_fmaf(pl, kLn2, 1.0f);
+}
+
+// Clamp to the domain of exp_f32; NaN stays NaN (IEEE 754-2019 maximum /
+// minimum: v_maximum3_f32 / v_minimum3_f32 on gfx950).
+__device__ __forceinline__ float exp_domain(float x) {
+  return __builtin_elementwise_minimum(__builtin_elementwise_maximum(x, -104.0f), 89.0f);
+}
+
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 }  // namespace hipo

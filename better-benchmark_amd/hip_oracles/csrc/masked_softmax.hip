@@ -3,6 +3,9 @@
 // Semantics (eager op order of softmax(x * scale + mask, -1) on bf16):
 //   s = bf16(bf16(x * scale) + mask[q, :])       (each eager bf16 op rounds)
 //   out = bf16(exp(s - max(s)) / sum(exp(s - max(s))))   (fp32 max and sum)
+// exp is natural exp of the fp32 difference s - max(s) (as aten.exp and
+// Inductor's libdevice.exp), evaluated to about one ulp by exp_f32, the
+// device library's extended-precision reduction (no exp2 rewrite).
 // When `scale` is a power of two, x * scale is exact in fp32 and the first
 // rounding is the identity, so it is skipped.
 //
@@ -25,7 +28,13 @@
 namespace hipo {
 namespace {
 
-constexpr float kLog2e = 1.4426950408889634f;
+// exp(s - m): masked entries (s = -inf) give exactly 0; (-inf) - (-inf)
+// gives NaN for an all-masked row, exactly as the eager formula.
+constexpr uint32_t kNegInfPair = 0xFF80FF80u;  // two bf16 -inf
+
+__device__ __forceinline__ float exp_shifted(float s, float m) {
+  return exp_f32(exp_domain(s - m));
+}
 
 template <int U, int WT, bool ROUND_SCALE>
 __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
@@ -81,15 +90,12 @@ __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
     for (int k = 1; k < waves_per_row; ++k) m = fmaxf(m, pmax[first + k]);
   }
 
-  // exp(s - m) = 2^(s*log2e - m*log2e); (-inf) - (-inf) gives NaN exactly as
-  // the eager formula does for an all-masked row.
-  const float ml = m * kLog2e;
   float sum = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      s[u][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][e], kLog2e, -ml));
+      s[u][e] = exp_shifted(s[u][e], m);
       sum += s[u][e];
     }
   }
@@ -180,11 +186,10 @@ __global__ __launch_bounds__(kShortThreads) void masked_softmax_short_rows(
       m = fmaxf(m, fmaxf(s[2 * d], s[2 * d + 1]));
     }
     m = seg_max<L>(m);
-    const float ml = m * kLog2e;
     float sum = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      s[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], kLog2e, -ml));
+      s[e] = exp_shifted(s[e], m);
       sum += s[e];
     }
     const float inv = 1.0f / seg_sum<L>(sum);
@@ -280,6 +285,7 @@ __global__ __launch_bounds__(256) void masked_softmax_shared_mask(
   const u32x4_t mv = *reinterpret_cast<const u32x4_t*>(&mrow[col / 2]);
 
   float s[8];
+  uint32_t tw[4];  // the rounded scores as bf16 pairs
   float m = -__builtin_inff();
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
@@ -291,6 +297,7 @@ __global__ __launch_bounds__(256) void masked_softmax_shared_mask(
       a1 = bf16hi(r);
     }
     const uint32_t t = pack_bf16x2(a0 + bf16lo(mv[d]), a1 + bf16hi(mv[d]));
+    tw[d] = t;
     s[2 * d] = bf16lo(t);
     s[2 * d + 1] = bf16hi(t);
     m = fmaxf(m, fmaxf(s[2 * d], s[2 * d + 1]));
@@ -302,13 +309,21 @@ __global__ __launch_bounds__(256) void masked_softmax_shared_mask(
 #pragma unroll
   for (int k = 1; k < W; ++k) m = fmaxf(m, pmax[rr * W + k]);
 
-  // (-inf) - (-inf) gives NaN for an all-masked row, as the eager formula.
-  const float ml = m * kLog2e;
+  // A lane whose 8 scores are all -inf (a fully masked group: the causal
+  // mask's upper triangle makes whole waves of them) has exp = 0 for each;
+  // the test is on the rounded score words, so a NaN score still goes
+  // through exp and poisons the row as in eager.
   float sum = 0.f;
+  if ((tw[0] & tw[1] & tw[2] & tw[3]) == kNegInfPair &&
+      (tw[0] | tw[1] | tw[2] | tw[3]) == kNegInfPair) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    s[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], kLog2e, -ml));
-    sum += s[e];
+    for (int e = 0; e < 8; ++e) s[e] = 0.f;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s[e] = exp_shifted(s[e], m);
+      sum += s[e];
+    }
   }
   sum = wave_sum(sum);
   if (lane == 0) psum[wave] = sum;
@@ -395,14 +410,13 @@ __global__ __launch_bounds__(256) void masked_softmax_rows_scalar(
   float m = -__builtin_inff();
   for (int64_t j = lane; j < K; j += kWave) m = fmaxf(m, score(j));
   m = wave_max(m);
-  const float ml = m * kLog2e;
   float sum = 0.f;
   for (int64_t j = lane; j < K; j += kWave)
-    sum += __builtin_amdgcn_exp2f(__builtin_fmaf(score(j), kLog2e, -ml));
+    sum += exp_shifted(score(j), m);
   sum = wave_sum(sum);
   const float inv = 1.0f / sum;
   for (int64_t j = lane; j < K; j += kWave) {
-    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(score(j), kLog2e, -ml));
+    const float e = exp_shifted(score(j), m);
     orow[j] = static_cast<uint16_t>(pack_bf16x2(e * inv, 0.f) & 0xffffu);
   }
 }

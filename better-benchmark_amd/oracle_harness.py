@@ -556,6 +556,17 @@ def _compare_oracle_outputs(eager, oracle_out, stochastic, *, atol, rtol) -> boo
     return ok_all
 
 
+def _device_fault_messages() -> list[str]:
+    """Faults that HIP kernels recorded in device memory since the last check
+    (a bounded cross-workgroup wait that timed out leaves NaN outputs behind
+    a successful launch).  Reads and clears the words; synchronises.  Empty
+    when no kernel library with such words is loaded."""
+    mod = sys.modules.get("hip_oracles")
+    if mod is None or not hasattr(mod, "device_faults") or not torch.cuda.is_available():
+        return []
+    return mod.device_faults(clear=True)
+
+
 def check_oracle(oracle_forward, instance, inputs, *, atol: float = 1e-2,
                  rtol: float = 1e-2, skip_stochastic: bool = True) -> bool:
     """Eager vs oracle on the same inputs (reference :926-963)."""
@@ -565,9 +576,14 @@ def check_oracle(oracle_forward, instance, inputs, *, atol: float = 1e-2,
         print(f"  NO_ORACLE_FOR_SHAPE: {str(e)[:200]}")
         return False
     stochastic = detect_stochastic_outputs(instance, inputs) if skip_stochastic else set()
+    _device_fault_messages()  # start clean: report only this call's faults
     with torch.no_grad():
         eager = instance(*inputs)
         got = oracle_forward(inputs)
+    faults = _device_fault_messages()
+    if faults:
+        print(f"  DEVICE_FAULT: {'; '.join(faults)[:300]}")
+        return False
     return _compare_oracle_outputs(eager, got, stochastic, atol=atol, rtol=rtol)
 
 
@@ -615,9 +631,15 @@ def check_oracle_all_shapes(oracle_forward, repro_dir, repro_id: str, *,
             print(f"  NO_ORACLE_FOR_SHAPE: {str(e)[:200]}")
             results[label] = False
             continue
+        _device_fault_messages()
         with torch.no_grad():
             eager = instance(*eager_inputs)
             got = selected(oracle_inputs)
+        faults = _device_fault_messages()
+        if faults:
+            print(f"  DEVICE_FAULT: {'; '.join(faults)[:300]}")
+            results[label] = False
+            continue
         results[label] = _compare_oracle_outputs(eager, got, stochastic, atol=atol, rtol=rtol)
     return results
 
@@ -714,11 +736,17 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def host_cpu_threads() -> int:
+    """Threads for the host-CPU eager baseline: os.cpu_count()."""
+    return os.cpu_count() or 1
+
+
 def time_cpu_eager(instance, inputs, *, warmup: int = 1, rep: int = 5,
                    threads: int | None = None) -> dict:
     """Eager repro on the host CPU: warmup, then min of `rep` perf_counter runs
-    (the method of the reference's _do_bench CPU path, :1734-1748)."""
-    threads = threads or min(os.cpu_count() or 1, 16)
+    (the method of the reference's _do_bench CPU path, :1734-1748), on
+    `threads` torch threads (default os.cpu_count())."""
+    threads = threads or host_cpu_threads()
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
@@ -735,25 +763,39 @@ def time_cpu_eager(instance, inputs, *, warmup: int = 1, rep: int = 5,
                     best = min(best, dt)
     finally:
         torch.set_num_threads(prev)
-    return {"cpu_eager_us": round(best, 1), "cpu_threads": threads, "cpu_model": _cpu_model()}
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"cpu_eager_us": round(best, 1), "cpu_threads": threads, "cpu_model": _cpu_model(),
+            "cpu_affinity": affinity}
 
 
 def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int = 25,
                  rep: int = 200, rounds: int = 5, _skip_numerics_gate: bool = False,
                  numerics_optout: dict | None = None, disable_gpu_lock: bool = False,
-                 compare_compile: bool = True, flush_bytes: int = DEFAULT_FLUSH_BYTES,
+                 compare_compile: bool = True, coordinate_descent: bool = True,
+                 flush_bytes: int = DEFAULT_FLUSH_BYTES,
                  cpu_eager: bool = False, hardware: str | None = None) -> dict:
     """Time one oracle point on the GPU (reference :1057-1287, ROCm path).
 
-    Steps: resolve dispatch; optional torch.compile comparator captured in a
-    graph; oracle captured in a hipGraph (any graph-related warning during
-    capture -> INVALID_CUDAGRAPH_WARNING); fp64-anchored numerics gate
-    against the compiled output (or GPU eager when there is no compiled
-    comparator); then, under the exclusive GPU lock, `rounds` interleaved
-    rounds of `rep` hipEvent-timed replays with a cache flush before each.
-    Reports min-of-rounds µs, effective bytes, GB/s and fraction of the HBM
-    peak.  Status: GOOD / AT_FLOOR / BAD_ORACLE vs compiled at +-5 %,
-    ORACLE_ONLY without a comparator, or an invalid status.
+    Steps: resolve dispatch; torch.compile comparator (Inductor, coordinate
+    descent on as in the reference) captured in a graph; oracle captured in a
+    hipGraph (any graph-related warning during capture ->
+    INVALID_CUDAGRAPH_WARNING); fp64-anchored numerics gate against the
+    compiled output (GPU eager when there is no compiled comparator); then,
+    under the exclusive GPU lock, `rounds` interleaved rounds of `rep`
+    hipEvent-timed graph replays of oracle and compiled, a cache flush before
+    each.  `oracle_us` / `compile_us` are the min-of-rounds graph-replay
+    times, as in the reference (:1225-1241), and the status GOOD / AT_FLOOR /
+    BAD_ORACLE at +-5 % (:1243-1255) comes from them; ORACLE_ONLY without a
+    comparator.  Also reported: the oracle's direct-launch minimum
+    (`oracle_launch_us`, no graph-launch gap inside the event pair), effective
+    bytes and, from the direct-launch time, GB/s and the fraction of the HBM
+    peak after a read flush (`clean_cache_*`: the Infinity Cache is clean then
+    and can absorb part of the writes, so these flatter write-heavy kernels).
+    A fault recorded by a kernel (hip_oracles.device_faults) gives
+    ORACLE_DEVICE_FAULT.
     """
     from byte_accounting import HBM_PEAK_BYTES_PER_S, achieved_gbps, sol_fraction
     dispatch_info = None
@@ -778,6 +820,15 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
             result["dispatch"] = d
         return result
 
+    def device_fault(where):
+        faults = _device_fault_messages()
+        if not faults:
+            return None
+        result = {"repro_id": repro_id, "status": "ORACLE_DEVICE_FAULT", "where": where,
+                  "faults": faults[:5]}
+        print(json.dumps(with_dispatch(result)))
+        return result
+
     device = _get_device(inputs)
     if device.type != "cuda":
         return _bench_oracle_cpu(oracle_forward, instance, inputs, repro_id,
@@ -788,17 +839,21 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
 
     compiled = g_compile = None
     compile_error = None
+    compile_wall_s = None
     if compare_compile:
         try:
             import importlib
             icfg = importlib.import_module("torch._inductor.config")
-            icfg.coordinate_descent_tuning = True
+            icfg.coordinate_descent_tuning = bool(coordinate_descent)
+            # Fresh dynamo state per shape, as the reference (:1143-1146).
             importlib.import_module("torch._dynamo").reset()
+            t0 = time.perf_counter()
             compiled = torch.compile(instance)
             with torch.no_grad():
                 for _ in range(5):
                     compiled(*inputs)
             torch.cuda.synchronize()
+            compile_wall_s = time.perf_counter() - t0
             g_compile, warns = _capture_graph_checked(lambda: compiled(*inputs))
             if warns:
                 result = {"repro_id": repro_id, "status": "INVALID_CUDAGRAPH_WARNING",
@@ -807,12 +862,16 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
                 return result
         except Exception as e:  # Inductor unavailable: oracle still timed
             compiled = g_compile = None
-            compile_error = f"{type(e).__name__}: {str(e)[:200]}"
+            compile_error = f"{type(e).__name__}: {str(e)[:300]}"
 
+    _device_fault_messages()
     with torch.no_grad():
         for _ in range(3):
             oracle_forward(inputs)
     torch.cuda.synchronize()
+    bad = device_fault("warmup")
+    if bad:
+        return bad
     g_oracle, warns = _capture_graph_checked(lambda: oracle_forward(inputs))
     if warns:
         result = {"repro_id": repro_id, "status": "INVALID_CUDAGRAPH_WARNING",
@@ -827,6 +886,9 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
         numerics_result = _run_anchored_numerics_gate(oracle_forward, instance, comparator, inputs)
         if numerics_result is not None:
             numerics_result["comparator"] = "compiled" if compiled is not None else "eager"
+        bad = device_fault("numerics_gate")
+        if bad:
+            return bad
         if numerics_result is not None and not numerics_result["pass"]:
             verdict = numerics_optout_applies(numerics_result, numerics_optout)
             if verdict["accept"]:
@@ -845,19 +907,16 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
         with torch.no_grad():
             oracle_forward(inputs)
 
-    def run_compiled():
-        with torch.no_grad():
-            compiled(*inputs)
-
-    quick, _ = _time_launches(run_oracle, 3, 10, flush=flush)
+    # Adaptive rep count from a quick estimate (reference :1216-1223).
+    quick, _ = _time_graph(g_oracle, 3, 10, flush=flush)
     if g_compile is not None:
-        quick = min(quick, _time_launches(run_compiled, 3, 10, flush=flush)[0])
+        quick = min(quick, _time_graph(g_compile, 3, 10, flush=flush)[0])
     if quick < 50:
         rep = max(rep, 500)
     elif quick < 200:
         rep = max(rep, 300)
 
-    best_oracle = best_compile = best_graph = best_compile_graph = math.inf
+    best_graph = best_compile_graph = best_launch = math.inf
     medians = []
     with _gpu_exclusive_lock(repro_id, disabled=disable_gpu_lock):
         for _ in range(warmup):
@@ -865,19 +924,22 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
             if g_compile is not None:
                 g_compile.replay()
         torch.cuda.synchronize()
+        # Interleaved rounds, min-of-N (reference :1225-1241).
         for _ in range(rounds):
-            o_min, o_med = _time_launches(run_oracle, warmup, rep, flush=flush)
-            best_oracle = min(best_oracle, o_min)
-            medians.append(o_med)
-            best_graph = min(best_graph, _time_graph(g_oracle, warmup, rep, flush=flush)[0])
+            g_min, g_med = _time_graph(g_oracle, warmup, rep, flush=flush)
+            best_graph = min(best_graph, g_min)
+            medians.append(g_med)
             if g_compile is not None:
-                best_compile = min(best_compile,
-                                   _time_launches(run_compiled, warmup, rep, flush=flush)[0])
                 best_compile_graph = min(best_compile_graph,
                                          _time_graph(g_compile, warmup, rep, flush=flush)[0])
+            best_launch = min(best_launch,
+                              _time_launches(run_oracle, warmup, rep, flush=flush)[0])
+    bad = device_fault("timing")
+    if bad:
+        return bad
 
     if g_compile is not None:
-        ratio = best_compile / best_oracle if best_oracle > 0 else 0.0
+        ratio = best_compile_graph / best_graph if best_graph > 0 else 0.0
         if optout_verdict is not None:
             status = "NUMERICS_OPTOUT_ACCEPTED"
         elif ratio > 1.05:
@@ -892,25 +954,30 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
 
     result = {
         "repro_id": repro_id,
-        "oracle_us": round(best_oracle, 2),
-        "oracle_median_us": round(sorted(medians)[len(medians) // 2], 2),
-        "oracle_graph_us": round(best_graph, 2),
-        "compile_us": round(best_compile, 2) if g_compile is not None else None,
-        "compile_graph_us": round(best_compile_graph, 2) if g_compile is not None else None,
+        "oracle_us": round(best_graph, 2),
+        "compile_us": round(best_compile_graph, 2) if g_compile is not None else None,
         "ratio": round(ratio, 3) if ratio is not None else None,
         "status": status,
+        "oracle_median_us": round(sorted(medians)[len(medians) // 2], 2),
+        "oracle_launch_us": round(best_launch, 2),
         "hardware": hw,
         "bytes": nbytes,
     }
     if nbytes:
-        result["gbps"] = round(achieved_gbps(nbytes, best_oracle), 1)
+        result["clean_cache_gbps"] = round(achieved_gbps(nbytes, best_launch), 1)
         if hw in HBM_PEAK_BYTES_PER_S:
-            result["sol_frac"] = round(sol_fraction(nbytes, best_oracle, hw), 4)
+            result["clean_cache_sol_frac"] = round(sol_fraction(nbytes, best_launch, hw), 4)
             result["sol_peak_gbps"] = HBM_PEAK_BYTES_PER_S[hw] / 1e9
-    result["timing"] = {"method": "hipevent pair per launch, cache-flush read before each",
-                        "graph_method": "hipevent pair per hipGraph replay",
+    result["timing"] = {"method": "hipevent pair per hipGraph replay, cache-flush read "
+                                  "before each; min over rounds (oracle_us, compile_us)",
+                        "launch_method": "hipevent pair per direct launch (oracle_launch_us)",
                         "rep": rep, "rounds": rounds,
                         "flush_bytes": flush.nbytes if flush else 0}
+    if compare_compile:
+        result["compile"] = {"backend": "inductor",
+                             "coordinate_descent_tuning": bool(coordinate_descent),
+                             "compile_wall_s": (round(compile_wall_s, 1)
+                                                if compile_wall_s is not None else None)}
     if compile_error:
         result["compile_error"] = compile_error
     if numerics_result is not None:
@@ -1234,6 +1301,8 @@ _INVALID_STATUSES = frozenset({
     "INVALID_CUDAGRAPH_WARNING",
     "NUMERICS_WORSE_THAN_COMPILED",
     "NO_ORACLE_FOR_SHAPE",
+    # Not in the reference: a kernel recorded a fault (its outputs are NaN).
+    "ORACLE_DEVICE_FAULT",
 })
 
 

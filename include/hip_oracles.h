@@ -271,6 +271,21 @@ int hipo_batchnorm_train_fwd_f32(const float* x, const float* gamma,
                                  void* workspace, size_t workspace_bytes,
                                  hipStream_t stream);
 
+/*
+ * Flat stream copy (a measurement yardstick, not an oracle): reads
+ * read_bytes from src and writes write_bytes to dst in one launch with the
+ * oracle kernels' access style (16-byte non-temporal accesses, 1 KiB per
+ * wave, one-shot grid in memory order); chunk i of dst receives chunk i of
+ * src where both exist.  Sizes are multiples of 1024 (write_bytes >= 1024),
+ * pointers 16-byte aligned.  The time of this copy at a config's read and
+ * write bytes is the ceiling the config's kernel is compared with.
+ * Counterpart of the reference's memcopy speed-of-light construction
+ * (repro_harness.py:952-958, an fp32 add(src, 1, out=dst) over the same
+ * bytes), written for MI355X with the stores that kernel lacks.
+ */
+int hipo_flat_copy(const void* src, int64_t read_bytes, void* dst,
+                   int64_t write_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -4,7 +4,15 @@ Inputs are generated on the CPU (seed 1, the harness's oracle seed) and
 copied to the device, so all three see identical data.  Tolerances (from
 the BASELINE north star):
   fp32 outputs (means, rstd, BN y / stats / running stats): rtol = atol = 1e-5
-  bf16 outputs (fp32 accumulation inside):                  rtol = atol = 1.6e-2
+  bf16 outputs (fp32 accumulation inside): rtol = 1.6e-2 (relative), with an
+    absolute floor per output for values near zero, where a relative bound
+    means nothing: 1e-6 for softmax probabilities, GELU and RMSNorm y (pure
+    products and quotients), 1e-5 for LayerNorm y ((h - mean) * rstd * gamma
+    + beta cancels near zero), 1e-5 elsewhere; the residual sum h is exact.
+  At every BASELINE point each bf16 output is also within one bf16 ulp of the
+  C oracle's correctly rounded value wherever |value| >= the output's ulp
+  floor (an fp32 evaluation rounds to a neighbour of the correct bf16 only
+  when it lands within a few fp32 ulps of a rounding boundary).
 Integer/index work: none on this path.
 """
 import importlib.util
@@ -17,24 +25,67 @@ from conftest import CANONICAL, REPRO_IDS, VARIANT_IDS
 
 pytestmark = pytest.mark.gpu
 
-F32_TOL = 1e-5
-BF16_TOL = 1.6e-2
+F32_TOL = (1e-5, 1e-5)          # (rtol, atol)
+BF16_TOL = (1.6e-2, 1e-5)        # bf16 default: relative, 1e-5 floor
+PROB_TOL = (1.6e-2, 1e-6)        # softmax probabilities, GELU, RMSNorm y
+EXACT = (0.0, 0.0)
+
+# Per BASELINE repro: (rtol, atol) and the ulp floor of each output (None:
+# fp32 output, no ulp check; the floor is where the one-ulp bound starts).
+OUTPUT_TOLS = {
+    "mean_lastdim_f32": [(F32_TOL, None)],
+    # GELU: below ~1e-4 the tanh form's 1 + tanh(u) cancels (eager does the
+    # same), so the result is only pinned by the 1e-6 absolute floor there.
+    "pointwise_bias_gelu_tanh_nhwc": [(PROB_TOL, 1e-4)],
+    "amax_sum_scaled_masked_softmax": [(PROB_TOL, 0.0)],
+    "var_mean_residual_layernorm": [(EXACT, 0.0), (BF16_TOL, 1e-5), (F32_TOL, None),
+                                    (F32_TOL, None)],
+    "mean_rmsnorm": [(PROB_TOL, 1e-6), (F32_TOL, None)],
+    "var_mean_batchnorm_train_relu": [(F32_TOL, None)] * 5,
+}
 
 
 def _tol(t):
     return BF16_TOL if t.dtype == torch.bfloat16 else F32_TOL
 
 
+def _rtol_atol(tol):
+    return (tol, tol) if isinstance(tol, float) else tol
+
+
 def assert_close(got, want, tol, what):
+    rtol, atol = _rtol_atol(tol)
     g = got.detach().float().cpu()
     w = want.detach().float().cpu()
     assert g.shape == w.shape, f"{what}: shape {tuple(g.shape)} != {tuple(w.shape)}"
-    ok = torch.allclose(g, w, rtol=tol, atol=tol, equal_nan=True)
+    ok = torch.allclose(g, w, rtol=rtol, atol=atol, equal_nan=True)
     if not ok:
         d = (g - w).abs().nan_to_num(0)
-        idx = int(d.argmax())
-        pytest.fail(f"{what}: max |diff| {d.max().item():.3e} at flat {idx} "
-                    f"(got {g.flatten()[idx].item()}, want {w.flatten()[idx].item()}), tol {tol}")
+        excess = (d - atol - rtol * w.abs()).nan_to_num(0)
+        idx = int(excess.argmax())
+        pytest.fail(f"{what}: |diff| {d.flatten()[idx].item():.3e} at flat {idx} "
+                    f"(got {g.flatten()[idx].item()}, want {w.flatten()[idx].item()}), "
+                    f"rtol {rtol}, atol {atol}; max |diff| {d.max().item():.3e}")
+
+
+def bf16_ulp_distance(a, b):
+    """|a - b| in bf16 ulps (ordered integer codes; +0 and -0 coincide)."""
+    def code(t):
+        v = t.detach().cpu().contiguous().view(torch.int16).int()
+        return torch.where(v < 0, -(v & 0x7FFF), v)
+    return (code(a) - code(b)).abs()
+
+
+def assert_bf16_ulps(got, want, floor, what, max_ulp=1):
+    """Every finite bf16 value with |want| >= floor within max_ulp ulps of
+    want; returns the number of values that differ at all."""
+    w = want.detach().float().cpu()
+    sel = torch.isfinite(w) & (w.abs() >= floor)
+    d = bf16_ulp_distance(got, want)[sel]
+    worst = int(d.max()) if d.numel() else 0
+    assert worst <= max_ulp, (f"{what}: {int((d > max_ulp).sum())} values more than "
+                              f"{max_ulp} bf16 ulp from the oracle (worst {worst})")
+    return int((d > 0).sum())
 
 
 def _load(rid):
@@ -79,15 +130,21 @@ def test_all_points_vs_oracle_and_eager(rid, rocm_device):
         got = _normalize_outputs(impl(dev_in))
         torch.cuda.synchronize()
         want = _oracle_outputs(rid, cpu_in)
-        assert len(got) == len(want)
-        for i, (g, w) in enumerate(zip(got, want)):
+        assert len(got) == len(want) == len(OUTPUT_TOLS[rid])
+        for i, (g, w, (tol, floor)) in enumerate(zip(got, want, OUTPUT_TOLS[rid])):
             assert g.dtype == w.dtype, f"{label} out{i} dtype"
             assert g.stride() == w.stride(), f"{label} out{i} strides {g.stride()} vs {w.stride()}"
-            assert_close(g, w, _tol(w), f"{rid}/{label} out{i} vs oracle")
+            assert_close(g, w, tol, f"{rid}/{label} out{i} vs oracle")
+            if floor is not None:
+                flips = assert_bf16_ulps(g, w, floor, f"{rid}/{label} out{i} vs oracle")
+                print(f"[{rid}] {label} out{i}: {flips} of {w.numel()} values one bf16 ulp "
+                      f"off the correctly rounded oracle", flush=True)
         with torch.no_grad():
             eager = _normalize_outputs(inst(*[t.clone() for t in cpu_in]))
-        for i, (g, e) in enumerate(zip(got, eager)):
-            assert_close(g, e, _tol(e), f"{rid}/{label} out{i} vs eager")
+        for i, (g, e, (tol, _)) in enumerate(zip(got, eager, OUTPUT_TOLS[rid])):
+            # Eager is itself up to one ulp off the correctly rounded value:
+            # the residual sum is exact, the rest within the stated tolerance.
+            assert_close(g, e, tol, f"{rid}/{label} out{i} vs eager")
         del cpu_in, dev_in, got, want, eager
 
 
@@ -147,7 +204,15 @@ def test_family_points_vs_eager(rid, rocm_device):
             assert g.stride() == e.stride(), f"{label} out{i} strides {g.stride()} vs {e.stride()}"
             assert_close(g, o.reshape(e.shape), _tol(e), f"{rid}/{label} out{i} vs oracle")
             assert_close(g, e, _tol(e), f"{rid}/{label} out{i} vs eager")
-            assert_close(g, x, _tol(e), f"{rid}/{label} out{i} vs fp64")
+            # fp64 skips the graph's intermediate bf16 roundings, so it is an
+            # anchor, not a tolerance target: the reference's gate rule
+            # (oracle_harness.py:1511-1530) -- no worse than 3x eager's error.
+            xf = x.double().cpu()
+            err_k = (g.double().cpu() - xf).abs().nan_to_num(0).max().item()
+            err_e = (e.double().cpu() - xf).abs().nan_to_num(0).max().item()
+            bound = max(3 * err_e, 1e-5 * max(xf.abs().nan_to_num(0).max().item(), 1.0))
+            assert err_k <= bound, (f"{rid}/{label} out{i}: error vs fp64 {err_k:.3e} > "
+                                    f"3 x eager's {err_e:.3e}")
         del cpu_in, dev_in, got, eager, exact, oracle_out
 
 
@@ -191,9 +256,9 @@ def test_bias_gelu_edges(rocm_device):
     x = x.view(1, 1, 1, 8).repeat(1, 8, 1, 1).contiguous()
     out = hip_oracles.bias_gelu_nchw_to_nhwc(x.to(rocm_device), torch.zeros(8, dtype=bf, device=rocm_device)).cpu()
     want = torch.nn.functional.gelu(x.float(), approximate="tanh").to(bf)
-    assert_close(out[..., :4], want[..., :4], BF16_TOL, "gelu large |t|")
+    assert_close(out[..., :4], want[..., :4], PROB_TOL, "gelu large |t|")
     assert out[0, 0, 0, 4].item() == float("inf") and math.isnan(out[0, 0, 0, 5].float().item())
-    assert_close(out[..., 6:], want[..., 6:], BF16_TOL, "gelu +-0.5")
+    assert_close(out[..., 6:], want[..., 6:], PROB_TOL, "gelu +-0.5")
     # shapes off the vector path (C % 8, HW % 8) and partial channel groups
     # (65537, 8, 1, 8): more images than a grid's z dimension holds, so the
     # tile kernel takes its 1-D numbering instead of the 3-D grid
@@ -203,19 +268,22 @@ def test_bias_gelu_edges(rocm_device):
         b = (0.1 * torch.randn(shape[1], generator=g)).to(bf)
         got = hip_oracles.bias_gelu_nchw_to_nhwc(x.to(rocm_device), b.to(rocm_device))
         assert got.is_contiguous(memory_format=torch.channels_last)
-        assert_close(got, ref.bias_gelu_nchw_to_nhwc(x, b), BF16_TOL, f"gelu {shape}")
+        assert_close(got, ref.bias_gelu_nchw_to_nhwc(x, b), PROB_TOL, f"gelu {shape}")
 
 
 def test_bias_gelu_every_bf16_input(rocm_device):
     """All 65536 bf16 bit patterns as x (bias 0), through both the tile
     kernel (C = 8, HW = 2048) and the scalar path (C = 8, HW = 8193).
 
-    The kernel evaluates GELU in fp32 (as eager does) and rounds once, so it
-    matches the oracle's correctly rounded fp64 GELU except where the fp32
-    value sits within a few ulps of a bf16 rounding boundary: there the two
-    differ by one bf16 ulp.  Bar: every finite input within the bf16
-    tolerance; outside the far negative tail (|y| < 1e-12) at most 64 inputs
-    differ at all, each by exactly one ulp; special values as eager."""
+    The kernel evaluates eager's tanh GELU in fp32 with the device library's
+    tanhf and rounds once, so it matches the oracle's correctly rounded fp64
+    GELU except (a) where the fp32 value sits within a few ulps of a bf16
+    rounding boundary: there the two differ by one bf16 ulp; (b) in the far
+    negative tail, where 1 + tanh(u) cancels in fp32 (as in eager) and only
+    the absolute floor pins the result.  Bar: every finite input within
+    rtol 1.6e-2 / atol 1e-6; every value with |y| >= 1e-5 within one ulp, at
+    most 64 of them off at all; special values as eager.  The counts are
+    printed."""
     import hip_oracles
     import oracle as ref
     bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
@@ -228,16 +296,58 @@ def test_bias_gelu_every_bf16_input(rocm_device):
         g, w = got.float(), want.float()
         xf = x.float()
         finite = torch.isfinite(xf)
-        assert_close(torch.where(finite, g, 0), torch.where(finite, w, 0), BF16_TOL,
+        assert_close(torch.where(finite, g, 0), torch.where(finite, w, 0), PROB_TOL,
                      f"gelu every input ({what})")
-        exact = (got.view(torch.int16) == want.view(torch.int16)) | (torch.isnan(g) & torch.isnan(w))
-        off = finite & ~exact & (w.abs() >= 1e-12)
-        ulps = (got.view(torch.int16).int() - want.view(torch.int16).int()).abs()
+        sel = finite & (w.abs() >= 1e-5)
+        ulps = bf16_ulp_distance(got, want)
+        off = sel & (ulps > 0)
+        tail = finite & ~sel & (ulps > 0)
+        print(f"gelu every input ({what}): {int(off.sum())} of {int(sel.sum())} values with "
+              f"|y| >= 1e-5 one ulp off; {int(tail.sum())} tail values (|y| < 1e-5) differ, "
+              f"max |diff| {float((g - w)[tail].abs().max()) if tail.any() else 0.0:.2e}",
+              flush=True)
         assert int(off.sum()) <= 64, f"{what}: {int(off.sum())} inputs off the correctly rounded GELU"
         assert (ulps[off] == 1).all(), f"{what}: a result more than one bf16 ulp off"
         assert torch.isnan(g[torch.isnan(xf)]).all()
         assert (g[xf == float("inf")] == float("inf")).all()
         assert torch.isnan(g[xf == float("-inf")]).all()
+
+
+def test_bias_gelu_is_the_correctly_rounded_gelu(rocm_device):
+    """Bit for bit, over all 65536 bf16 t (bias 0, tile and scalar kernels):
+    the kernel's output is the exact GELU_tanh(t) rounded to nearest even
+    (the mapping tests/test_gelu_table.py pins against mpmath on the CPU);
+    NaN in, NaN out."""
+    import importlib.util
+    import hip_oracles
+    from conftest import PKG
+    pytest.importorskip("mpmath")
+    spec = importlib.util.spec_from_file_location(
+        "gen_gelu_table", PKG / "hip_oracles" / "gen_gelu_table.py")
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    want = []
+    for tb in range(65536):
+        mag = tb & 0x7FFF
+        if mag >= 0x7F80 or mag < 0x100:  # inf, NaN: as eager; subnormal t: t / 2
+            want.append(None)
+        else:
+            want.append(gen.to_bf16(gen.gelu_tanh_exact(gen.bf16_value(tb))))
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    xs = bits.view(torch.bfloat16)
+    b = torch.zeros(8, dtype=torch.bfloat16)
+    for what, x, order in (("tiles", xs.reshape(4, 8, 64, 32).contiguous(), None),
+                           ("scalar", torch.cat([xs, xs[:8]]).reshape(1, 8, 8193, 1).contiguous(),
+                            None)):
+        got = hip_oracles.bias_gelu_nchw_to_nhwc(x.to(rocm_device), b.to(rocm_device)).cpu()
+        g = got.contiguous(memory_format=torch.contiguous_format).view(torch.int16).reshape(-1)
+        tin = x.view(torch.int16).reshape(-1)
+        bad = 0
+        for tv, gv in zip(tin.tolist(), g.tolist()):
+            w = want[tv & 0xFFFF]
+            if w is not None and (gv & 0xFFFF) != w:
+                bad += 1
+        assert bad == 0, f"{what}: {bad} inputs differ from the correctly rounded GELU"
 
 
 def test_softmax_closed_forms(rocm_device):
@@ -252,7 +362,7 @@ def test_softmax_closed_forms(rocm_device):
     cols = torch.arange(k).view(1, k)
     want = torch.where(cols <= rows, 1.0 / (rows + 1).float(), torch.zeros(()))
     want = want.to(bf).float().expand(2, q, k)
-    assert_close(out, want, BF16_TOL, "uniform causal row -> 1/(q+1)")
+    assert_close(out, want, PROB_TOL, "uniform causal row -> 1/(q+1)")
     assert (out.masked_select((cols > rows).expand(2, q, k)) == 0).all(), "masked entries must be exactly 0"
     # fully masked row -> NaN everywhere (as eager)
     full = torch.full((4, 64), float("-inf")).to(bf)
@@ -265,7 +375,7 @@ def test_softmax_closed_forms(rocm_device):
         x = (3 * torch.randn(b_, q_, k_, generator=g)).to(bf)
         m = torch.triu(torch.full((q_, k_), float("-inf")), 1).to(bf)
         got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), m.to(rocm_device), scale)
-        assert_close(got, ref.scaled_masked_softmax(x, m, scale), BF16_TOL, f"softmax {k_} {scale}")
+        assert_close(got, ref.scaled_masked_softmax(x, m, scale), PROB_TOL, f"softmax {k_} {scale}")
     # rows sum to 1 (bf16 outputs, fp32 sum)
     x = torch.randn(4, 128, 1024).to(bf)
     got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), mask[:128].contiguous().to(rocm_device), 0.125)
@@ -289,20 +399,20 @@ def test_softmax_short_rows(rocm_device):
             m[q // 2] = float("-inf")                      # one fully masked row -> NaN
             got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), m.to(rocm_device), scale)
             want = ref.scaled_masked_softmax(x, m, scale)
-            assert_close(got, want, BF16_TOL, what)
+            assert_close(got, want, PROB_TOL, what)
             assert torch.isnan(got[:, q // 2].float()).all().item(), what + " masked row"
         x = torch.randn(12, 9, k).to(bf)
         bias = torch.randn(3, 9, k).to(bf)
         got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), 1.0, 4)
         want = torch.softmax((x.view(3, 4, 9, k) + bias.unsqueeze(1)).float(), -1).to(bf).view(12, 9, k)
-        assert_close(got, want, BF16_TOL, f"short bias softmax k={k}")
+        assert_close(got, want, PROB_TOL, f"short bias softmax k={k}")
     # the TrOCR shape: 1024 rows of 256 per group of 16 heads
     g = torch.Generator().manual_seed(11)
     x = torch.randn(64, 256, 256, generator=g).to(bf)
     bias = torch.randn(4, 256, 256, generator=g).to(bf)
     got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), 1.0, 16)
     want = torch.softmax((x.view(4, 16, 256, 256) + bias.unsqueeze(1)).float(), -1).to(bf).view(64, 256, 256)
-    assert_close(got, want, BF16_TOL, "trocr-like")
+    assert_close(got, want, PROB_TOL, "trocr-like")
     assert_close(got.float().sum(-1), torch.ones(64, 256), 1e-2, "row sums")
 
 
@@ -326,7 +436,7 @@ def test_softmax_mid_rows(rocm_device):
             m[q // 2] = float("-inf")                      # one fully masked row -> NaN
             got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), m.to(rocm_device), scale)
             want = ref.scaled_masked_softmax(x, m, scale)
-            assert_close(got, want, BF16_TOL, what)
+            assert_close(got, want, PROB_TOL, what)
             assert torch.isnan(got[:, q // 2].float()).all().item(), what + " masked row"
     for b, heads, q, k in ((12, 4, 9, 768), (9, 3, 9, 768), (6, 1, 5, 1024), (4, 2, 6, 2048),
                            (3, 3, 4, 1536), (8, 2, 7, 1024), (6, 6, 3, 1024), (3, 1, 5, 2048)):
@@ -336,17 +446,17 @@ def test_softmax_mid_rows(rocm_device):
         x = torch.randn(b, q, k, generator=g).to(bf)
         bias = torch.randn(b // heads, q, k, generator=g).to(bf)
         got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), 1.0, heads)
-        assert_close(got, ref.scaled_bias_softmax(x, bias, 1.0, heads), BF16_TOL, what)
+        assert_close(got, ref.scaled_bias_softmax(x, bias, 1.0, heads), PROB_TOL, what)
         # each batch entry's rows against a direct fp32 softmax of its own bias group
         want = torch.softmax((x.float().view(b // heads, heads, q, k) + bias.float().unsqueeze(1))
                              .to(bf).float(), -1).to(bf).view(b, q, k)
-        assert_close(got, want, BF16_TOL, what + " vs torch")
+        assert_close(got, want, PROB_TOL, what + " vs torch")
         # the same bias as a padded view: row stride k + 8, batch stride q (k + 8)
         padded = torch.randn(b // heads, q, k + 8, generator=g).to(bf)
         got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), padded.to(rocm_device)[:, :, :k],
                                               1.0, heads)
         assert_close(got, ref.scaled_bias_softmax(x, padded[:, :, :k].contiguous(), 1.0, heads),
-                     BF16_TOL, what + " padded bias rows")
+                     PROB_TOL, what + " padded bias rows")
 
 
 def test_norm_closed_forms(rocm_device):
@@ -360,7 +470,7 @@ def test_norm_closed_forms(rocm_device):
     h, y, mean, rstd = hip_oracles.residual_layernorm(*(t.to(rocm_device) for t in (x, r, gamma, beta)), eps)
     assert torch.equal(h.cpu(), torch.full((3, 4096), 2.0, dtype=bf))
     assert torch.equal(mean.cpu(), torch.full((3,), 2.0))
-    assert_close(rstd, torch.full((3,), 1 / math.sqrt(eps)), F32_TOL * 1 / math.sqrt(eps), "rstd=1/sqrt(eps)")
+    assert_close(rstd, torch.full((3,), 1 / math.sqrt(eps)), (1e-5, 1e-5 / math.sqrt(eps)), "rstd=1/sqrt(eps)")
     assert torch.equal(y.cpu(), beta.expand(3, 4096)), "constant row -> y = beta"
     z = torch.zeros(2, 1024, dtype=bf)
     y, rstd = hip_oracles.rmsnorm(z.to(rocm_device), gamma[:1024].contiguous().to(rocm_device), eps)
@@ -444,7 +554,7 @@ def test_row_layouts_multiwave(rocm_device):
         x = torch.randn(b, q, k, generator=g).to(bf)
         mask = torch.triu(torch.full((q, k), float("-inf")), 1).to(bf)
         got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), mask.to(rocm_device), 0.125)
-        assert_close(got, ref.scaled_masked_softmax(x, mask, 0.125), BF16_TOL, f"softmax {b}x{q}x{k}")
+        assert_close(got, ref.scaled_masked_softmax(x, mask, 0.125), PROB_TOL, f"softmax {b}x{q}x{k}")
     for rows, cols in [(3, 4), (9, 132), (5, 1028), (4, 4100), (2, 32772), (2, 100000), (17, 4096)]:
         print(f"[multiwave] row_mean {rows}x{cols}", flush=True)
         g = torch.Generator().manual_seed(rows * 7 + cols)
@@ -519,18 +629,18 @@ def test_scaled_bias_softmax_heads_and_strides(rocm_device):
         x = torch.randn(b, q, k, generator=g).to(bf)
         bias = torch.randn(b // heads, q, k, generator=g).to(bf)
         got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), scale, heads)
-        assert_close(got, ref(x, bias, scale, heads), BF16_TOL, what)
+        assert_close(got, ref(x, bias, scale, heads), PROB_TOL, what)
         # the same bias as a padded view (row stride > K) and as a broadcast
         # over Q (row stride 0, materialised by the wrapper)
         padded = torch.randn(b // heads, q, k + 8, generator=g).to(bf)
         view = padded.to(rocm_device)[:, :, :k]
         got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), view, scale, heads)
-        assert_close(got, ref(x, padded[:, :, :k], scale, heads), BF16_TOL, what + " padded")
+        assert_close(got, ref(x, padded[:, :, :k], scale, heads), PROB_TOL, what + " padded")
         row = torch.randn(b // heads, 1, k, generator=g).to(bf)
         got = hip_oracles.scaled_bias_softmax(x.to(rocm_device),
                                               row.to(rocm_device).expand(b // heads, q, k),
                                               scale, heads)
-        assert_close(got, ref(x, row.expand(b // heads, q, k), scale, heads), BF16_TOL,
+        assert_close(got, ref(x, row.expand(b // heads, q, k), scale, heads), PROB_TOL,
                      what + " broadcast over q")
     # closed form: a bias of -inf except one column gives a one-hot row
     x = torch.randn(4, 3, 64).to(bf)
@@ -551,7 +661,7 @@ def test_masked_softmax_broadcast_mask_rows(rocm_device):
     row = torch.randn(1, 264).to(bf)
     got = hip_oracles.scaled_masked_softmax(x.to(rocm_device), row.to(rocm_device).expand(6, 264), 0.125)
     assert_close(got, ref.scaled_masked_softmax(x, row.expand(6, 264).contiguous(), 0.125),
-                 BF16_TOL, "broadcast mask")
+                 PROB_TOL, "broadcast mask")
 
 
 def test_spatial_mean_layouts(rocm_device):
@@ -652,7 +762,7 @@ def test_batchnorm_nchw_act_mean(n, c, h, w, act, rocm_device):
         d[0], d[1], d[2], d[3], d[4], momentum=0.1, eps=1e-5, var_scale=1.5, act=act)
     wm, wr, wy, wrm, wrv = _bn_bf16_ref(x, gm, bt, rm, rv, 1e-5, 0.1, 1.5, act)
     assert_close(mean, wm, F32_TOL, "save_mean")
-    assert_close(rstd, wr, F32_TOL * max(1.0, float(wr.abs().max())), "save_rstd")
+    assert_close(rstd, wr, (1e-5, 1e-5 * max(1.0, float(wr.abs().max()))), "save_rstd")
     assert_close(d[3], wrm, F32_TOL, "running_mean")
     assert_close(d[4], wrv, F32_TOL, "running_var")
     assert out.shape == (n, c) and out.dtype == torch.bfloat16
@@ -682,7 +792,7 @@ def test_batchnorm_bf16_closed_forms(rocm_device):
             y = out.cpu().view(4, c, 1, 1)
             eps = 1e-5
         assert torch.equal(mean.cpu().flatten(), torch.full((c,), 1.5)), layout
-        assert_close(rstd, torch.full((1, c, 1, 1), 1 / math.sqrt(eps)), F32_TOL / math.sqrt(eps), layout)
+        assert_close(rstd, torch.full((1, c, 1, 1), 1 / math.sqrt(eps)), (1e-5, 1e-5 / math.sqrt(eps)), layout)
         want = torch.relu(beta.to(bf)).view(1, c, 1, 1).expand_as(y)
         assert torch.equal(y, want), layout
         assert_close(d[2], torch.full((c,), 0.15), F32_TOL, layout + " running_mean")
@@ -780,6 +890,102 @@ def test_batchnorm_workspace_contract(rocm_device):
         assert torch.equal(u, v)
     assert int(ws[8:12].view(torch.int32).item()) == 0
     assert int(ws[4:8].view(torch.int32).item()) == 3, "one epoch per launch"
+
+
+def test_batchnorm_workspace_growth_keeps_captured_graph_valid(rocm_device):
+    """A graph captured on the shared workspace stays valid after a larger
+    shape grows it: the old workspace is retired, not freed, so replays keep
+    using live memory and their own epoch state."""
+    import hip_oracles
+    dev = rocm_device
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(4, 8, 8, 8, generator=g) * 2 + 0.5).to(dev)
+    gamma, beta = (1 + 0.1 * torch.randn(8, generator=g)).to(dev), torch.zeros(8, device=dev)
+    rm0, rv0 = torch.zeros(8, device=dev), torch.ones(8, device=dev)
+    rm, rv = rm0.clone(), rv0.clone()
+    hip_oracles.batchnorm_train(x, gamma, beta, rm, rv, momentum=0.1, eps=1e-5)  # warm
+    own = torch.zeros(hip_oracles.batchnorm_workspace_bytes(4, 8, 64), dtype=torch.uint8,
+                      device=dev)
+    want_rm, want_rv = rm0.clone(), rv0.clone()
+    want = hip_oracles.batchnorm_train(x, gamma, beta, want_rm, want_rv, momentum=0.1,
+                                       eps=1e-5, workspace=own)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = hip_oracles.batchnorm_train(x, gamma, beta, rm, rv, momentum=0.1, eps=1e-5)
+    old = hip_oracles._bn_workspaces[dev.index]
+    # grow the shared workspace past its current size
+    c = 4096
+    while hip_oracles.batchnorm_workspace_bytes(2, c, 16) <= old.numel():
+        c *= 2
+    xb = torch.randn(2, c, 4, 4, device=dev)
+    ones, zeros = torch.ones(c, device=dev), torch.zeros(c, device=dev)
+    hip_oracles.batchnorm_train(xb, ones, zeros, zeros.clone(), ones.clone(), momentum=0.1,
+                                eps=1e-5)
+    assert hip_oracles._bn_workspaces[dev.index] is not old, "the workspace did not grow"
+    assert any(w is old for w in hip_oracles._bn_retired[dev.index])
+    del xb
+    torch.cuda.empty_cache()
+    _ = torch.randn(1 << 20, device=dev).sum().item()  # reuse freed memory in between
+    for rep in range(3):
+        rm.copy_(rm0)
+        rv.copy_(rv0)
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, w in zip(("y", "mean", "invstd", "rm", "rv"), (*captured, rm, rv),
+                              (*want, want_rm, want_rv)):
+            assert torch.equal(a, w), f"replay {rep} {name} differs after the workspace grew"
+    assert hip_oracles.device_faults(dev) == []
+
+
+def test_batchnorm_forced_timeout_is_reported(rocm_device, monkeypatch):
+    """Failure injection from the host (HIPO_TEST_FORCE_BN_TIMEOUT: every
+    exchange wait looks for a tag no workgroup publishes, a few polls, then
+    the timeout path; the kernel exits normally): the outputs and the
+    running statistics are NaN, device_faults / raise_on_device_faults
+    report it once, the harness's check fails the point, and the next call
+    without injection is correct again."""
+    import hip_oracles
+    import oracle as ref
+    import oracle_harness
+    from repro_harness import make_inputs_from_config
+    dev = rocm_device
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(8, 16, 8, 8, generator=g) * 2 + 0.5
+    gamma, beta = 1 + 0.1 * torch.randn(16, generator=g), 0.1 * torch.randn(16, generator=g)
+    rm, rv = torch.zeros(16), torch.ones(16)
+    hip_oracles.device_faults()  # start clean
+    monkeypatch.setenv("HIPO_TEST_FORCE_BN_TIMEOUT", "1")
+    rm_d, rv_d = rm.to(dev), rv.to(dev)
+    y, sm, si = hip_oracles.batchnorm_train(x.to(dev), gamma.to(dev), beta.to(dev), rm_d, rv_d,
+                                            momentum=0.1, eps=1e-5)
+    torch.cuda.synchronize()
+    for name, t in (("y", y), ("save_mean", sm), ("save_invstd", si), ("running_mean", rm_d),
+                    ("running_var", rv_d)):
+        assert torch.isnan(t).all(), f"{name} not poisoned after a timed-out exchange"
+    faults = hip_oracles.device_faults()
+    assert len(faults) == 1 and "timed out" in faults[0], faults
+    assert hip_oracles.device_faults() == [], "the error word was not cleared"
+    # the harness turns the fault into a failed point
+    fn, inst = _load("var_mean_batchnorm_train_relu")
+    label, cfg = list(_points("var_mean_batchnorm_train_relu").items())[1]
+    torch.manual_seed(1)
+    inputs = make_inputs_from_config(cfg, device=dev)
+    assert oracle_harness.check_oracle(fn, inst, inputs) is False
+    r = oracle_harness.bench_oracle(fn, inst, inputs, "forced_timeout", warmup=1, rep=3,
+                                    rounds=1, compare_compile=False, disable_gpu_lock=True)
+    assert r["status"] == "ORACLE_DEVICE_FAULT" and r["status"] in oracle_harness._INVALID_STATUSES
+    with pytest.raises(hip_oracles.HipOraclesDeviceFault):
+        hip_oracles.batchnorm_train(x.to(dev), gamma.to(dev), beta.to(dev), rm.to(dev),
+                                    rv.to(dev), momentum=0.1, eps=1e-5)
+        hip_oracles.raise_on_device_faults()
+    monkeypatch.delenv("HIPO_TEST_FORCE_BN_TIMEOUT")
+    rm_d, rv_d = rm.to(dev), rv.to(dev)
+    got = hip_oracles.batchnorm_train(x.to(dev), gamma.to(dev), beta.to(dev), rm_d, rv_d,
+                                      momentum=0.1, eps=1e-5)
+    want = ref.batchnorm_train(x, gamma, beta, rm, rv, momentum=0.1, eps=1e-5, relu=True)
+    for name, a, w in zip(("y", "mean", "invstd", "rm", "rv"), (*got, rm_d, rv_d), want):
+        assert_close(a, w, F32_TOL, f"after the injected timeout: {name}")
+    assert hip_oracles.device_faults() == []
 
 
 def test_graph_capture_replays_match_eager(rocm_device):

@@ -76,8 +76,10 @@ def test_gate_detects_exp2_substitution():
 
 
 def test_invalid_statuses():
+    # the reference's four, plus a kernel-recorded device fault (NaN outputs)
     assert _INVALID_STATUSES == {"UNVERIFIED_NUMERICS", "INVALID_CUDAGRAPH_WARNING",
-                                 "NUMERICS_WORSE_THAN_COMPILED", "NO_ORACLE_FOR_SHAPE"}
+                                 "NUMERICS_WORSE_THAN_COMPILED", "NO_ORACLE_FOR_SHAPE",
+                                 "ORACLE_DEVICE_FAULT"}
     assert "ORACLE_ONLY" not in _INVALID_STATUSES
     assert "NUMERICS_OPTOUT_ACCEPTED" not in _INVALID_STATUSES
 
