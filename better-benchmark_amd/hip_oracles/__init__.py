@@ -68,6 +68,9 @@ _SIGNATURES = {
         [_c_ptr] * 8 + [_c_i64, _c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int,
                         _c_ptr, ctypes.c_size_t, _c_ptr]),
     "hipo_flat_copy": (ctypes.c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
+    "hipo_batchnorm_train_fwd_f32_noalloc": (
+        ctypes.c_int,
+        [_c_ptr] * 8 + [_c_i64, _c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int, _c_ptr]),
 }
 
 _lib = None

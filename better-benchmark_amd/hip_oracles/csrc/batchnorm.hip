@@ -21,6 +21,8 @@
 //      (0, c) also writes save_mean / save_invstd and updates the running
 //      statistics (unbiased variance, count / (count - 1)).
 // This path reads x twice (once per launch).
+#include <mutex>
+
 #include "welford.h"
 
 namespace hipo {
@@ -284,4 +286,89 @@ extern "C" int hipo_batchnorm_train_fwd_f32(
         ws, n, c, hw, S, momentum, eps, relu);
   }
   return check_launch("batchnorm_train_fwd_f32 (normalize)");
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the workspace is a file-scope device array.
+//
+// Each device the library runs on holds its own copy of `scratch`, for the
+// life of the process.  On the host the array's name is only a stand-in for
+// that memory: its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and only that address is
+// passed to kernels.  The first call on a device also clears the array with
+// a fill kernel on the caller's stream, ordered before the call's own
+// kernels: the single-pass kernel's control words (completion count, epoch)
+// must start at zero and its exchange slots must carry no tag of a future
+// epoch.  After that, the epoch protocol keeps the array consistent from one
+// call to the next, for any shape that fits; calls that overlap on one
+// device (two streams) race on it.
+// ---------------------------------------------------------------------------
+namespace hipo {
+namespace {
+
+constexpr size_t kBnScratchBytes = size_t{4} << 20;  // 4 MiB per device
+static __device__ __align__(256) unsigned char scratch[kBnScratchBytes];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+
+__global__ __launch_bounds__(256) void bn_scratch_clear(u32x4_t* __restrict__ p,
+                                                       uint32_t n16) {
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n16; i += gridDim.x * 256u)
+    p[i] = u32x4_t{0u, 0u, 0u, 0u};
+}
+
+// The device address of this device's scratch array, set up (and cleared on
+// `stream`) by the first call on the device; nullptr after an error.
+void* scratch_for_current_device(hipStream_t stream) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    set_error("batchnorm (no-alloc): no current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] != nullptr) return g_scratch_ptr[dev];
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    set_error("batchnorm (no-alloc): the first call on a device sets up its scratch "
+              "array and must not be captured; call once outside capture first");
+    return nullptr;
+  }
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || ptr == nullptr) {
+    (void)hipGetLastError();
+    set_error("batchnorm (no-alloc): hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  const uint32_t n16 = static_cast<uint32_t>(kBnScratchBytes / 16);
+  bn_scratch_clear<<<dim3(256), dim3(256), 0, stream>>>(static_cast<u32x4_t*>(ptr), n16);
+  if (check_launch("batchnorm (no-alloc) scratch clear") != 0) return nullptr;
+  g_scratch_ptr[dev] = ptr;
+  return ptr;
+}
+
+}  // namespace
+}  // namespace hipo
+
+extern "C" int hipo_batchnorm_train_fwd_f32_noalloc(
+    const float* x, const float* gamma, const float* beta, float* running_mean,
+    float* running_var, float* y, float* save_mean, float* save_invstd,
+    int64_t n, int64_t c, int64_t hw, float momentum, float eps, int relu,
+    hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  HIPO_REQUIRE(n > 0 && c > 0 && hw > 0, "batchnorm: sizes must be positive");
+  const size_t need = hipo_batchnorm_workspace_bytes(n, c, hw);
+  HIPO_REQUIRE(need <= kBnScratchBytes,
+               "batchnorm (no-alloc): this shape needs %zu bytes of workspace, more "
+               "than the %zu-byte scratch array; use hipo_batchnorm_train_fwd_f32",
+               need, kBnScratchBytes);
+  void* ws = scratch_for_current_device(stream);
+  if (ws == nullptr) return HIPO_EINVAL;
+  return hipo_batchnorm_train_fwd_f32(x, gamma, beta, running_mean, running_var, y,
+                                      save_mean, save_invstd, n, c, hw, momentum, eps,
+                                      relu, ws, kBnScratchBytes, stream);
 }

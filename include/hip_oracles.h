@@ -272,6 +272,30 @@ int hipo_batchnorm_train_fwd_f32(const float* x, const float* gamma,
                                  hipStream_t stream);
 
 /*
+ * hipo_batchnorm_train_fwd_f32 without a caller workspace and without any
+ * allocation: no counterpart in the reference.  For callers that cannot
+ * allocate device memory or pass a workspace (code under hipGraph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * semantics, kernels and results as hipo_batchnorm_train_fwd_f32, minus the
+ * workspace: it uses a 4 MiB file-scope device array per device instead,
+ * held until the process ends.  Shapes whose
+ * hipo_batchnorm_workspace_bytes(n, c, hw) exceeds 4 MiB are rejected with
+ * HIPO_EINVAL (config [128, 256, 56, 56] needs about 96 KiB).  The first
+ * call on a device looks up the array's address and clears it with a fill
+ * kernel on `stream`; that first call must not be under stream capture
+ * (HIPO_EINVAL), later ones may be.  Every call on a device shares that
+ * device's array: calls that overlap on one device (several streams) race
+ * and must not be issued.
+ */
+int hipo_batchnorm_train_fwd_f32_noalloc(const float* x, const float* gamma,
+                                         const float* beta, float* running_mean,
+                                         float* running_var, float* y,
+                                         float* save_mean, float* save_invstd,
+                                         int64_t n, int64_t c, int64_t hw,
+                                         float momentum, float eps, int relu,
+                                         hipStream_t stream);
+
+/*
  * Flat stream copy (a measurement yardstick, not an oracle): reads
  * read_bytes from src and writes write_bytes to dst in one launch with the
  * oracle kernels' access style (16-byte non-temporal accesses, 1 KiB per
