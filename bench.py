@@ -368,7 +368,8 @@ def per_config(want_cpu, steady_steps=64, compare_compile=True, coordinate_desce
             f"{elapsed:.0f} s elapsed)")
         r = oh.bench_oracle(fn, oh.get_repro_instance(d), inputs, f"{rid}_{label}",
                             warmup=10, rep=100, rounds=5, compare_compile=use_compile,
-                            coordinate_descent=coordinate_descent, cpu_eager=want_cpu)
+                            coordinate_descent=coordinate_descent, cpu_eager=want_cpu,
+                            numerics_optout=oh.load_numerics_optout(d))
         entry = {"config": tag, "repro": rid, "status": r.get("status"),
                  "bytes": r.get("bytes"), "read_bytes": rd, "write_bytes": wr,
                  "steady_us": ss["device_us_per_step"], "steady_gbps": ss["achieved"],
@@ -388,6 +389,9 @@ def per_config(want_cpu, steady_steps=64, compare_compile=True, coordinate_desce
         for k in ("compile", "compile_error"):
             if k in r:
                 entry[k] = r[k]
+        if "numerics_optout" in r:
+            entry["numerics_optout"] = {"accepted": True,
+                                        "reason": r["numerics_optout"]["annotation"]["reason"]}
         gate = r.get("numerics_gate")
         if gate is not None:
             entry["numerics_gate_pass"] = gate.get("pass")
@@ -406,15 +410,21 @@ def per_config(want_cpu, steady_steps=64, compare_compile=True, coordinate_desce
 
 
 def copy_calibration(mib: int, reps: int = 20) -> None:
-    """A plain device copy of known size, for scaling rocprof byte counters."""
+    """Copies of known size, for reading rocprof byte counters: the runtime's
+    device copy (dst.copy_(src)) and hipo_flat_copy (16-byte non-temporal
+    accesses, the oracle kernels' style), `reps` each over the same buffers."""
     import torch
+    import hip_oracles
     n = mib * (1 << 20) // 4
     src = torch.ones(n, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(reps):
         dst.copy_(src)
+    for _ in range(reps):
+        hip_oracles.flat_copy(src, dst)
     torch.cuda.synchronize()
-    print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4, "reps": reps}))
+    print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4,
+                      "reps": reps, "kernels": ["runtime copy", "flat_copy_chunks"]}))
 
 
 def main(argv=None) -> int:

@@ -28,8 +28,9 @@ ROCm specifics: GPU discovery and the pinning variable come from gpu_lock
 `rocm-smi --setperfdeterminism <MHz>` / `--resetperfdeterminism` (the
 counterpart of `nvidia-smi -lgc` / `-rgc`), best effort and never fatal, off
 by default (it needs root); device errors are recognised by HIP's messages.
-The torch.compile comparator is optional (`--no-compile` gives the
-ORACLE_ONLY status, still a valid floor).
+The torch.compile (Inductor) comparator runs by default, as in the
+reference's bench_oracle; `--no-compile` skips it (ORACLE_ONLY status, still
+a valid floor).
 
 Only the oracle path is provided: the reference's compile-path sweep,
 full-graph mode, perf.json updates and merges are outside this backend.
@@ -376,14 +377,17 @@ def _is_device_error(message: str) -> bool:
 def _bench_oracle_point(canonical_dir: str, shape_label: str, cfg: dict) -> dict:
     """Numerics check of one point, then bench_oracle (or an invalid status)."""
     from oracle_harness import (_load_oracle_module, bench_oracle, check_oracle_all_shapes,
-                                get_inputs, get_repro_instance)
+                                get_inputs, get_repro_instance, load_numerics_optout)
     from repro_harness import load_shape_configs, make_inputs_from_config
 
     _, fn, d = _load_oracle_module(canonical_dir)
     repro_id = d.name
     configs = load_shape_configs(str(d / "repro.py"))
+    # The repro's reviewed numerics opt-out applies here as in the runner and
+    # bench_oracle_all_shapes (oracle_harness.py:1405-1406, 1848-1888).
     bench_kw = dict(warmup=cfg["n_warmup"], rep=cfg["n_rep"],
-                    compare_compile=cfg["compile"])
+                    compare_compile=cfg["compile"],
+                    numerics_optout=load_numerics_optout(d))
     if shape_label == _DEFAULT_SHAPE_TOKEN or not configs:
         passed = True
         if not cfg["skip_check"]:
@@ -652,7 +656,8 @@ def main(argv=None) -> int:
     ap.add_argument("--n-warmup", type=int, default=25)
     ap.add_argument("--n-rep", type=int, default=100)
     ap.add_argument("--compile", dest="compile", action=argparse.BooleanOptionalAction,
-                    default=False, help="also time the torch.compile comparator")
+                    default=True, help="time the torch.compile (Inductor) comparator "
+                                       "(--no-compile: ORACLE_ONLY)")
     ap.add_argument("--oracle-skip-check", action="store_true")
     ap.add_argument("--output", type=Path, default=None,
                     help="timings file for model_graph_accounting --timings")

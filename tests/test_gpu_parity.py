@@ -1110,8 +1110,10 @@ def test_wrappers_reject_bad_operands(rocm_device):
 
 def test_bench_parallel_oracles_end_to_end(rocm_device, tmp_path):
     """The parallel runner on the GPU: two canonical dirs, every shapes.json
-    point, one worker pinned with HIP_VISIBLE_DEVICES; the timings file has
-    one priced entry per dir with points_by_shape keyed by shape hash."""
+    point, one worker pinned with HIP_VISIBLE_DEVICES, the torch.compile
+    (Inductor) comparator on (the default); the timings file has one priced
+    entry per dir with points_by_shape keyed by shape hash, each with a
+    compile_us and a reference status."""
     import json
     import subprocess
     import sys
@@ -1121,8 +1123,8 @@ def test_bench_parallel_oracles_end_to_end(rocm_device, tmp_path):
     print("[bench_parallel] running 6 points", flush=True)
     proc = subprocess.run([sys.executable, "-u", "-m", "bench_parallel", *dirs, "--oracles",
                            "--output", str(out), "--n-warmup", "2", "--n-rep", "5",
-                           "--task-timeout", "90"],
-                          cwd=str(PKG), capture_output=True, text=True, timeout=110)
+                           "--task-timeout", "150"],
+                          cwd=str(PKG), capture_output=True, text=True, timeout=260)
     print(proc.stdout[-3000:], proc.stderr[-2000:], flush=True)
     assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-2000:]
     timed = json.loads(out.read_text())
@@ -1133,7 +1135,8 @@ def test_bench_parallel_oracles_end_to_end(rocm_device, tmp_path):
         assert set(entry["points_by_shape"]) == {baseline} | ragged
         assert entry["n_points"] == 3
         for shape_hash, point in entry["points_by_shape"].items():
-            assert point["status"] == "ORACLE_ONLY" and point["oracle_us"] > 0
+            assert point["status"] in ("GOOD", "AT_FLOOR", "BAD_ORACLE"), point
+            assert point["oracle_us"] > 0 and point["compile_us"] > 0
             # the BASELINE point has a shape-specific MI355X registration; the
             # ragged ones dispatch to the shape-general one
             assert point["fallback"] is (shape_hash != baseline)
