@@ -16,8 +16,9 @@
 // kernels by row length:
 //   K <= 512: L lanes per row, 64 / L rows per access instruction, 2 KiB of
 //     x per wave, reductions within lane segments, no LDS;
-//   K = 1024 or 2048 (config [384, 1024, 1024]): 1 KiB of x per wave, the
-//     rows of one q for 4 / W consecutive batch entries in a 256-thread
+//   K = 1024 or 2048 (config [384, 1024, 1024]): 1 KiB of x per wave and
+//     row, each wave taking RPW = 4 rows with their loads issued together,
+//     the rows of one q for 4 RPW / W batch entries in a 256-thread
 //     workgroup, their shared mask row loaded once and staged through LDS;
 //   otherwise (or a per-batch mask the grouping cannot share): the
 //     row_layout.h plan, W waves per row, 2 KiB per wave.
@@ -33,7 +34,9 @@ namespace {
 constexpr uint32_t kNegInfPair = 0xFF80FF80u;  // two bf16 -inf
 
 __device__ __forceinline__ float exp_shifted(float s, float m) {
-  return exp_f32(exp_domain(s - m));
+  // s - m <= 0 (m is the row max) or NaN, so only exp_f32's lower bound
+  // needs the clamp (IEEE maximum: NaN stays NaN).
+  return exp_f32(__builtin_elementwise_maximum(s - m, -104.0f));
 }
 
 template <int U, int WT, bool ROUND_SCALE>
@@ -222,18 +225,25 @@ void launch_short(bool round_scale, dim3 grid, hipStream_t stream, const uint16_
 
 // Rows of exactly K = 1024 or 2048 (KC, a compile-time constant):
 // 256-thread workgroups, W = KC / 512 waves per row (one 16-byte group per
-// lane: 1 KiB of x per wave, no idle lanes), NR = 4 / W rows per workgroup.
-// Workgroup (q, y, z) of the 3-D grid takes the rows (b0 + i) * Q + q,
-// i < NR, b0 = (z * gy + y) * NR: the same q of NR consecutive batch
-// entries, which share one mask row.  z is the mask's batch group (offset
-// z * mask_batch_stride; a single z when the mask is broadcast over batch)
-// and gy its workgroups along y, so the kernel does no integer division; x
-// is fastest, so dispatch order walks q in memory order.  The mask row
-// (2 KC bytes, 2 KC / 256 per thread) is loaded once per workgroup, issued
-// before the x load, and staged through LDS; row max and sum combine the W
-// wave results through LDS in a fixed order.  Rows past the batch end (NR
-// not dividing a broadcast batch) re-read the last batch entry and store
-// nothing.
+// lane: 1 KiB of x per wave and row, no idle lanes), NR = 4 / W row slots
+// per workgroup, RPW rows per slot.  Workgroup (q, y, z) of the 3-D grid
+// takes the rows (b0 + i) * Q + q, i < NR * RPW, b0 = (z * gy + y) * NR *
+// RPW: the same q of NR * RPW consecutive batch entries, which share one
+// mask row; slot rr holds entries b0 + rr + NR * j, j < RPW, whose loads a
+// wave issues together before working through them.  z is the mask's batch
+// group (offset z * mask_batch_stride; a single z when the mask is
+// broadcast over batch) and gy its workgroups along y, so the kernel does
+// no integer division; x is fastest, so dispatch order walks q in memory
+// order.  The mask row (2 KC bytes, 2 KC / 256 per thread) is loaded once
+// per workgroup, issued before the x loads, and staged through LDS; row max
+// and sum combine the W wave results through LDS in a fixed order.  Rows
+// past the batch end (NR * RPW not dividing a broadcast batch) re-read the
+// last batch entry and store nothing.
+// With the accurate exp (exp_f32: about 9 issue slots per element against
+// 5 for a bare exp2) one row per wave ran at 288-291 us at [384, 1024,
+// 1024]; issuing 2 / 4 / 8 / 16 rows' loads per wave 280 / 271-276 /
+// 275-280 / 303-306 us (the bare exp2 form, one row per wave, 269-273 us on
+// the same boxes).
 // Measured on MI355X (graph loop, rotating buffers, 2 B read + 2 B written
 // per element, % of 8 TB/s), [384, 1024, 1024]: one wave per row with every
 // wave reading its own mask row (the row-plan kernel) 261.6-263.5 us
@@ -243,7 +253,7 @@ void launch_short(bool round_scale, dim3 grid, hipStream_t stream, const uint16_
 // 260-267 us.  [192, 1024, 2048]: 258.7-260.1 us against 253.3 us.  With a
 // runtime K and idle lanes (K = 776, 1032) the layout lost 8-15 % to the
 // row-plan kernel, so other row lengths stay there.
-template <int KC, bool ROUND_SCALE>
+template <int KC, bool ROUND_SCALE, int RPW>
 __global__ __launch_bounds__(256) void masked_softmax_shared_mask(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
     uint16_t* __restrict__ out, uint32_t batch, uint32_t Q, uint32_t gy,
@@ -253,15 +263,15 @@ __global__ __launch_bounds__(256) void masked_softmax_shared_mask(
   static_assert(W * NR * kWave == 256 && W * kWave * kRowGroup == KC, "full rows");
   constexpr int kStageWords = KC / 512;  // 32-bit words of the mask row per thread
   __shared__ __align__(16) uint32_t mrow[KC / 2];  // read back as 16-byte groups
-  __shared__ float pmax[W * NR], psum[W * NR];
+  __shared__ float pmax[RPW][W * NR], psum[RPW][W * NR];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int w = wave % W;
   const int rr = wave / W;
   const uint32_t q = blockIdx.x;
-  const uint32_t b = (blockIdx.z * gy + blockIdx.y) * NR + rr;
-  const bool row_ok = b < batch;
-  const int64_t row = static_cast<int64_t>(row_ok ? b : batch - 1) * Q + q;
+  // The workgroup's NR * RPW rows: batch entries b0 + rr + NR * i of query q;
+  // wave (rr, w) takes the RPW rows of slot rr, all loads issued up front.
+  const uint32_t b0 = (blockIdx.z * gy + blockIdx.y) * (NR * RPW) + rr;
 
   const uint16_t* mr = mask + blockIdx.z * mask_batch_stride +
                        static_cast<int64_t>(q) * mask_stride;
@@ -277,71 +287,89 @@ __global__ __launch_bounds__(256) void masked_softmax_shared_mask(
     for (int i = 0; i < 4; ++i) mval[i] = v[i];
   }
   const int col = (w * kWave + lane) * kRowGroup;
-  const u32x4_t xv =
-      __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + row * KC + col));
+  u32x4_t xv[RPW];
+  int64_t row[RPW];
+  bool row_ok[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const uint32_t b = b0 + NR * i;
+    row_ok[i] = b < batch;
+    // Rows past the batch end re-read the last batch entry and store nothing.
+    row[i] = static_cast<int64_t>(row_ok[i] ? b : batch - 1) * Q + q;
+    xv[i] = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t*>(x + row[i] * KC + col));
+  }
 #pragma unroll
   for (int i = 0; i < kStageWords; ++i) mrow[st + i] = mval[i];
   __syncthreads();
   const u32x4_t mv = *reinterpret_cast<const u32x4_t*>(&mrow[col / 2]);
 
-  float s[8];
-  uint32_t tw[4];  // the rounded scores as bf16 pairs
-  float m = -__builtin_inff();
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    float a0 = bf16lo(xv[d]) * scale;
-    float a1 = bf16hi(xv[d]) * scale;
-    if (ROUND_SCALE) {
-      const uint32_t r = pack_bf16x2(a0, a1);
-      a0 = bf16lo(r);
-      a1 = bf16hi(r);
+  for (int i = 0; i < RPW; ++i) {
+    float s[8];
+    uint32_t tw[4];  // the rounded scores as bf16 pairs
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      float a0 = bf16lo(xv[i][d]) * scale;
+      float a1 = bf16hi(xv[i][d]) * scale;
+      if (ROUND_SCALE) {
+        const uint32_t r = pack_bf16x2(a0, a1);
+        a0 = bf16lo(r);
+        a1 = bf16hi(r);
+      }
+      const uint32_t t = pack_bf16x2(a0 + bf16lo(mv[d]), a1 + bf16hi(mv[d]));
+      tw[d] = t;
+      s[2 * d] = bf16lo(t);
+      s[2 * d + 1] = bf16hi(t);
+      m = fmaxf(m, fmaxf(s[2 * d], s[2 * d + 1]));
     }
-    const uint32_t t = pack_bf16x2(a0 + bf16lo(mv[d]), a1 + bf16hi(mv[d]));
-    tw[d] = t;
-    s[2 * d] = bf16lo(t);
-    s[2 * d + 1] = bf16hi(t);
-    m = fmaxf(m, fmaxf(s[2 * d], s[2 * d + 1]));
-  }
-  m = wave_max(m);
-  if (lane == 0) pmax[wave] = m;
-  __syncthreads();
-  m = pmax[rr * W];
+    m = wave_max(m);
+    if (lane == 0) pmax[i][wave] = m;
+    __syncthreads();
+    m = pmax[i][rr * W];
 #pragma unroll
-  for (int k = 1; k < W; ++k) m = fmaxf(m, pmax[rr * W + k]);
+    for (int k = 1; k < W; ++k) m = fmaxf(m, pmax[i][rr * W + k]);
 
-  // A lane whose 8 scores are all -inf (a fully masked group: the causal
-  // mask's upper triangle makes whole waves of them) has exp = 0 for each;
-  // the test is on the rounded score words, so a NaN score still goes
-  // through exp and poisons the row as in eager.
-  float sum = 0.f;
-  if ((tw[0] & tw[1] & tw[2] & tw[3]) == kNegInfPair &&
-      (tw[0] | tw[1] | tw[2] | tw[3]) == kNegInfPair) {
+    // A lane whose 8 scores are all -inf (a fully masked group: the causal
+    // mask's upper triangle makes whole waves of them) has exp = 0 for each;
+    // the test is on the rounded score words, so a NaN score still goes
+    // through exp and poisons the row as in eager.
+    float sum = 0.f;
+    if ((tw[0] & tw[1] & tw[2] & tw[3]) == kNegInfPair &&
+        (tw[0] | tw[1] | tw[2] | tw[3]) == kNegInfPair) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s[e] = 0.f;
-  } else {
+      for (int e = 0; e < 8; ++e) s[e] = 0.f;
+    } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      s[e] = exp_shifted(s[e], m);
-      sum += s[e];
+      for (int e = 0; e < 8; ++e) {
+        s[e] = exp_shifted(s[e], m);
+        sum += s[e];
+      }
     }
-  }
-  sum = wave_sum(sum);
-  if (lane == 0) psum[wave] = sum;
-  __syncthreads();
-  sum = psum[rr * W];
+    sum = wave_sum(sum);
+    if (lane == 0) psum[i][wave] = sum;
+    __syncthreads();
+    sum = psum[i][rr * W];
 #pragma unroll
-  for (int k = 1; k < W; ++k) sum += psum[rr * W + k];
-  const float inv = 1.0f / sum;
+    for (int k = 1; k < W; ++k) sum += psum[i][rr * W + k];
+    const float inv = 1.0f / sum;
 
-  u32x4_t o;
+    u32x4_t o;
 #pragma unroll
-  for (int d = 0; d < 4; ++d) o[d] = pack_bf16x2(s[2 * d] * inv, s[2 * d + 1] * inv);
-  if (row_ok) __builtin_nontemporal_store(o, reinterpret_cast<u32x4_t*>(out + row * KC + col));
+    for (int d = 0; d < 4; ++d) o[d] = pack_bf16x2(s[2 * d] * inv, s[2 * d + 1] * inv);
+    if (row_ok[i])
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x4_t*>(out + row[i] * KC + col));
+  }
 }
+
+// Rows per wave of the shared-mask kernel (consecutive rows of one query in
+// steps of NR batch entries; their loads are issued together).
+constexpr int kSharedMaskRowsPerWave = 4;
 
 // Launch shape of the shared-mask kernel: its row length (1024 or 2048; 0
 // when the kernel does not apply) and the 3-D grid.  It does not apply to
-// other K, to a per-batch mask whose heads groups NR = 4 / W does not
+// other K, to a per-batch mask whose heads groups the NR * RPW rows of a workgroup do not
 // divide, or to grids beyond the y / z limits.
 struct SharedMaskPlan {
   int k = 0;
@@ -353,7 +381,7 @@ SharedMaskPlan shared_mask_plan(int64_t batch, int64_t Q, int64_t K, int64_t mbs
                                 int64_t heads) {
   SharedMaskPlan plan;
   if ((K != 1024 && K != 2048) || Q > 0x7fffffff) return plan;
-  const int nr = K == 1024 ? 2 : 1;
+  const int nr = (K == 1024 ? 2 : 1) * kSharedMaskRowsPerWave;  // rows per workgroup
   int64_t gy, gz;
   if (mbs == 0) {
     gy = (batch + nr - 1) / nr;
@@ -378,11 +406,11 @@ void launch_shared_mask(bool round_scale, const SharedMaskPlan& plan, hipStream_
   const auto bt = static_cast<uint32_t>(batch);
   const auto q = static_cast<uint32_t>(Q);
   if (round_scale) {
-    masked_softmax_shared_mask<KC, true><<<plan.grid, dim3(256), 0, stream>>>(
-        x, mask, out, bt, q, plan.gy, ms, mbs, scale);
+    masked_softmax_shared_mask<KC, true, kSharedMaskRowsPerWave>
+        <<<plan.grid, dim3(256), 0, stream>>>(x, mask, out, bt, q, plan.gy, ms, mbs, scale);
   } else {
-    masked_softmax_shared_mask<KC, false><<<plan.grid, dim3(256), 0, stream>>>(
-        x, mask, out, bt, q, plan.gy, ms, mbs, scale);
+    masked_softmax_shared_mask<KC, false, kSharedMaskRowsPerWave>
+        <<<plan.grid, dim3(256), 0, stream>>>(x, mask, out, bt, q, plan.gy, ms, mbs, scale);
   }
 }
 

@@ -285,12 +285,13 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_scalar(
 }
 
 // Rows of exactly KC columns (4096, the config): 256-thread workgroups of
-// NR = 2 rows, W = 2 waves per row (4 groups of 16 bytes per lane and
-// stream), gamma and beta staged once per workgroup in LDS, row index from
-// the block index without division.  Same arithmetic as
+// NR = 2 row slots, W = 2 waves per row (4 groups of 16 bytes per lane and
+// stream), RPW rows per slot (rows b * NR * RPW + rr + NR * j, j < RPW),
+// their loads issued together; gamma and beta staged once per workgroup in
+// LDS, row index from the block index without division.  Same arithmetic as
 // residual_layernorm_rows (per-wave two-pass statistics of the bf16 h,
 // closed-form merge of the W triples in wave order).
-template <int KC>
+template <int KC, int RPW>
 __global__ __launch_bounds__(256) void residual_layernorm_k(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
     const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
@@ -301,93 +302,109 @@ __global__ __launch_bounds__(256) void residual_layernorm_k(
   static_assert(U * W * kWave == G && W * NR * kWave == 256, "row shape");
   __shared__ __align__(16) u32x4_t gs[G];
   __shared__ __align__(16) u32x4_t bs[G];
-  __shared__ Welford part[W * NR];
+  __shared__ Welford part[RPW][W * NR];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int w = wave % W;
   const int rr = wave / W;
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * NR + rr;
-  const bool valid = r < rows;
-  const int64_t base = (valid ? r : rows - 1) * KC;
 
-  u32x4_t hv[U], rv[U];
+  u32x4_t hv[RPW][U], rv[RPW][U];
+  int64_t r[RPW], base[RPW];
+  bool valid[RPW];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int col = ((u * W + w) * kWave + lane) * kRowGroup;
-    hv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + base + col));
-    rv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(res + base + col));
+  for (int j = 0; j < RPW; ++j) {
+    r[j] = static_cast<int64_t>(blockIdx.x) * (NR * RPW) + rr + NR * j;
+    valid[j] = r[j] < rows;
+    base[j] = (valid[j] ? r[j] : rows - 1) * KC;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int col = ((u * W + w) * kWave + lane) * kRowGroup;
+      hv[j][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + base[j] + col));
+      rv[j][u] =
+          __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(res + base[j] + col));
+    }
   }
   for (int i = threadIdx.x; i < G; i += 256) {
     gs[i] = *reinterpret_cast<const u32x4_t*>(gamma + i * kRowGroup);
     bs[i] = *reinterpret_cast<const u32x4_t*>(beta + i * kRowGroup);
   }
 
-  float sum = 0.f;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
+  for (int j = 0; j < RPW; ++j) {
+    float sum = 0.f;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      hv[u][d] = pack_bf16x2(bf16lo(hv[u][d]) + bf16lo(rv[u][d]),
-                             bf16hi(hv[u][d]) + bf16hi(rv[u][d]));
-      sum += bf16lo(hv[u][d]) + bf16hi(hv[u][d]);
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        hv[j][u][d] = pack_bf16x2(bf16lo(hv[j][u][d]) + bf16lo(rv[j][u][d]),
+                                  bf16hi(hv[j][u][d]) + bf16hi(rv[j][u][d]));
+        sum += bf16lo(hv[j][u][d]) + bf16hi(hv[j][u][d]);
+      }
+      if (h != nullptr && valid[j])
+        __builtin_nontemporal_store(
+            hv[j][u],
+            reinterpret_cast<u32x4_t*>(h + base[j] + ((u * W + w) * kWave + lane) * kRowGroup));
     }
-    if (h != nullptr && valid)
-      __builtin_nontemporal_store(
-          hv[u], reinterpret_cast<u32x4_t*>(h + base + ((u * W + w) * kWave + lane) * kRowGroup));
-  }
-  constexpr float n = U * kRowGroup * kWave;
-  const float wmean = wave_sum(sum) / n;
-  float sq = 0.f;
+    constexpr float n = U * kRowGroup * kWave;
+    const float wmean = wave_sum(sum) / n;
+    float sq = 0.f;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < U; ++u) {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const float a = bf16lo(hv[u][d]) - wmean;
-      const float b = bf16hi(hv[u][d]) - wmean;
-      sq = __builtin_fmaf(a, a, sq);
-      sq = __builtin_fmaf(b, b, sq);
+      for (int d = 0; d < 4; ++d) {
+        const float a = bf16lo(hv[j][u][d]) - wmean;
+        const float b = bf16hi(hv[j][u][d]) - wmean;
+        sq = __builtin_fmaf(a, a, sq);
+        sq = __builtin_fmaf(b, b, sq);
+      }
     }
-  }
-  const Welford t{n, wmean, wave_sum(sq)};
-  if (lane == 0) part[wave] = t;
-  __syncthreads();  // also publishes gs / bs
-  const int first = rr * W;
-  float nn = 0.f, s1 = 0.f;
+    const Welford t{n, wmean, wave_sum(sq)};
+    if (lane == 0) part[j][wave] = t;
+    __syncthreads();  // also publishes gs / bs
+    const int first = rr * W;
+    float nn = 0.f, s1 = 0.f;
 #pragma unroll
-  for (int k = 0; k < W; ++k) {
-    nn += part[first + k].n;
-    s1 = __builtin_fmaf(part[first + k].n, part[first + k].mean, s1);
-  }
-  const float mean = s1 / nn;
-  float m2 = 0.f;
-#pragma unroll
-  for (int k = 0; k < W; ++k) {
-    const float d = part[first + k].mean - mean;
-    m2 += __builtin_fmaf(part[first + k].n * d, d, part[first + k].m2);
-  }
-  const float rstd = 1.0f / __builtin_sqrtf(m2 / static_cast<float>(KC) + eps);
-  const float shift = -mean * rstd;
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int g = (u * W + w) * kWave + lane;
-    const u32x4_t gv = gs[g];
-    const u32x4_t bv = bs[g];
-    u32x4_t o;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const float n0 = __builtin_fmaf(bf16lo(hv[u][d]), rstd, shift);
-      const float n1 = __builtin_fmaf(bf16hi(hv[u][d]), rstd, shift);
-      o[d] = pack_bf16x2(__builtin_fmaf(n0, bf16lo(gv[d]), bf16lo(bv[d])),
-                         __builtin_fmaf(n1, bf16hi(gv[d]), bf16hi(bv[d])));
+    for (int k = 0; k < W; ++k) {
+      nn += part[j][first + k].n;
+      s1 = __builtin_fmaf(part[j][first + k].n, part[j][first + k].mean, s1);
     }
-    if (valid)
-      __builtin_nontemporal_store(o, reinterpret_cast<u32x4_t*>(y + base + g * kRowGroup));
-  }
-  if (valid && w == 0 && lane == 0) {
-    if (mean_out != nullptr) mean_out[r] = mean;
-    if (rstd_out != nullptr) rstd_out[r] = rstd;
+    const float mean = s1 / nn;
+    float m2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const float d = part[j][first + k].mean - mean;
+      m2 += __builtin_fmaf(part[j][first + k].n * d, d, part[j][first + k].m2);
+    }
+    const float rstd = 1.0f / __builtin_sqrtf(m2 / static_cast<float>(KC) + eps);
+    const float shift = -mean * rstd;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int g = (u * W + w) * kWave + lane;
+      const u32x4_t gv = gs[g];
+      const u32x4_t bv = bs[g];
+      u32x4_t o;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const float n0 = __builtin_fmaf(bf16lo(hv[j][u][d]), rstd, shift);
+        const float n1 = __builtin_fmaf(bf16hi(hv[j][u][d]), rstd, shift);
+        o[d] = pack_bf16x2(__builtin_fmaf(n0, bf16lo(gv[d]), bf16lo(bv[d])),
+                           __builtin_fmaf(n1, bf16hi(gv[d]), bf16hi(bv[d])));
+      }
+      if (valid[j])
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x4_t*>(y + base[j] + g * kRowGroup));
+    }
+    if (valid[j] && w == 0 && lane == 0) {
+      if (mean_out != nullptr) mean_out[r[j]] = mean;
+      if (rstd_out != nullptr) rstd_out[r[j]] = rstd;
+    }
   }
 }
+
+// Rows per slot of residual_layernorm_k.  Measured at [16384, 4096], one
+// process: 1 row 90.2-90.8 us, 2 rows 93.4 us, 4 rows 100.6-102.8 us (each
+// wave already keeps 8 KiB in flight per row; the masked softmax, at 1 KiB
+// per row, gains from more).
+constexpr int kLayerNormRowsPerWave = 1;
 
 }  // namespace
 }  // namespace hipo
@@ -408,9 +425,11 @@ extern "C" int hipo_residual_layernorm_bf16(
   const bool vec = cols % 8 == 0 && row_plan(cols, plan) && aligned16(x) &&
                    aligned16(residual) && aligned16(gamma) && aligned16(beta) &&
                    (h == nullptr || aligned16(h)) && aligned16(y);
-  if (vec && cols == 4096 && (rows + 1) / 2 <= 0x7fffffff) {
-    residual_layernorm_k<4096><<<dim3(static_cast<unsigned>((rows + 1) / 2)), dim3(256), 0,
-                                 stream>>>(x, residual, gamma, beta, h, y, mean, rstd, rows, eps);
+  constexpr int kRowsPerBlock = 2 * kLayerNormRowsPerWave;
+  if (vec && cols == 4096 && (rows + kRowsPerBlock - 1) / kRowsPerBlock <= 0x7fffffff) {
+    residual_layernorm_k<4096, kLayerNormRowsPerWave>
+        <<<dim3(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock)), dim3(256), 0,
+           stream>>>(x, residual, gamma, beta, h, y, mean, rstd, rows, eps);
   } else if (vec) {
     const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "residual_layernorm: too many rows");
