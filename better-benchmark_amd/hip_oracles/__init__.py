@@ -68,6 +68,11 @@ _SIGNATURES = {
         [_c_ptr] * 8 + [_c_i64, _c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int,
                         _c_ptr, ctypes.c_size_t, _c_ptr]),
     "hipo_flat_copy": (ctypes.c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
+    "hipo_gelu_tanh_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
+    "hipo_gelu_tanh_f32": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
+    "hipo_transpose_last2": (
+        ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_ptr]),
+    "hipo_row_mean_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, ctypes.c_int, _c_ptr]),
     "hipo_batchnorm_train_fwd_f32_noalloc": (
         ctypes.c_int,
         [_c_ptr] * 8 + [_c_i64, _c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int, _c_ptr]),
@@ -178,6 +183,55 @@ def bias_gelu_nchw_to_nhwc(x: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
         _check(lib.hipo_bias_gelu_nchw_to_nhwc_bf16(_ptr(x), _ptr(bias), _ptr(out),
                                                     n, c, h * w, _stream(dev)),
                "bias_gelu_nchw_to_nhwc")
+    return out
+
+
+def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
+    """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) of a contiguous bf16
+    or fp32 tensor, same shape: bf16 correctly rounded per element, fp32 as
+    eager's sequence of fp32 operations."""
+    lib = load_library()
+    dev = _require_rocm(x)
+    _require(x.dtype in (torch.bfloat16, torch.float32), "gelu_tanh: bf16 or fp32 x required")
+    _require(x.is_contiguous(), "gelu_tanh: x must be contiguous")
+    y = torch.empty_like(x, memory_format=torch.contiguous_format)
+    fn = lib.hipo_gelu_tanh_bf16 if x.dtype == torch.bfloat16 else lib.hipo_gelu_tanh_f32
+    with torch.cuda.device(dev):
+        _check(fn(_ptr(x), _ptr(y), x.numel(), _stream(dev)), "gelu_tanh")
+    return y
+
+
+def transpose_last2(x: torch.Tensor) -> torch.Tensor:
+    """x.transpose(-2, -1).contiguous() for a contiguous tensor of >= 2 dims
+    with 2- or 4-byte elements, moved bit for bit."""
+    lib = load_library()
+    dev = _require_rocm(x)
+    _require(x.dim() >= 2 and x.is_contiguous(), "transpose_last2: contiguous x, >= 2 dims")
+    _require(x.element_size() in (2, 4), "transpose_last2: 2- or 4-byte elements required")
+    *lead, rows, cols = x.shape
+    y = torch.empty((*lead, cols, rows), dtype=x.dtype, device=dev)
+    batch = 1
+    for d in lead:
+        batch *= d
+    with torch.cuda.device(dev):
+        _check(lib.hipo_transpose_last2(_ptr(x), _ptr(y), batch, rows, cols,
+                                        x.element_size(), _stream(dev)), "transpose_last2")
+    return y
+
+
+def row_mean_bf16(x: torch.Tensor, *, relu: bool = False) -> torch.Tensor:
+    """bf16 mean over the last dim of a contiguous 2-D bf16 tensor (fp32 sum,
+    one rounding), of relu(x) with relu=True -> [rows] bf16."""
+    lib = load_library()
+    dev = _require_rocm(x)
+    _require(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(),
+             "row_mean_bf16: x must be contiguous 2-D bf16")
+    rows, cols = x.shape
+    _require(cols >= 1 or rows == 0, "row_mean_bf16: mean over zero elements")
+    out = torch.empty(rows, dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib.hipo_row_mean_bf16(_ptr(x), _ptr(out), rows, cols, 1 if relu else 0,
+                                      _stream(dev)), "row_mean_bf16")
     return out
 
 

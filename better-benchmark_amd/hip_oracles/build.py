@@ -37,6 +37,8 @@ SOURCES = [
     "spatial_mean.hip",
     "batchnorm_bf16.hip",
     "flat_copy.hip",
+    "gelu_flat.hip",
+    "transpose.hip",
 ]
 
 # Packed-FP32 VALU forms are disabled for all device code (the compiler

@@ -5,22 +5,9 @@
 //   y = bf16(GELU_tanh(t))           (fp32 arithmetic, one rounding)
 // GELU_tanh(t) = 0.5 t (1 + tanh(u)), u = sqrt(2/pi) (t + 0.044715 t^3).
 // t is a bf16 value, so the output is a function of its 65536 bit patterns,
-// and the kernel returns the correctly rounded bf16 of the exact function:
-//   2^-10 <= |t| < 16 (3584 inputs): read from a table of the correctly
-//     rounded results (gelu_table.h, generated at 96-bit precision), staged
-//     once per workgroup in LDS;
-//   2^-125 <= |t| < 2^-10: t / 2, an exponent decrement (GELU(t) = t/2 (1 +
-//     u + ...) with |u| < 0.8 * 2^-10, less than half a bf16 ulp, and t / 2
-//     is a bf16 value);
-//   t >= 16: t (1 - GELU(t) / t < e^-300);  t <= -16: -0 (|GELU(t)| <
-//     e^-300 underflows);  +inf -> +inf, -inf -> NaN (as -inf * 0 in
-//     eager), NaN -> NaN;
-//   |t| < 2^-125 (bf16 subnormal t / 2): t / 2 rounded to nearest even.
-// gen_gelu_table.py --check verifies the whole mapping against the exact
-// function.  Eager and Inductor evaluate the tanh form in fp32 and differ
-// from it by one ulp within a few fp32 ulps of a rounding boundary and in
-// the far negative tail, where their 1 + tanh(u) cancels.  No
-// transcendental is evaluated on the device.
+// and the kernel returns the correctly rounded bf16 of the exact function
+// (gelu_bf16.h: a 7 KiB table staged once per workgroup in LDS, bit
+// arithmetic outside its range).
 //
 // Layout: one wave64 per tile of 64 channels x 64 spatial positions of one
 // image.  Lane l owns an 8x8 (channel x position) block: cb = l / 8 picks 8
@@ -38,7 +25,7 @@
 // version of this kernel with the GELU read from a 128 KiB LDS table.
 // Loads and stores are non-temporal.
 // HBM-bound: algorithmic bytes per element = 2 (read) + 2 (write).
-#include "gelu_table.h"
+#include "gelu_bf16.h"
 #include "hipo_common.h"
 
 namespace hipo {
@@ -49,43 +36,6 @@ constexpr int kTileC = 64;   // channels per wave tile
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlockThreads = kWavesPerBlock * kWave;
 constexpr int kTilesPerWave = 1;  // consecutive position tiles per wave (3-D grid)
-
-// bf16 bits of t -> bf16 bits of GELU(t); `lut` holds kGeluTable.
-constexpr uint32_t kGeluLo = static_cast<uint32_t>(kGeluTableExpLo) << 7;  // |t| = 2^-10
-constexpr uint32_t kGeluHi = static_cast<uint32_t>(kGeluTableExpHi + 1) << 7;  // |t| = 16
-
-// The common inputs (2^-125 <= |t| < 16): the table or t / 2.  Branch-free:
-// the LDS index is clamped into the table, the read is unconditional, and a
-// select picks the result.
-__device__ __forceinline__ uint32_t gelu_bits_common(uint32_t tb, const uint16_t* lut) {
-  const uint32_t mag = tb & 0x7fffu;
-  const uint32_t off = mag - kGeluLo;  // wraps below the table
-  const uint32_t idx = __builtin_elementwise_min(off, static_cast<uint32_t>(kGeluTablePerSign - 1)) +
-                       (tb >> 15) * static_cast<uint32_t>(kGeluTablePerSign);
-  const uint32_t looked = lut[idx];
-  return off < static_cast<uint32_t>(kGeluTablePerSign) ? looked : tb - 0x80u;
-}
-
-// Inputs gelu_bits_common does not cover: |t| >= 16, inf, NaN, |t| <
-// 2^-125 (zero included).
-__device__ __forceinline__ bool gelu_rare(uint32_t tb) {
-  return ((tb & 0x7fffu) - 0x100u) >= (kGeluHi - 0x100u);
-}
-
-__device__ __forceinline__ uint32_t gelu_bits_rare(uint32_t tb) {
-  const uint32_t mag = tb & 0x7fffu;
-  if (mag < 0x100u)  // +-0 and subnormal results: t / 2 rounded to nearest even
-    return pack_bf16x2(0.5f * bf16_to_f32(static_cast<uint16_t>(tb)), 0.0f) & 0xffffu;
-  if ((tb & 0x8000u) == 0 || mag > 0x7f80u) return tb;  // t >= 16, +inf, NaN
-  return mag == 0x7f80u ? 0x7fc0u : 0x8000u;             // -inf -> NaN; t <= -16 -> -0
-}
-
-__device__ __forceinline__ uint32_t gelu_bits(uint32_t tb, const uint16_t* lut) {
-  return gelu_rare(tb) ? gelu_bits_rare(tb) : gelu_bits_common(tb, lut);
-}
-
-// The table's 16-byte chunks, staged into LDS by a workgroup.
-constexpr int kGeluTableChunks = kGeluTableSize * 2 / 16;
 
 struct TileGeom {
   int64_t C, HW;

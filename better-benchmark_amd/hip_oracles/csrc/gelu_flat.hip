@@ -1,0 +1,195 @@
+// GELU(tanh) of a contiguous tensor, element by element (no layout change).
+//
+// bf16: y = the correctly rounded bf16 GELU_tanh(x) for every bf16 x, by bit
+//   pattern (gelu_bf16.h): a 7 KiB table of correctly rounded results staged
+//   once per workgroup in LDS, bit arithmetic outside its range.  The
+//   repro's eager graph rounds every intermediate to bf16 (its 1 + tanh(u)
+//   cancels in the negative tail); Inductor and the reference's Triton
+//   oracle evaluate the chain in fp32 and round once -- the exact result is
+//   what both approximate.
+// fp32: eager's own sequence of fp32 operations, each rounded to fp32 and
+//   not contracted into FMAs:
+//     a = x * 0.5;  x3 = (x * x) * x;  b = x3 * 0.044715;  c = x + b;
+//     d = c * 0.7978845608028654;  e = tanh(d) + 1;  y = a * e
+//   with tanh from the device library (what eager and Inductor call).
+//
+// Layout: each wave64 moves a contiguous run of U KiB (U 1 KiB sub-chunks,
+// lane l taking the 16-byte vector l of each), loads issued together, four
+// waves per 256-thread workgroup, a one-shot grid in memory order; loads and
+// stores are non-temporal.  Elements past the last whole 16-byte vector are
+// done one by one by a second, one-workgroup launch.
+// HBM-bound: algorithmic bytes per element = 2 x sizeof(element).
+#include "gelu_bf16.h"
+#include "hipo_common.h"
+
+namespace hipo {
+namespace {
+
+constexpr int kGeluWaves = 4;
+constexpr int kGeluThreads = kGeluWaves * kWave;
+constexpr int kTabPerThread = (kGeluTableChunks + kGeluThreads - 1) / kGeluThreads;
+
+template <int U>
+__global__ __launch_bounds__(kGeluThreads) void gelu_bf16_flat(
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int64_t nvec) {
+  __shared__ __align__(16) uint16_t lut[kGeluTableSize];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t v0 =
+      (static_cast<int64_t>(blockIdx.x) * kGeluWaves + (threadIdx.x >> 6)) * (U * kWave) + lane;
+  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x);
+  u32x4_t* yv = reinterpret_cast<u32x4_t*>(y);
+
+  // The table's loads first (L2-resident), then the data's, so the table's
+  // LDS writes and the barrier overlap the HBM loads in flight.
+  u32x4_t tab[kTabPerThread];
+#pragma unroll
+  for (int k = 0; k < kTabPerThread; ++k) {
+    const int i = static_cast<int>(threadIdx.x) + k * kGeluThreads;
+    if (i < kGeluTableChunks) tab[k] = reinterpret_cast<const u32x4_t*>(kGeluTable)[i];
+  }
+  u32x4_t v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    // Slots past the end load the last vector (in bounds) and store nothing.
+    const int64_t i = v0 + u * kWave;
+    v[u] = __builtin_nontemporal_load(xv + (i < nvec ? i : nvec - 1));
+  }
+#pragma unroll
+  for (int k = 0; k < kTabPerThread; ++k) {
+    const int i = static_cast<int>(threadIdx.x) + k * kGeluThreads;
+    if (i < kGeluTableChunks) reinterpret_cast<u32x4_t*>(lut)[i] = tab[k];
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = v0 + u * kWave;
+    u32x4_t o;
+    bool rare = false;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[k] = gelu_pair_common(v[u][k], lut);
+      rare |= gelu_pair_rare(v[u][k]);
+    }
+    if (rare) {  // one branch per 8 values, not taken for ordinary data
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = gelu_pair(v[u][k], lut);
+    }
+    if (i < nvec) __builtin_nontemporal_store(o, yv + i);
+  }
+}
+
+// Elements [first, first + count), count < 8, from the table in global memory.
+__global__ __launch_bounds__(kWave) void gelu_bf16_tail(const uint16_t* __restrict__ x,
+                                                        uint16_t* __restrict__ y,
+                                                        int64_t first, int count) {
+  if (static_cast<int>(threadIdx.x) < count) {
+    const int64_t e = first + threadIdx.x;
+    y[e] = static_cast<uint16_t>(gelu_bits(x[e], kGeluTable));
+  }
+}
+
+__device__ __forceinline__ float gelu_tanh_eager_f32(float x) {
+#pragma clang fp contract(off)
+  const float a = x * 0.5f;
+  const float x3 = (x * x) * x;
+  const float b = x3 * 0.044715f;
+  const float c = x + b;
+  const float d = c * 0.7978845608028654f;
+  const float e = tanhf(d) + 1.0f;
+  return a * e;
+}
+
+template <int U>
+__global__ __launch_bounds__(kGeluThreads) void gelu_f32_flat(
+    const float* __restrict__ x, float* __restrict__ y, int64_t nvec) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t v0 =
+      (static_cast<int64_t>(blockIdx.x) * kGeluWaves + (threadIdx.x >> 6)) * (U * kWave) + lane;
+  const f32x4_t* xv = reinterpret_cast<const f32x4_t*>(x);
+  f32x4_t* yv = reinterpret_cast<f32x4_t*>(y);
+  f32x4_t v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = v0 + u * kWave;
+    v[u] = __builtin_nontemporal_load(xv + (i < nvec ? i : nvec - 1));
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = v0 + u * kWave;
+    f32x4_t o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = gelu_tanh_eager_f32(v[u][k]);
+    if (i < nvec) __builtin_nontemporal_store(o, yv + i);
+  }
+}
+
+__global__ __launch_bounds__(kWave) void gelu_f32_tail(const float* __restrict__ x,
+                                                       float* __restrict__ y, int64_t first,
+                                                       int count) {
+  if (static_cast<int>(threadIdx.x) < count) {
+    const int64_t e = first + threadIdx.x;
+    y[e] = gelu_tanh_eager_f32(x[e]);
+  }
+}
+
+// Vectors per lane: U KiB per wave, fewer when the tensor would not give
+// every CU a few workgroups.
+inline int vectors_per_lane(int64_t nvec, int big) {
+  const int64_t per_block_big = int64_t{big} * kGeluThreads;
+  return (nvec + per_block_big - 1) / per_block_big >= 1024 ? big : 2;
+}
+
+}  // namespace
+}  // namespace hipo
+
+extern "C" int hipo_gelu_tanh_bf16(const uint16_t* x, uint16_t* y, int64_t n,
+                                   hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  HIPO_REQUIRE(n >= 0, "gelu_tanh: negative size");
+  if (n == 0) return 0;
+  HIPO_REQUIRE(x && y, "gelu_tanh: null pointer");
+  HIPO_REQUIRE(aligned16(x) && aligned16(y), "gelu_tanh: pointers must be 16-byte aligned");
+  const int64_t nvec = n / 8;
+  const int tail = static_cast<int>(n % 8);
+  if (nvec > 0) {
+    const int u = vectors_per_lane(nvec, 8);
+    const int64_t per_block = int64_t{u} * kGeluThreads;
+    const int64_t blocks = (nvec + per_block - 1) / per_block;
+    HIPO_REQUIRE(blocks < (int64_t{1} << 31), "gelu_tanh: too large");
+    const dim3 grid(static_cast<unsigned>(blocks)), block(kGeluThreads);
+    if (u == 8) {
+      gelu_bf16_flat<8><<<grid, block, 0, stream>>>(x, y, nvec);
+    } else {
+      gelu_bf16_flat<2><<<grid, block, 0, stream>>>(x, y, nvec);
+    }
+  }
+  if (tail > 0) gelu_bf16_tail<<<dim3(1), dim3(kWave), 0, stream>>>(x, y, nvec * 8, tail);
+  return check_launch("gelu_tanh_bf16");
+}
+
+extern "C" int hipo_gelu_tanh_f32(const float* x, float* y, int64_t n, hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  HIPO_REQUIRE(n >= 0, "gelu_tanh: negative size");
+  if (n == 0) return 0;
+  HIPO_REQUIRE(x && y, "gelu_tanh: null pointer");
+  HIPO_REQUIRE(aligned16(x) && aligned16(y), "gelu_tanh: pointers must be 16-byte aligned");
+  const int64_t nvec = n / 4;
+  const int tail = static_cast<int>(n % 4);
+  if (nvec > 0) {
+    const int u = vectors_per_lane(nvec, 4);
+    const int64_t per_block = int64_t{u} * kGeluThreads;
+    const int64_t blocks = (nvec + per_block - 1) / per_block;
+    HIPO_REQUIRE(blocks < (int64_t{1} << 31), "gelu_tanh: too large");
+    const dim3 grid(static_cast<unsigned>(blocks)), block(kGeluThreads);
+    if (u == 4) {
+      gelu_f32_flat<4><<<grid, block, 0, stream>>>(x, y, nvec);
+    } else {
+      gelu_f32_flat<2><<<grid, block, 0, stream>>>(x, y, nvec);
+    }
+  }
+  if (tail > 0) gelu_f32_tail<<<dim3(1), dim3(kWave), 0, stream>>>(x, y, nvec * 4, tail);
+  return check_launch("gelu_tanh_f32");
+}

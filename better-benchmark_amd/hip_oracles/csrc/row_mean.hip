@@ -87,6 +87,99 @@ __global__ __launch_bounds__(256) void row_mean_f32_scalar(
   if (lane == 0) out[row] = s / static_cast<float>(cols);
 }
 
+
+// bf16 rows, fp32 accumulation, optional ReLU (NaN kept):
+//   out[r] = bf16(sum_j act(x[r, j]) / cols)   (one rounding, nearest even).
+// Short rows (cols <= 512, contiguous, 16-byte aligned x): each wave takes 8
+// consecutive rows -- 16 * cols bytes, a whole number of 16-byte vectors
+// whatever cols is, so the input is read as one flat stream of non-temporal
+// vector loads (the SqueezeNet rows are 169 elements, 338 bytes, not
+// vector-aligned one by one).  The wave stages its 8 rows in LDS; then 8
+// lanes per row sum every 8th element in order and combine in a fixed
+// butterfly.  Longer rows: one wave per row.
+constexpr int kBf16RowsPerWave = 8;
+constexpr int kBf16ShortCols = 512;
+constexpr int kBf16Waves = 4;
+
+template <bool RELU>
+__device__ __forceinline__ float act_relu(float v) {
+  return RELU ? __builtin_elementwise_maximum(v, 0.0f) : v;
+}
+
+__device__ __forceinline__ uint16_t round_to_bf16(float v) {
+  return static_cast<uint16_t>(pack_bf16x2(v, 0.0f) & 0xffffu);
+}
+
+template <bool RELU, int VPL>
+__global__ __launch_bounds__(kBf16Waves * kWave) void row_mean_bf16_short(
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ out, int64_t rows, int cols) {
+  __shared__ __align__(16) uint16_t stage[kBf16Waves][kBf16RowsPerWave * kBf16ShortCols];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kBf16Waves + wave) * kBf16RowsPerWave;
+  const int64_t nrows = rows - row0 < kBf16RowsPerWave ? rows - row0 : kBf16RowsPerWave;
+  uint16_t* lds = stage[wave];
+  if (nrows > 0) {
+    // The wave's rows: `cols` vectors of 16 bytes when all 8 rows exist;
+    // the last group may end inside a vector, whose elements move singly.
+    const int64_t elems = nrows * cols;
+    const int whole = static_cast<int>(elems / 8);
+    const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x + row0 * cols);
+    u32x4_t v[VPL];
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int i = lane + k * kWave;
+      if (i < whole) v[k] = __builtin_nontemporal_load(xv + i);
+    }
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int i = lane + k * kWave;
+      if (i < whole) reinterpret_cast<u32x4_t*>(lds)[i] = v[k];
+    }
+    const int rest = static_cast<int>(elems - int64_t{whole} * 8);
+    if (lane < rest) lds[whole * 8 + lane] = x[row0 * cols + whole * 8 + lane];
+  }
+  __syncthreads();
+  if (nrows <= 0) return;
+  const int r = lane >> 3;   // row of the group
+  const int k = lane & 7;    // this lane's residue class
+  float s = 0.0f;
+  if (r < nrows) {
+    const uint16_t* p = lds + r * cols;
+    for (int j = k; j < cols; j += 8) s += act_relu<RELU>(bf16_to_f32(p[j]));
+  }
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 4);
+  if (k == 0 && r < nrows) out[row0 + r] = round_to_bf16(s / static_cast<float>(cols));
+}
+
+template <bool RELU, bool VEC>
+__global__ __launch_bounds__(256) void row_mean_bf16_long(const uint16_t* __restrict__ x,
+                                                          uint16_t* __restrict__ out,
+                                                          int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // wave-uniform; no barrier follows
+  const uint16_t* p = x + row * cols;
+  float acc = 0.0f;
+  if constexpr (VEC) {
+    const u32x4_t* pv = reinterpret_cast<const u32x4_t*>(p);
+    for (int64_t i = lane; i < cols / 8; i += kWave) {
+      const u32x4_t w = __builtin_nontemporal_load(pv + i);
+      float t = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        t += act_relu<RELU>(bf16lo(w[q])) + act_relu<RELU>(bf16hi(w[q]));
+      acc += t;
+    }
+  } else {
+    for (int64_t i = lane; i < cols; i += kWave) acc += act_relu<RELU>(bf16_to_f32(p[i]));
+  }
+  const float s = wave_sum(acc);
+  if (lane == 0) out[row] = round_to_bf16(s / static_cast<float>(cols));
+}
+
 }  // namespace
 }  // namespace hipo
 
@@ -140,4 +233,47 @@ extern "C" int hipo_row_mean_f32(const float* x, float* out, int64_t rows,
                           stream>>>(x, out, rows, cols, row_stride);
   }
   return check_launch("row_mean_f32");
+}
+
+extern "C" int hipo_row_mean_bf16(const uint16_t* x, uint16_t* out, int64_t rows,
+                                  int64_t cols, int relu, hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  HIPO_REQUIRE(rows >= 0 && cols >= 0, "row_mean_bf16: negative size");
+  if (rows == 0) return 0;
+  HIPO_REQUIRE(cols > 0, "row_mean_bf16: mean over zero elements");
+  HIPO_REQUIRE(x != nullptr && out != nullptr, "row_mean_bf16: null pointer");
+  const bool act = relu != 0;
+  if (cols <= kBf16ShortCols && aligned16(x)) {
+    const int64_t groups = (rows + kBf16RowsPerWave - 1) / kBf16RowsPerWave;
+    const int64_t blocks = (groups + kBf16Waves - 1) / kBf16Waves;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "row_mean_bf16: too many rows");
+    const dim3 grid(static_cast<unsigned>(blocks)), block(kBf16Waves * kWave);
+    const int c = static_cast<int>(cols);
+    // cols vectors of 16 bytes per wave: ceil(cols / 64) per lane.
+#define HIPO_RMB(V_)                                                                    \
+  (act ? row_mean_bf16_short<true, V_><<<grid, block, 0, stream>>>(x, out, rows, c)     \
+       : row_mean_bf16_short<false, V_><<<grid, block, 0, stream>>>(x, out, rows, c))
+    if (cols <= 2 * kWave) {
+      HIPO_RMB(2);
+    } else if (cols <= 4 * kWave) {
+      HIPO_RMB(4);
+    } else {
+      HIPO_RMB(8);
+    }
+#undef HIPO_RMB
+  } else {
+    const bool vec = cols % 8 == 0 && aligned16(x);
+    const int64_t blocks = (rows + 3) / 4;
+    HIPO_REQUIRE(blocks <= 0x7fffffff, "row_mean_bf16: too many rows");
+    const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+    if (vec) {
+      if (act) row_mean_bf16_long<true, true><<<grid, block, 0, stream>>>(x, out, rows, cols);
+      else row_mean_bf16_long<false, true><<<grid, block, 0, stream>>>(x, out, rows, cols);
+    } else {
+      if (act) row_mean_bf16_long<true, false><<<grid, block, 0, stream>>>(x, out, rows, cols);
+      else row_mean_bf16_long<false, false><<<grid, block, 0, stream>>>(x, out, rows, cols);
+    }
+  }
+  return check_launch("row_mean_bf16");
 }

@@ -1,0 +1,38 @@
+"""
+MI355X oracle for pointwise_2d969ac9ad59: tanh GELU of a contiguous bf16 or
+fp32 activation, returned in the second view's shape.
+
+Kernels: hipo_gelu_tanh_bf16 -- the correctly rounded bf16 GELU of every
+bf16 input by bit pattern (a 7 KiB table of exactly rounded results staged
+in LDS, bit arithmetic outside its range; the eager graph's per-op bf16
+roundings and Inductor's fp32 chain both approximate this value);
+hipo_gelu_tanh_f32 -- eager's fp32 operation sequence, uncontracted, with
+the device library's tanh.  Flat streams of 16-byte non-temporal accesses,
+8 KiB per wave.  Algorithmic bytes: 2 x numel x element size.
+Replaces the Triton body of the reference's
+repros/canonical/pointwise_2d969ac9ad59/oracle.py:44-62 (_tanh_gelu_kernel, :12).
+"""
+import sys
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+import hip_oracles  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
+
+_POINTS = ("cd47785e", "92efc45e", "d05618d1", "7b14189f", "5cd82a46", "8f687505")
+
+
+def oracle_forward(inputs):
+    x, _shape, out_shape = inputs
+    return hip_oracles.gelu_tanh(x).view(out_shape)
+
+
+for _point in _POINTS:
+    oracle_forward = oracle_impl(hardware="MI355X", point=_point,
+                                 description="flat tanh GELU")(oracle_forward)
+oracle_forward = oracle_impl(hardware="MI355X",
+                             description="flat tanh GELU, shape-general")(oracle_forward)
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

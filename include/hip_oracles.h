@@ -58,9 +58,8 @@ int hipo_row_mean_f32(const float* x, float* out, int64_t rows, int64_t cols,
  * Channel bias + GELU(tanh) + NCHW -> NHWC:
  *   t = bf16(x[n,c,hw] + bias[c])       (eager order: the add rounds to bf16)
  *   y = 0.5 t (1 + tanh(sqrt(2/pi) (t + 0.044715 t^3)))
- *   out[n,hw,c] = bf16(y)    (y in fp32 as t / (1 + 2^(t (K0 + K1 t^2))),
- *                             the same function, with the hardware exp2 and
- *                             reciprocal; one rounding)
+ *   out[n,hw,c] = bf16(y), correctly rounded (t is bf16: a table of the
+ *                 exactly rounded results by bit pattern)
  * x is contiguous NCHW [n, c, hw]; out is the same logical tensor stored
  * channels-last (physical [n, hw, c]).
  * Replaces the Triton bodies of oracle_forward in
@@ -309,6 +308,45 @@ int hipo_batchnorm_train_fwd_f32_noalloc(const float* x, const float* gamma,
  */
 int hipo_flat_copy(const void* src, int64_t read_bytes, void* dst,
                    int64_t write_bytes, hipStream_t stream);
+
+/*
+ * GELU(tanh) of a contiguous tensor of n elements, element by element:
+ *   bf16: y = the correctly rounded bf16 of 0.5 x (1 + tanh(sqrt(2/pi)
+ *         (x + 0.044715 x^3))) for every bf16 x (no intermediate rounding);
+ *   fp32: eager's operation sequence in fp32, each op rounded, no FMA
+ *         contraction: (x * 0.5) * (tanh((x + ((x * x) * x) * 0.044715) *
+ *         0.7978845608028654) + 1), tanh from the device library.
+ * x and y are 16-byte aligned and do not overlap.
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/pointwise_2d969ac9ad59/oracle.py:44-62 (_tanh_gelu_kernel,
+ * same file :12-26), whose view-reshape wrapper stays in Python.
+ */
+int hipo_gelu_tanh_bf16(const uint16_t* x, uint16_t* y, int64_t n, hipStream_t stream);
+int hipo_gelu_tanh_f32(const float* x, float* y, int64_t n, hipStream_t stream);
+
+/*
+ * Batched transpose of the last two dimensions, bit for bit:
+ *   y[b, c, r] = x[b, r, c],  x [batch, rows, cols], y [batch, cols, rows],
+ * both contiguous, elements of elem_size bytes (2 or 4), x and y distinct.
+ * permute(0, 1, 3, 2) + clone of a contiguous 4-D tensor is the case
+ * batch = d0 * d1.  Replaces the Triton body of oracle_forward in
+ * repros/canonical/pointwise_021e90d9c17d/oracle.py:55-80
+ * (_visformer_attention_to_image_kernel, same file :23).
+ */
+int hipo_transpose_last2(const void* x, void* y, int64_t batch, int64_t rows,
+                         int64_t cols, int elem_size, hipStream_t stream);
+
+/*
+ * bf16 row mean with an optional ReLU (relu != 0; NaN propagates):
+ *   out[r] = bf16(sum_j act(x[r, j]) / cols), fp32 sum, one rounding.
+ * x is contiguous [rows, cols] (cols >= 1); out is [rows].  The NCHW
+ * spatial mean relu(x).mean([-1, -2]) is the case rows = N * C, cols = H * W.
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/mean_b402ee209d0b/oracle.py:53-80
+ * (_relu_spatial_mean_kernel, same file :23-50).
+ */
+int hipo_row_mean_bf16(const uint16_t* x, uint16_t* out, int64_t rows, int64_t cols,
+                       int relu, hipStream_t stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

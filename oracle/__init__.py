@@ -45,6 +45,10 @@ _SIGS = {
     "ref_batchnorm_nhwc_act_pad_bf16": (
         None, [_p] * 8 + [_i64] * 6 + [_f, _f, _f, _i, _i]),
     "ref_batchnorm_nchw_act_mean_bf16": (None, [_p] * 8 + [_i64] * 3 + [_f, _f, _f, _i, _i]),
+    "ref_gelu_tanh_bf16": (None, [_p, _p, _i64, _i]),
+    "ref_gelu_tanh_f32": (None, [_p, _p, _i64, _i]),
+    "ref_transpose_last2": (None, [_p, _p, _i64, _i64, _i64, _i, _i]),
+    "ref_row_mean_bf16": (None, [_p, _p, _i64, _i64, _i, _i]),
 }
 
 _ACTS = {None: 0, "none": 0, "relu": 1, "silu": 2}
@@ -235,3 +239,38 @@ def batchnorm_nchw_act_mean(x, gamma, beta, running_mean, running_var, *, moment
         sm.data_ptr(), sr.data_ptr(), out.data_ptr(), n, c, h * w, float(momentum),
         float(eps), float(var_scale), _ACTS[act], _th(threads))
     return sm, sr, out, rm, rv
+
+
+def gelu_tanh(x, threads=None):
+    """GELU(tanh) of a bf16 or fp32 tensor, evaluated in fp64 and rounded
+    once; same shape, contiguous."""
+    assert x.dtype in (torch.bfloat16, torch.float32), x.dtype
+    x = x.detach().to("cpu").contiguous()
+    y = torch.empty_like(x)
+    fn = load().ref_gelu_tanh_bf16 if x.dtype == torch.bfloat16 else load().ref_gelu_tanh_f32
+    fn(x.data_ptr(), y.data_ptr(), x.numel(), _th(threads))
+    return y
+
+
+def transpose_last2(x, threads=None):
+    """x.transpose(-2, -1) made contiguous, element bits copied."""
+    x = x.detach().to("cpu").contiguous()
+    *lead, rows, cols = x.shape
+    y = torch.empty((*lead, cols, rows), dtype=x.dtype)
+    batch = 1
+    for d in lead:
+        batch *= d
+    load().ref_transpose_last2(x.data_ptr(), y.data_ptr(), batch, rows, cols,
+                               x.element_size(), _th(threads))
+    return y
+
+
+def row_mean_bf16(x, *, relu: bool = False, threads=None):
+    """bf16 mean over the last dim of a 2-D bf16 tensor (of relu(x) with
+    relu=True), fp64 sum, one rounding -> [rows]."""
+    x = _cpu(x, torch.bfloat16)
+    rows, cols = x.shape
+    out = torch.empty(rows, dtype=torch.bfloat16)
+    load().ref_row_mean_bf16(x.data_ptr(), out.data_ptr(), rows, cols, 1 if relu else 0,
+                             _th(threads))
+    return out

@@ -10,6 +10,10 @@
  *   row mean            repros/canonical/mean_c9e1a8113328/repro.py:26
  *   bias + GELU(tanh)   repros/canonical/pointwise_2d969ac9ad59/repro.py:23-36
  *   NCHW -> NHWC        repros/canonical/pointwise_021e90d9c17d/repro.py:26-28
+ *   GELU(tanh), flat    repros/canonical/pointwise_2d969ac9ad59/oracle.py:12-26
+ *                       (the chain in fp32, one rounding; here in fp64)
+ *   permute + clone     repros/canonical/pointwise_021e90d9c17d/repro.py:26-28
+ *   ReLU + NCHW mean    repros/canonical/mean_b402ee209d0b/repro.py:24-26
  *   masked softmax      repros/canonical/amax_sum_192a3a5bd7ff/repro.py:23-44
  *   residual LayerNorm  repros/canonical/var_mean_80e7ff4dee7f/repro.py:23-39
  *   RMSNorm             repros/canonical/mean_4462ce967d63/repro.py:23-38
@@ -107,9 +111,14 @@ void ref_row_mean_f32(const float* x, float* out, int64_t rows, int64_t cols,
   }
 }
 
+/* 0.5 t (1 + tanh(u)) = t / (1 + e^(-2u)), u = sqrt(2/pi) (t + 0.044715 t^3):
+ * the second form does not cancel in the negative tail, where 1 + tanh(u)
+ * would lose every digit in double below t ~ -5.  Specials: gelu(+inf) =
+ * +inf, gelu(-inf) = NaN (as eager's -inf * 0), NaN -> NaN. */
 static inline double gelu_tanh(double t) {
   const double k = 0.7978845608028654; /* sqrt(2/pi) */
-  return 0.5 * t * (1.0 + tanh(k * (t + 0.044715 * t * t * t)));
+  const double u = k * (t + 0.044715 * t * t * t);
+  return t / (1.0 + exp(-2.0 * u));
 }
 
 /*
@@ -450,4 +459,49 @@ void ref_batchnorm_nchw_act_mean_bf16(const uint16_t* x, const float* gamma,
   }
   free(mean);
   free(rstd);
+}
+
+/* y = bf16(gelu_tanh(x)) of n bf16 values: fp64, one rounding. */
+void ref_gelu_tanh_bf16(const uint16_t* x, uint16_t* y, int64_t n, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t i = 0; i < n; ++i) y[i] = f64_to_bf16(gelu_tanh((double)bf16_to_f32(x[i])));
+}
+
+/* y = (float)gelu_tanh(x) of n fp32 values: fp64, one rounding. */
+void ref_gelu_tanh_f32(const float* x, float* y, int64_t n, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t i = 0; i < n; ++i) y[i] = (float)gelu_tanh((double)x[i]);
+}
+
+/* y[b, c, r] = x[b, r, c] for elements of es bytes (any es). */
+void ref_transpose_last2(const void* x, void* y, int64_t batch, int64_t rows, int64_t cols,
+                         int es, int threads) {
+  const unsigned char* xs = (const unsigned char*)x;
+  unsigned char* ys = (unsigned char*)y;
+#pragma omp parallel for num_threads(threads) schedule(static) collapse(2)
+  for (int64_t b = 0; b < batch; ++b) {
+    for (int64_t r = 0; r < rows; ++r) {
+      for (int64_t c = 0; c < cols; ++c) {
+        memcpy(ys + ((b * cols + c) * rows + r) * es, xs + ((b * rows + r) * cols + c) * es,
+               (size_t)es);
+      }
+    }
+  }
+}
+
+/* out[r] = bf16(sum_j act(x[r, j]) / cols), fp64 sum; act = ReLU (NaN kept)
+ * when relu != 0. */
+void ref_row_mean_bf16(const uint16_t* x, uint16_t* out, int64_t rows, int64_t cols,
+                       int relu, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint16_t* p = x + r * cols;
+    double s = 0.0;
+    for (int64_t j = 0; j < cols; ++j) {
+      double v = bf16_to_f32(p[j]);
+      if (relu && v < 0.0) v = 0.0;
+      s += v;
+    }
+    out[r] = f64_to_bf16(s / (double)cols);
+  }
 }

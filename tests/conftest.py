@@ -32,6 +32,9 @@ VARIANT_IDS = [
     "var_mean_80e7ff4dee7f",
     "var_mean_ceb5c315290a",
     "var_mean_mean_19ffdb35cc67",
+    "pointwise_2d969ac9ad59",
+    "pointwise_021e90d9c17d",
+    "mean_b402ee209d0b",
 ]
 
 

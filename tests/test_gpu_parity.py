@@ -34,9 +34,9 @@ EXACT = (0.0, 0.0)
 # fp32 output, no ulp check; the floor is where the one-ulp bound starts).
 OUTPUT_TOLS = {
     "mean_lastdim_f32": [(F32_TOL, None)],
-    # GELU: below ~1e-4 the tanh form's 1 + tanh(u) cancels (eager does the
-    # same), so the result is only pinned by the 1e-6 absolute floor there.
-    "pointwise_bias_gelu_tanh_nhwc": [(PROB_TOL, 1e-4)],
+    # GELU: kernel (a table of exactly rounded results) and oracle (fp64 in
+    # the non-cancelling form t / (1 + e^-2u)) both round the exact value.
+    "pointwise_bias_gelu_tanh_nhwc": [(PROB_TOL, 0.0)],
     "amax_sum_scaled_masked_softmax": [(PROB_TOL, 0.0)],
     "var_mean_residual_layernorm": [(EXACT, 0.0), (BF16_TOL, 1e-5), (F32_TOL, None),
                                     (F32_TOL, None)],
@@ -162,6 +162,13 @@ def _family_oracle(rid, i):
     if rid == "var_mean_80e7ff4dee7f":
         x, r, g, b = i[0], i[1].reshape(i[0].shape), i[2], i[3]
         return [ref.residual_layernorm(x, r, g, b, 1e-5)[1].reshape(i[4])]
+    if rid == "pointwise_2d969ac9ad59":
+        return [ref.gelu_tanh(i[0])]
+    if rid == "pointwise_021e90d9c17d":
+        return [ref.transpose_last2(i[0])]
+    if rid == "mean_b402ee209d0b":
+        x = i[0]
+        return [ref.row_mean_bf16(x.reshape(x.shape[0] * x.shape[1], -1), relu=True)]
     if rid == "var_mean_ceb5c315290a":
         x, rm, rv, g, b = i
         return list(ref.batchnorm_nhwc_act_pad(x, g, b, rm, rv, momentum=0.1, eps=1e-3,
@@ -170,6 +177,27 @@ def _family_oracle(rid, i):
     x, rm, rv, g, b = i
     return list(ref.batchnorm_nchw_act_mean(x, g, b, rm, rv, momentum=0.1, eps=1e-5,
                                             var_scale=1.0001594642002871, act="relu"))
+
+
+# Family outputs held to something other than _tol(output) (rtol, atol):
+#   vs the C oracle -- the permute + clone moves bits (exact); the bf16 GELU
+#     is the correctly rounded value, as is the oracle's (within one ulp,
+#     checked below, of which the rounding boundaries allow a few);
+#   vs eager -- the decomposed GELU graph rounds each of its eight ops to
+#     bf16, and its 1 + tanh(u) loses up to half its digits in the negative
+#     tail (about 2e-3 absolute near x = -3), so eager is held to the
+#     reference harness's own comparison, allclose(atol=rtol=1e-2)
+#     (oracle_harness.py:865-923); the fp64 gate below still applies.
+# The ulp floor above which a family's bf16 output must be within one ulp of
+# the C oracle (families with no cancellation inside: the GELU table and
+# the fp64 oracle both round the exact value; a ReLU'd sum has no
+# cancellation; a transpose is exact).
+FAMILY_ORACLE_TOLS = {"pointwise_021e90d9c17d": {torch.bfloat16: EXACT},
+                      "pointwise_2d969ac9ad59": {torch.bfloat16: PROB_TOL}}
+FAMILY_EAGER_TOLS = {"pointwise_2d969ac9ad59": {torch.bfloat16: (1e-2, 1e-2)},
+                     "pointwise_021e90d9c17d": {torch.bfloat16: EXACT}}
+FAMILY_ULP_FLOOR = {"pointwise_2d969ac9ad59": 0.0, "pointwise_021e90d9c17d": 0.0,
+                    "mean_b402ee209d0b": 0.0}
 
 
 @pytest.mark.parametrize("rid", VARIANT_IDS)
@@ -202,8 +230,16 @@ def test_family_points_vs_eager(rid, rocm_device):
         for i, (g, e, x, o) in enumerate(zip(got, eager, exact, oracle_out)):
             assert g.dtype == e.dtype and g.shape == e.shape, f"{label} out{i}"
             assert g.stride() == e.stride(), f"{label} out{i} strides {g.stride()} vs {e.stride()}"
-            assert_close(g, o.reshape(e.shape), _tol(e), f"{rid}/{label} out{i} vs oracle")
-            assert_close(g, e, _tol(e), f"{rid}/{label} out{i} vs eager")
+            o = o.reshape(e.shape)
+            assert_close(g, o, FAMILY_ORACLE_TOLS.get(rid, {}).get(e.dtype, _tol(e)),
+                         f"{rid}/{label} out{i} vs oracle")
+            if g.dtype == torch.bfloat16 and rid in FAMILY_ULP_FLOOR:
+                flips = assert_bf16_ulps(g, o, FAMILY_ULP_FLOOR[rid],
+                                         f"{rid}/{label} out{i} vs oracle")
+                print(f"[{rid}] {label} out{i}: {flips} of {g.numel()} values one bf16 ulp "
+                      f"off the oracle", flush=True)
+            assert_close(g, e, FAMILY_EAGER_TOLS.get(rid, {}).get(e.dtype, _tol(e)),
+                         f"{rid}/{label} out{i} vs eager")
             # fp64 skips the graph's intermediate bf16 roundings, so it is an
             # anchor, not a tolerance target: the reference's gate rule
             # (oracle_harness.py:1511-1530) -- no worse than 3x eager's error.
@@ -273,17 +309,13 @@ def test_bias_gelu_edges(rocm_device):
 
 def test_bias_gelu_every_bf16_input(rocm_device):
     """All 65536 bf16 bit patterns as x (bias 0), through both the tile
-    kernel (C = 8, HW = 2048) and the scalar path (C = 8, HW = 8193).
+    kernel (C = 8, HW = 2048) and the scalar path (C = 8, HW = 8193),
+    against the C oracle (fp64, one rounding).
 
-    The kernel evaluates eager's tanh GELU in fp32 with the device library's
-    tanhf and rounds once, so it matches the oracle's correctly rounded fp64
-    GELU except (a) where the fp32 value sits within a few ulps of a bf16
-    rounding boundary: there the two differ by one bf16 ulp; (b) in the far
-    negative tail, where 1 + tanh(u) cancels in fp32 (as in eager) and only
-    the absolute floor pins the result.  Bar: every finite input within
-    rtol 1.6e-2 / atol 1e-6; every value with |y| >= 1e-5 within one ulp, at
-    most 64 of them off at all; special values as eager.  The counts are
-    printed."""
+    Both round the exact GELU_tanh(t); they can differ only where fp64's own
+    error (~1e-13 relative) straddles a bf16 rounding boundary.  Bar: every
+    finite input within one ulp, at most 4 off at all; NaN -> NaN,
+    +inf -> +inf, -inf -> NaN.  The count is printed."""
     import hip_oracles
     import oracle as ref
     bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
@@ -298,15 +330,11 @@ def test_bias_gelu_every_bf16_input(rocm_device):
         finite = torch.isfinite(xf)
         assert_close(torch.where(finite, g, 0), torch.where(finite, w, 0), PROB_TOL,
                      f"gelu every input ({what})")
-        sel = finite & (w.abs() >= 1e-5)
         ulps = bf16_ulp_distance(got, want)
-        off = sel & (ulps > 0)
-        tail = finite & ~sel & (ulps > 0)
-        print(f"gelu every input ({what}): {int(off.sum())} of {int(sel.sum())} values with "
-              f"|y| >= 1e-5 one ulp off; {int(tail.sum())} tail values (|y| < 1e-5) differ, "
-              f"max |diff| {float((g - w)[tail].abs().max()) if tail.any() else 0.0:.2e}",
-              flush=True)
-        assert int(off.sum()) <= 64, f"{what}: {int(off.sum())} inputs off the correctly rounded GELU"
+        off = finite & (ulps > 0)
+        print(f"gelu every input ({what}): {int(off.sum())} of {int(finite.sum())} finite "
+              f"inputs off the oracle", flush=True)
+        assert int(off.sum()) <= 4, f"{what}: {int(off.sum())} inputs off the correctly rounded GELU"
         assert (ulps[off] == 1).all(), f"{what}: a result more than one bf16 ulp off"
         assert torch.isnan(g[torch.isnan(xf)]).all()
         assert (g[xf == float("inf")] == float("inf")).all()
@@ -348,6 +376,104 @@ def test_bias_gelu_is_the_correctly_rounded_gelu(rocm_device):
             if w is not None and (gv & 0xFFFF) != w:
                 bad += 1
         assert bad == 0, f"{what}: {bad} inputs differ from the correctly rounded GELU"
+
+
+def test_gelu_flat_every_input_and_sizes(rocm_device):
+    """Flat GELU: bf16 bit for bit equal to the transposing kernel's mapping
+    (the correctly rounded GELU) over all 65536 inputs, at sizes that leave
+    a tail of 1..7 elements and below one vector; fp32 against the C oracle
+    (fp64) to fp32 error, and bit for bit against eager's op sequence on the
+    device."""
+    import hip_oracles
+    import oracle as ref
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    xs = bits.view(torch.bfloat16)
+    want = hip_oracles.bias_gelu_nchw_to_nhwc(
+        xs.reshape(4, 8, 64, 32).to(rocm_device), torch.zeros(8, dtype=torch.bfloat16,
+                                                              device=rocm_device))
+    want = want.cpu().contiguous().reshape(-1)  # logical NCHW order = the order of xs
+    got = hip_oracles.gelu_tanh(xs.to(rocm_device)).cpu()
+    # the tile kernel maps t = bf16(x + bias), which quiets NaNs and turns
+    # -0 into +0; the flat kernel maps x's own bits: compare the rest
+    xf = xs.float()
+    same = ~torch.isnan(xf) & (bits != torch.tensor(-32768, dtype=torch.int16))
+    assert torch.equal(got.view(torch.int16)[same], want.view(torch.int16)[same]), \
+        "flat vs tile mapping"
+    assert torch.isnan(got.float()[torch.isnan(xf)]).all(), "NaN -> NaN"
+    neg0 = got[bits == torch.tensor(-32768, dtype=torch.int16)].float()
+    assert neg0.item() == 0 and torch.signbit(neg0).item(), "gelu(-0) = -0"
+    for n in (1, 7, 8, 9, 1023, 65536 + 5, 3 * 2**20 + 3):
+        g = torch.Generator().manual_seed(n)
+        x = (4 * torch.randn(n, generator=g)).to(torch.bfloat16)
+        y = hip_oracles.gelu_tanh(x.to(rocm_device)).cpu()
+        assert_bf16_ulps(y, ref.gelu_tanh(x), 0.0, f"bf16 n={n}")
+        xf = 4 * torch.randn(n, generator=g)
+        yf = hip_oracles.gelu_tanh(xf.to(rocm_device))
+        # eager's fp32 sequence: 1 + tanh(u) cancels in the negative tail, so
+        # the error there is absolute (~1e-7), inside F32_TOL's floor
+        assert_close(yf, ref.gelu_tanh(xf), F32_TOL, f"fp32 n={n}")
+        xd = xf.to(rocm_device)
+        eager = (xd * 0.5) * (torch.tanh((xd + (xd * xd * xd) * 0.044715) * 0.7978845608028654) + 1)
+        same = int((yf == eager).sum())
+        print(f"gelu fp32 n={n}: {same} of {n} bit-identical to eager on the device", flush=True)
+        # the same fp32 operations in the same order, the same device tanh
+        assert same == n, f"fp32 n={n}: {n - same} values differ from eager's op sequence"
+    with pytest.raises(RuntimeError, match="aligned"):
+        hip_oracles.gelu_tanh(torch.zeros(17, dtype=torch.bfloat16, device=rocm_device)[1:])
+
+
+def test_transpose_last2_paths(rocm_device):
+    """Bit-exact against the C oracle on every path: whole matrices with an
+    odd and an even row count (pad slots), several matrices per workgroup,
+    rows not 16-byte multiples on the element path, misaligned pointers,
+    4-byte elements, matrices above 32 KiB (tiles), NaN payloads kept."""
+    import hip_oracles
+    import oracle as ref
+    cases = [((128, 6, 49, 128), torch.bfloat16), ((128, 6, 196, 64), torch.bfloat16),
+             ((3000, 4, 8), torch.bfloat16), ((5, 7, 13), torch.bfloat16),
+             ((2, 3, 33, 16), torch.float32), ((4, 130, 70), torch.bfloat16),
+             ((2, 300, 257), torch.float32), ((1, 1, 1), torch.bfloat16), ((7, 2, 1), torch.float32)]
+    for shape, dtype in cases:
+        g = torch.Generator().manual_seed(sum(shape))
+        if dtype == torch.bfloat16:
+            x = torch.randint(-32768, 32767, shape, generator=g, dtype=torch.int16).view(dtype)
+        else:
+            x = torch.randn(shape, generator=g)
+        got = hip_oracles.transpose_last2(x.to(rocm_device)).cpu()
+        want = ref.transpose_last2(x)
+        view = torch.int16 if dtype == torch.bfloat16 else torch.int32
+        assert torch.equal(got.view(view), want.view(view)), f"transpose {shape} {dtype}"
+    # a misaligned start: the element path
+    base = torch.randn(1 + 6 * 49 * 128).to(torch.bfloat16)
+    x = base.to(rocm_device)[1:].view(6, 49, 128)
+    got = hip_oracles.transpose_last2(x).cpu()
+    assert torch.equal(got.view(torch.int16),
+                       ref.transpose_last2(base[1:].view(6, 49, 128)).view(torch.int16))
+
+
+def test_row_mean_bf16_paths(rocm_device):
+    """bf16 row mean (+ ReLU): short rows through LDS in groups of 8 (row
+    counts not multiples of 8, so the last group ends inside a vector), long
+    rows per wave with vector or element loads, a misaligned start; within
+    one ulp of the C oracle with ReLU (no cancellation), the bf16 tolerance
+    without; NaN propagates."""
+    import hip_oracles
+    import oracle as ref
+    for rows, cols in ((16000, 169), (9, 7), (13, 1), (3, 512), (5, 513), (6, 4096), (11, 1001)):
+        g = torch.Generator().manual_seed(rows * 7 + cols)
+        x = (torch.randn(rows, cols, generator=g) + 0.3).to(torch.bfloat16)
+        xd = x.to(rocm_device)
+        got = hip_oracles.row_mean_bf16(xd, relu=True).cpu()
+        assert_bf16_ulps(got, ref.row_mean_bf16(x, relu=True), 0.0, f"relu {rows}x{cols}")
+        got = hip_oracles.row_mean_bf16(xd).cpu()
+        assert_close(got, ref.row_mean_bf16(x), BF16_TOL, f"mean {rows}x{cols}")
+    base = torch.randn(1 + 10 * 169).to(torch.bfloat16)
+    got = hip_oracles.row_mean_bf16(base.to(rocm_device)[1:].view(10, 169), relu=True).cpu()
+    assert_bf16_ulps(got, ref.row_mean_bf16(base[1:].view(10, 169), relu=True), 0.0, "misaligned")
+    x = torch.randn(9, 169).to(torch.bfloat16)
+    x[4, 100] = float("nan")
+    got = hip_oracles.row_mean_bf16(x.to(rocm_device), relu=True).cpu().float()
+    assert torch.isnan(got[4]) and not torch.isnan(got[[0, 1, 2, 3, 5, 6, 7, 8]]).any()
 
 
 def test_softmax_closed_forms(rocm_device):

@@ -298,6 +298,90 @@ def check_bn_nchw(fn):
     assert torch.equal(out.float(), torch.tensor([[0.0, 0.75]] * 3)), "relu(beta) on constant channels"
 
 
+def _exact_gelu_bits(bits):
+    """Correctly rounded bf16 GELU(tanh) by mpmath (the GELU table's generator)."""
+    import importlib.util
+    gen_path = Path(__file__).resolve().parents[1] / "better-benchmark_amd" / "hip_oracles" \
+        / "gen_gelu_table.py"
+    spec = importlib.util.spec_from_file_location("gen_gelu_table", gen_path)
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    return [gen.to_bf16(gen.gelu_tanh_exact(gen.bf16_value(b))) for b in bits]
+
+
+def check_gelu_flat(fn):
+    # bf16: every 7th finite bit pattern against the exact function at 96
+    # bits, rounded to nearest even -- equal but for fp64's own error at a
+    # rounding boundary (a handful, one ulp)
+    bits = [b for b in range(0, 65536, 7) if (b & 0x7FFF) < 0x7F80]
+    x = torch.tensor(bits, dtype=torch.int32).to(torch.int16).view(BF)
+    got = fn(x).view(torch.int16).int().tolist()
+    want = _exact_gelu_bits(bits)
+    off = [(b, g & 0xFFFF, w) for b, g, w in zip(bits, got, want) if (g & 0xFFFF) != w]
+    assert len(off) <= 4 and all(abs((g & 0x7FFF) - (w & 0x7FFF)) == 1 for _, g, w in off), \
+        f"bf16 vs exact: {[(hex(b), hex(g), hex(w)) for b, g, w in off[:8]]}"
+    # specials and closed forms
+    sp = torch.tensor([0.0, -0.0, 16.0, 300.0, -16.0, -300.0, float("inf"), float("-inf"),
+                       float("nan"), 2.0 ** -20, -(2.0 ** -20)]).to(BF)
+    y = fn(sp).float()
+    assert y[0] == 0 and not torch.signbit(y[0]) and y[1] == 0 and torch.signbit(y[1])
+    assert y[2] == 16.0 and y[3] == 300.0, "gelu(t) = t for large t"
+    assert y[4] == 0 and y[5] == 0, "gelu(t) -> 0 for large negative t"
+    assert y[6] == float("inf") and torch.isnan(y[7]) and torch.isnan(y[8])
+    assert y[9] == 2.0 ** -21 and y[10] == -(2.0 ** -21), "gelu(t) = t / 2 for tiny t"
+    # fp32: ATen's own fp64 tanh GELU (an independent implementation) where
+    # it does not cancel, and the exact function in the tail
+    g = torch.Generator().manual_seed(3)
+    xf = torch.randn(20000, generator=g) * 3
+    keep = xf > -5
+    got = fn(xf)
+    want = torch.nn.functional.gelu(xf.double(), approximate="tanh")
+    assert torch.allclose(got[keep].double(), want[keep], rtol=1e-6, atol=1e-30), "fp32 vs ATen"
+    import mpmath
+    for v in (-6.0, -8.5, -12.0):
+        t = mpmath.mpf(v)
+        u = mpmath.sqrt(2 / mpmath.pi) * (t + mpmath.mpf("0.044715") * t ** 3)
+        ex = torch.tensor(float(t / (1 + mpmath.exp(-2 * u))), dtype=torch.float64).float()
+        r = fn(torch.tensor([v]))[0]
+        assert abs(r - ex) <= 1e-6 * abs(ex) and torch.signbit(r) == torch.signbit(ex), \
+            f"fp32 tail gelu({v}) {r.item()} vs {ex.item()}"
+
+
+def check_transpose(fn):
+    g = torch.Generator().manual_seed(5)
+    for shape, dtype in (((2, 3, 5, 7), BF), ((4, 49, 128), BF), ((3, 1, 9), torch.float32),
+                         ((1, 64, 65), torch.int16), ((6, 6), torch.float32)):
+        if dtype == torch.int16:
+            x = torch.randint(-32768, 32767, shape, generator=g, dtype=torch.int16)
+        else:
+            x = torch.randn(shape, generator=g).to(dtype)
+        got = fn(x)
+        want = x.transpose(-2, -1).contiguous()
+        assert got.shape == want.shape and got.is_contiguous(), f"{shape} layout"
+        assert torch.equal(got.view(torch.uint8) if got.element_size() == 1 else got, want), \
+            f"{shape} values"
+    # bit patterns move untouched: NaN payloads and -0 included
+    bits = torch.tensor([[0x7FC1, 0xFFFF], [0x8000, 0x7F81]], dtype=torch.int32).to(torch.int16)
+    got = fn(bits.view(BF)).view(torch.int16)
+    assert torch.equal(got, bits.t().contiguous()), "bit-exact"
+
+
+def check_row_mean_bf16(fn):
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(9, 169, generator=g).to(BF)
+    for relu in (False, True):
+        got = fn(x, relu=relu)
+        rows = x.double().clamp_min(0) if relu else x.double()
+        want = [bf16_round(math.fsum(r) / 169) for r in rows.tolist()]
+        assert got.float().tolist() == want, f"brute force relu={relu}"
+    assert torch.equal(fn(torch.full((3, 13), 2.5, dtype=BF)).float(), torch.full((3,), 2.5))
+    assert torch.equal(fn(torch.full((2, 7), -1.0, dtype=BF), relu=True).float(), torch.zeros(2))
+    nan_row = torch.tensor([[1.0, float("nan"), -3.0]]).to(BF)
+    assert torch.isnan(fn(nan_row, relu=True)).all(), "ReLU keeps NaN"
+    mixed = torch.tensor([[4.0, -2.0, 1.0, -7.0]]).to(BF)
+    assert fn(mixed, relu=True).item() == 1.25 and fn(mixed).item() == -1.0, "mean(relu(x))"
+
+
 CHECKS = {
     "row_mean": (check_row_mean, ref.row_mean),
     "bias_gelu": (check_bias_gelu, ref.bias_gelu_nchw_to_nhwc),
@@ -310,6 +394,9 @@ CHECKS = {
     "rmsnorm_ex": (check_rmsnorm_ex, ref.rmsnorm_ex),
     "bn_nhwc": (check_bn_nhwc, ref.batchnorm_nhwc_act_pad),
     "bn_nchw": (check_bn_nchw, ref.batchnorm_nchw_act_mean),
+    "gelu_flat": (check_gelu_flat, ref.gelu_tanh),
+    "transpose": (check_transpose, ref.transpose_last2),
+    "row_mean_bf16": (check_row_mean_bf16, ref.row_mean_bf16),
 }
 
 
@@ -401,7 +488,39 @@ def _bn_nchw_mean_before_relu(x, *a, act=None, **k):
     return ref.batchnorm_nchw_act_mean(x, *a, act=None, **k)
 
 
+def _gelu_erf_form(x):
+    return torch.nn.functional.gelu(x.double()).to(x.dtype)
+
+
+def _gelu_no_cubic(x):
+    return (0.5 * x.double() * (1 + torch.tanh(0.7978845608028654 * x.double()))).to(x.dtype)
+
+
+def _transpose_leading_dims(x):
+    return ref.transpose_last2(x.transpose(0, 1).contiguous()) if x.dim() > 2 else \
+        ref.transpose_last2(x).t().contiguous()
+
+
+def _transpose_reshape_only(x):
+    return x.reshape(*x.shape[:-2], x.shape[-1], x.shape[-2]).clone()
+
+
+def _row_mean_relu_after(x, *, relu=False):
+    m = ref.row_mean_bf16(x)
+    return m.clamp_min(0) if relu else m
+
+
+def _row_mean_wrong_divisor(x, *, relu=False):
+    return (ref.row_mean_bf16(x, relu=relu).double() * x.shape[1] / (x.shape[1] - 1)).to(BF)
+
+
 MUTANTS = [
+    ("gelu_flat", _gelu_erf_form),
+    ("gelu_flat", _gelu_no_cubic),
+    ("transpose", _transpose_leading_dims),
+    ("transpose", _transpose_reshape_only),
+    ("row_mean_bf16", _row_mean_relu_after),
+    ("row_mean_bf16", _row_mean_wrong_divisor),
     ("spatial_mean", _spatial_mean_wrong_divisor),
     ("bias_softmax", _bias_softmax_groups_reversed),
     ("rmsnorm_ex", _rmsnorm_ex_t5_order_dropped),
@@ -475,6 +594,20 @@ def test_oracle_matches_family_repros():
     x, bias = torch.randn(8, 5, 12, generator=g).to(BF), torch.randn(2, 1, 5, 12, generator=g).to(BF)
     want = get_repro_instance(CANONICAL / "amax_sum_20ccc18dda60")(x, bias, [2, 4, 5, 12], [8, 5, 12])
     assert close(ref.scaled_bias_softmax(x, bias.view(2, 5, 12), 1.0, 4), want, 1.6e-2)
+    # decomposed GELU: eager rounds each op to bf16 (the reference harness's
+    # allclose 1e-2 holds); in fp32 eager and the oracle agree to fp32 error
+    x = (3 * torch.randn(6, 64, generator=g)).to(BF)
+    gelu_repro = get_repro_instance(CANONICAL / "pointwise_2d969ac9ad59")
+    assert close(ref.gelu_tanh(x), gelu_repro(x, [2, 3, 64], [6, 64]), 1e-2)
+    xf = 3 * torch.randn(6, 64, generator=g)
+    assert torch.allclose(ref.gelu_tanh(xf), gelu_repro(xf, [2, 3, 64], [-1, 64]),
+                          rtol=1e-5, atol=1e-6)
+    x = torch.randn(2, 3, 4, 8, generator=g).to(BF)
+    want = get_repro_instance(CANONICAL / "pointwise_021e90d9c17d")(x, [2, 24, 2, 2])
+    assert torch.equal(ref.transpose_last2(x).view(2, 24, 2, 2), want)
+    x = torch.randn(2, 5, 3, 3, generator=g).to(BF)
+    want = get_repro_instance(CANONICAL / "mean_b402ee209d0b")(x, [2, 5])
+    assert close(ref.row_mean_bf16(x.reshape(10, 9), relu=True).view(2, 5), want, 1.6e-2)
     for rid, fmt, call in (
             ("var_mean_ceb5c315290a", torch.channels_last,
              lambda x, rm, rv, w, b: ref.batchnorm_nhwc_act_pad(
