@@ -259,16 +259,12 @@ __global__ __launch_bounds__(256) void bn_nhwc_apply_pad_scalar(
 }
 
 // ---------------------------------------------------------------------------
-// NCHW with a small spatial extent: a workgroup of kNchwImages waves covers
-// a block of 64 channels (lane = channel) of kNchwImages consecutive images
-// (wave = image).  When the slab of an (image, channel block) is 16-byte
-// aligned and fits (STAGED), each wave copies it to LDS with 16-byte loads
-// and the lanes read their channel's HW values from there; otherwise the
-// lanes read them from memory directly.
+// NCHW, general shapes: a workgroup of kNchwImages waves covers a block of
+// 64 channels (lane = channel) of kNchwImages consecutive images (wave =
+// image); each lane reads its channel's HW values from memory.
 // ---------------------------------------------------------------------------
 constexpr int kNchwImages = 4;
 constexpr int kNchwChannels = 64;
-constexpr int64_t kNchwMaxStagedHw = 80;  // LDS: 4 x 64 x 80 x 2 B + 6 KiB < 48 KiB
 
 // What the NCHW epilogue pass needs to merge its channels' slice statistics
 // itself (the statistics pass wrote (mean, M2) per (channel, slice of
@@ -283,27 +279,6 @@ struct NchwMerge {
   float momentum, eps, var_scale;
 };
 
-template <bool STAGED, bool LAST_USE>
-__device__ __forceinline__ const uint16_t* nchw_stage(const uint16_t* __restrict__ x,
-                                                      uint16_t* lds_wave, int64_t img,
-                                                      int64_t C, int64_t c0, int64_t HW,
-                                                      bool img_valid, int lane) {
-  const uint16_t* seg = x + (img * C + c0) * HW;
-  if constexpr (STAGED) {
-    const int64_t len = std::min<int64_t>(kNchwChannels, C - c0) * HW;  // multiple of 8
-    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(seg);
-    u32x4_t* dst = reinterpret_cast<u32x4_t*>(lds_wave);
-    if (img_valid) {
-      for (int64_t i = lane; i < len / 8; i += kWave)
-        dst[i] = LAST_USE ? __builtin_nontemporal_load(src + i) : src[i];
-    }
-    __syncthreads();
-    return lds_wave;
-  } else {
-    return seg;
-  }
-}
-
 // MODE 0: per (channel, slice of kNchwImages images) partial (mean, M2),
 //         exact two-pass statistics of each (image, channel) segment merged
 //         over the images in order.
@@ -312,12 +287,11 @@ __device__ __forceinline__ const uint16_t* nchw_stage(const uint16_t* __restrict
 //         waves added in order: the same result in every workgroup; the
 //         workgroups of the first image group write save_* and the running
 //         statistics), then out[n, c] = bf16(sum_hw act(bn(x[n, c, hw])) / HW).
-template <int MODE, bool STAGED>
+template <int MODE>
 __global__ __launch_bounds__(kNchwImages * kWave) void bn_nchw_small_hw(
     const uint16_t* __restrict__ x, float2* __restrict__ part, NchwMerge mg,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     uint16_t* __restrict__ out, int64_t N, int64_t C, int64_t HW, int act) {
-  extern __shared__ __align__(16) uint16_t slab[];  // [kNchwImages][64 * HW] when STAGED
   __shared__ float2 stats[kNchwImages][kNchwChannels];
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x >> 6;
@@ -326,9 +300,7 @@ __global__ __launch_bounds__(kNchwImages * kWave) void bn_nchw_small_hw(
   const int64_t c = c0 + lane;
   const bool img_valid = img < N;
   const bool valid = img_valid && c < C;
-  const uint16_t* base = nchw_stage<STAGED, MODE == 1>(x, slab + w * kNchwChannels * HW,
-                                            img_valid ? img : 0, C, c0, HW, img_valid, lane);
-  const uint16_t* seg = base + static_cast<int64_t>(lane) * HW;
+  const uint16_t* seg = x + ((img_valid ? img : 0) * C + c0 + lane) * HW;
   if constexpr (MODE == 0) {
     float mu = 0.f, m2 = 0.f;
     if (valid) {
@@ -395,6 +367,180 @@ __global__ __launch_bounds__(kNchwImages * kWave) void bn_nchw_small_hw(
     float sum = 0.f;
     for (int64_t j = 0; j < HW; ++j) sum += bn_act(bf16_to_f32(seg[j]), mc, rc, gc, bc, act);
     out[img * C + c] = static_cast<uint16_t>(pack_bf16x2(sum / static_cast<float>(HW), 0.f) & 0xffffu);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// NCHW with small planes (C % 8 == 0, HW <= kPlanesMaxHw, x 16-byte
+// aligned): a wave covers 8 consecutive channels of the kNchwImages images
+// of one slice -- per image, 8 consecutive H x W planes: 16 * HW bytes, a
+// whole number of 16-byte vectors whatever HW is.  The wave issues all its
+// non-temporal 16-byte loads at once, stages the planes in LDS, and reduces
+// each plane over 8 lanes (lane 8r + k takes elements k, k + 8, ... of plane
+// r) with a fixed butterfly.  A workgroup holds kPlaneWaves such waves: 32
+// channels of one slice.
+// MODE 0: each plane's exact two-pass (mean, M2), merged over the slice's
+//   images in order -> part[c * slices + s] (the layout of the general path).
+// MODE 1: the channel's slices merged in fp64 about the shift m_0 (8 lanes,
+//   a fixed order: the same in every wave; the waves of slice 0 write save_*
+//   and the running statistics) while the loads are in flight, then
+//   out[n, c] = bf16(sum_hw act(bn(x)) / HW).
+// ---------------------------------------------------------------------------
+constexpr int kPlaneWaves = 4;
+constexpr int kPlaneChannels = 8;  // per wave
+constexpr int kPlanesMaxHw = 128;
+
+// HWB: plane-size bucket (8, 16, 32, 64 or 128 >= HW): each lane holds
+// HWB / 8 values of a plane, and a wave loads at most 4 * HWB / 64 vectors
+// per lane, so both loops have fixed trip counts and their loads issue
+// together.
+template <int MODE, int HWB>
+__global__ __launch_bounds__(kPlaneWaves * kWave) void bn_nchw_planes(
+    const uint16_t* __restrict__ x, float2* __restrict__ part, NchwMerge mg,
+    const float* __restrict__ gamma, const float* __restrict__ beta,
+    uint16_t* __restrict__ out, int64_t N, int64_t C, int HW, DivMagic by_hw, int act) {
+  constexpr int kVec = (kNchwImages * HWB + kWave - 1) / kWave;  // vectors per lane
+  constexpr int kVals = HWB / 8;                                  // plane values per lane
+  __shared__ __align__(16) uint16_t stage[kPlaneWaves][kNchwImages * kPlaneChannels * HWB];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x >> 6;
+  const int r = lane >> 3;
+  const int k = lane & 7;
+  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * kPlaneWaves + w) * kPlaneChannels;
+  const bool wave_ok = c0 < C;  // wave-uniform; C % 8 == 0, so all 8 channels exist
+  const int64_t s = blockIdx.y;
+  const int64_t n0 = s * kNchwImages;
+  const int imgs = static_cast<int>(N - n0 < kNchwImages ? N - n0 : kNchwImages);
+  const int64_t c = c0 + r;
+  u32x4_t* lds = reinterpret_cast<u32x4_t*>(stage[w]);
+
+  // The slice's planes of these 8 channels: image im's block of 8 planes is
+  // HW vectors at ((n0 + im) * C + c0) * HW elements; in LDS the blocks sit
+  // back to back, vector i of the wave at lds[i].
+  // Loads without a branch: slots past the end reload the last vector, and
+  // a wave past the last channel block reads the last block (it stores
+  // nothing), so all loads are in flight before the first is used.  The
+  // epilogue's slice partials, gamma and beta are loaded first, so the merge
+  // waits for them alone while x is in flight.
+  const int nvec = imgs * HW;
+  const int64_t cl = wave_ok ? c0 : C - kPlaneChannels;
+  constexpr int kPre = 4;  // slice partials per lane loaded up front
+  float2 pre[kPre], first;
+  float gc = 0.f, bc = 0.f;
+  const float2* pc = nullptr;
+  if constexpr (MODE == 1) {
+    pc = mg.part + (cl + r) * mg.slices;
+    first = pc[0];
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      const int64_t t = k + 8 * u;
+      pre[u] = pc[t < mg.slices ? t : 0];
+    }
+    gc = gamma[cl + r];
+    bc = beta[cl + r];
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of x's
+  }
+  const uint16_t* xb = x + (n0 * C + cl) * static_cast<int64_t>(HW);
+  u32x4_t v[kVec];
+#pragma unroll
+  for (int q = 0; q < kVec; ++q) {
+    const int i0 = lane + q * kWave;
+    const int i = i0 < nvec ? i0 : nvec - 1;
+    const int im = static_cast<int>(div_by(static_cast<uint32_t>(i), by_hw));
+    const int64_t off = static_cast<int64_t>(im) * C * HW + static_cast<int64_t>(i - im * HW) * 8;
+    v[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(xb + off));
+  }
+
+  float mc = 0.f, rc = 0.f;
+  if constexpr (MODE == 1) {
+    if (wave_ok) {
+      const double K = static_cast<double>(first.x);
+      double n = 0.0, s1 = 0.0, s2 = 0.0;
+      auto add = [&](int64_t t, float2 pv) {
+        const int64_t hi = (t + 1) * kNchwImages < N ? (t + 1) * kNchwImages : N;
+        const double cnt = static_cast<double>((hi - t * kNchwImages) * HW);
+        const double d = static_cast<double>(pv.x) - K;
+        n += cnt;
+        s1 = __builtin_fma(cnt, d, s1);
+        s2 += __builtin_fma(cnt * d, d, static_cast<double>(pv.y));
+      };
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) {
+        if (k + 8 * u < mg.slices) add(k + 8 * u, pre[u]);
+      }
+      for (int64_t t = k + 8 * kPre; t < mg.slices; t += 8) add(t, pc[t]);
+      n = sum8(n);
+      s1 = sum8(s1);
+      s2 = sum8(s2);
+      const double dm = s1 / n;
+      mc = static_cast<float>(K + dm);
+      const float var_f = static_cast<float>(std::max(0.0, s2 - s1 * dm) / n);
+      rc = 1.0f / __builtin_sqrtf(__fadd_rn(var_f, mg.eps));
+      if (s == 0 && k == 0) {
+        mg.save_mean[c] = mc;
+        mg.save_rstd[c] = rc;
+        const float keep = 1.0f - mg.momentum;
+        mg.running_mean[c] =
+            __fadd_rn(__fmul_rn(mc, mg.momentum), __fmul_rn(mg.running_mean[c], keep));
+        mg.running_var[c] = __fadd_rn(__fmul_rn(__fmul_rn(var_f, mg.var_scale), mg.momentum),
+                                      __fmul_rn(mg.running_var[c], keep));
+      }
+    }
+  }
+
+#pragma unroll
+  for (int q = 0; q < kVec; ++q) {
+    const int i = lane + q * kWave;
+    if (i < nvec) lds[i] = v[q];
+  }
+  __syncthreads();
+  if (!wave_ok) return;  // wave-uniform, after the only barrier
+
+  // Lane 8r + k's values of plane r of every image: elements k + 8t, read
+  // all at once (indices clamped into the plane, values past its end unused).
+  const uint16_t* planes = stage[w];
+  float val[kNchwImages][kVals];
+#pragma unroll
+  for (int im = 0; im < kNchwImages; ++im) {
+    const int ic = im < imgs ? im : imgs - 1;
+    const uint16_t* pl = planes + (ic * kPlaneChannels + r) * HW;
+#pragma unroll
+    for (int t = 0; t < kVals; ++t) {
+      const int j = k + 8 * t;
+      val[im][t] = bf16_to_f32(pl[j < HW ? j : HW - 1]);
+    }
+  }
+  if constexpr (MODE == 0) {
+    float cnt = 0.f, mean = 0.f, m2 = 0.f;
+#pragma unroll
+    for (int im = 0; im < kNchwImages; ++im) {
+      if (im >= imgs) break;  // wave-uniform
+      float sum = 0.f;
+#pragma unroll
+      for (int t = 0; t < kVals; ++t) sum += k + 8 * t < HW ? val[im][t] : 0.f;
+      const float mu = sum8(sum) / static_cast<float>(HW);
+      float q2 = 0.f;
+#pragma unroll
+      for (int t = 0; t < kVals; ++t) {
+        const float d = val[im][t] - mu;
+        q2 = k + 8 * t < HW ? __builtin_fmaf(d, d, q2) : q2;
+      }
+      chan_merge(cnt, mean, m2, static_cast<float>(HW), mu, sum8(q2));
+    }
+    if (k == 0) part[c * static_cast<int64_t>(gridDim.y) + s] = make_float2(mean, m2);
+  } else {
+#pragma unroll
+    for (int im = 0; im < kNchwImages; ++im) {
+      if (im >= imgs) break;  // wave-uniform
+      float sum = 0.f;
+#pragma unroll
+      for (int t = 0; t < kVals; ++t)
+        sum += k + 8 * t < HW ? bn_act(val[im][t], mc, rc, gc, bc, act) : 0.f;
+      sum = sum8(sum);
+      if (k == 0)
+        out[(n0 + im) * C + c] =
+            static_cast<uint16_t>(pack_bf16x2(sum / static_cast<float>(HW), 0.f) & 0xffffu);
+    }
   }
 }
 
@@ -619,24 +765,42 @@ extern "C" int hipo_batchnorm_nchw_act_mean_bf16(
                need);
   HIPO_REQUIRE(slices <= 65535, "%s: too many images", what);
   float2* part = static_cast<float2*>(workspace);
-  const bool staged = c % 8 == 0 && hw <= kNchwMaxStagedHw && aligned16(x);
-  const dim3 grid(static_cast<unsigned>((c + kNchwChannels - 1) / kNchwChannels),
-                  static_cast<unsigned>(slices));
-  const dim3 block(kNchwImages * kWave);
-  const size_t lds = staged ? static_cast<size_t>(kNchwImages * kNchwChannels * hw) * 2 : 0;
   const NchwMerge none{};
   const NchwMerge mg{part, slices, running_mean, running_var, save_mean, save_rstd,
                      momentum, eps, var_scale};
-  if (staged) {
-    bn_nchw_small_hw<0, true><<<grid, block, lds, stream>>>(x, part, none, nullptr, nullptr,
-                                                            nullptr, n, c, hw, act);
-    bn_nchw_small_hw<1, true><<<grid, block, lds, stream>>>(x, nullptr, mg, gamma, beta, out,
-                                                            n, c, hw, act);
+  if (c % kPlaneChannels == 0 && hw <= kPlanesMaxHw && aligned16(x)) {
+    const int64_t cb = (c + kPlaneWaves * kPlaneChannels - 1) / (kPlaneWaves * kPlaneChannels);
+    const dim3 grid(static_cast<unsigned>(cb), static_cast<unsigned>(slices));
+    const dim3 block(kPlaneWaves * kWave);
+    const int h = static_cast<int>(hw);
+    const DivMagic by_hw = div_magic(static_cast<uint32_t>(hw));
+#define HIPO_PLANES(B_)                                                                      \
+  do {                                                                                       \
+    bn_nchw_planes<0, B_><<<grid, block, 0, stream>>>(x, part, none, nullptr, nullptr,        \
+                                                      nullptr, n, c, h, by_hw, act);         \
+    bn_nchw_planes<1, B_><<<grid, block, 0, stream>>>(x, nullptr, mg, gamma, beta, out, n, c, \
+                                                      h, by_hw, act);                        \
+  } while (0)
+    if (hw <= 8) {
+      HIPO_PLANES(8);
+    } else if (hw <= 16) {
+      HIPO_PLANES(16);
+    } else if (hw <= 32) {
+      HIPO_PLANES(32);
+    } else if (hw <= 64) {
+      HIPO_PLANES(64);
+    } else {
+      HIPO_PLANES(128);
+    }
+#undef HIPO_PLANES
   } else {
-    bn_nchw_small_hw<0, false><<<grid, block, 0, stream>>>(x, part, none, nullptr, nullptr,
-                                                           nullptr, n, c, hw, act);
-    bn_nchw_small_hw<1, false><<<grid, block, 0, stream>>>(x, nullptr, mg, gamma, beta, out,
-                                                           n, c, hw, act);
+    const dim3 grid(static_cast<unsigned>((c + kNchwChannels - 1) / kNchwChannels),
+                    static_cast<unsigned>(slices));
+    const dim3 block(kNchwImages * kWave);
+    bn_nchw_small_hw<0><<<grid, block, 0, stream>>>(x, part, none, nullptr, nullptr, nullptr,
+                                                    n, c, hw, act);
+    bn_nchw_small_hw<1><<<grid, block, 0, stream>>>(x, nullptr, mg, gamma, beta, out, n, c, hw,
+                                                    act);
   }
   return check_launch(what);
 }

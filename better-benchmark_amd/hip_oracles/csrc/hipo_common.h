@@ -110,10 +110,36 @@ constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
 constexpr int kDppRowRor4 = 0x124;  // row_ror:4
 constexpr int kDppRowRor8 = 0x128;  // row_ror:8
 
+constexpr int kDppRowHalfMirror = 0x141;  // row_half_mirror: lane i of 8 <- lane 7 - i
+
 template <int Ctrl>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(
       0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+
+template <int Ctrl>
+__device__ __forceinline__ double dpp(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(b)), Ctrl, 0xF, 0xF,
+                                  false));
+  const uint32_t hi = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(b >> 32)), Ctrl,
+                                  0xF, 0xF, false));
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Sum over each aligned group of 8 lanes, every lane of the group receiving
+// it (quad butterflies, then the mirrored half-row); all 64 lanes active.
+// Every lane adds the same two values at each step (a + b = b + a), so the
+// 8 results are identical.
+template <typename T>
+__device__ __forceinline__ T sum8(T v) {
+  v += dpp<kDppQuadXor1>(v);
+  v += dpp<kDppQuadXor2>(v);
+  v += dpp<kDppRowHalfMirror>(v);
+  return v;
 }
 
 // Full-wave sum; every lane receives the same value.  All 64 lanes must be

@@ -106,8 +106,7 @@ __device__ __forceinline__ void row_store_stream(uint16_t* row, int64_t col,
 // (DPP quad swaps, half-row and row mirrors, then lane-xor shuffles across
 // 16-lane rows); every lane of a segment receives the same value, and the
 // order of the additions is fixed.  All 64 lanes must be active.
-constexpr int kDppRowMirror = 0x140;      // lane i <- 15 - i within a row
-constexpr int kDppRowHalfMirror = 0x141;  // lane i <- 7 - i within a half-row
+constexpr int kDppRowMirror = 0x140;  // lane i <- 15 - i within a row
 
 template <int L>
 __device__ __forceinline__ float seg_sum(float v) {

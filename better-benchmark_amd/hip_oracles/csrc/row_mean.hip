@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void row_mean_f32_scalar(
 // vector loads (the SqueezeNet rows are 169 elements, 338 bytes, not
 // vector-aligned one by one).  The wave stages its 8 rows in LDS; then 8
 // lanes per row sum every 8th element in order and combine in a fixed
-// butterfly.  Longer rows: one wave per row.
+// DPP butterfly.  Longer rows: one wave per row.
 constexpr int kBf16RowsPerWave = 8;
 constexpr int kBf16ShortCols = 512;
 constexpr int kBf16Waves = 4;
@@ -125,16 +125,20 @@ __global__ __launch_bounds__(kBf16Waves * kWave) void row_mean_bf16_short(
     const int64_t elems = nrows * cols;
     const int whole = static_cast<int>(elems / 8);
     const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x + row0 * cols);
-    u32x4_t v[VPL];
+    if (whole > 0) {  // wave-uniform
+      // Loads without a branch (slots past the end reload the last vector),
+      // so all of them are in flight before the first is used.
+      u32x4_t v[VPL];
 #pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const int i = lane + k * kWave;
-      if (i < whole) v[k] = __builtin_nontemporal_load(xv + i);
-    }
+      for (int k = 0; k < VPL; ++k) {
+        const int i = lane + k * kWave;
+        v[k] = __builtin_nontemporal_load(xv + (i < whole ? i : whole - 1));
+      }
 #pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const int i = lane + k * kWave;
-      if (i < whole) reinterpret_cast<u32x4_t*>(lds)[i] = v[k];
+      for (int k = 0; k < VPL; ++k) {
+        const int i = lane + k * kWave;
+        if (i < whole) reinterpret_cast<u32x4_t*>(lds)[i] = v[k];
+      }
     }
     const int rest = static_cast<int>(elems - int64_t{whole} * 8);
     if (lane < rest) lds[whole * 8 + lane] = x[row0 * cols + whole * 8 + lane];
@@ -148,9 +152,7 @@ __global__ __launch_bounds__(kBf16Waves * kWave) void row_mean_bf16_short(
     const uint16_t* p = lds + r * cols;
     for (int j = k; j < cols; j += 8) s += act_relu<RELU>(bf16_to_f32(p[j]));
   }
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  s += __shfl_xor(s, 4);
+  s = sum8(s);
   if (k == 0 && r < nrows) out[row0 + r] = round_to_bf16(s / static_cast<float>(cols));
 }
 

@@ -48,7 +48,9 @@ __device__ __forceinline__ T word_elem(const u32x4_t& v, int j) {
   }
 }
 
-template <typename T, bool VEC>
+// U: 16-byte input vectors per thread (VEC), the smallest power of two that
+// covers the workgroup's run; 0 for the element path.
+template <typename T, int U>
 __global__ __launch_bounds__(kTrThreads) void transpose_whole(const T* __restrict__ x,
                                                               T* __restrict__ y, WholeGeom g) {
   extern __shared__ __align__(16) u32x4_t slots[];
@@ -60,32 +62,35 @@ __global__ __launch_bounds__(kTrThreads) void transpose_whole(const T* __restric
   const T* xb = x + b0 * g.M;
   T* yb = y + b0 * g.M;
 
-  if constexpr (VEC) {
+  if constexpr (U > 0) {
     const int nvec = elems / V;
     const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(xb);
-    u32x4_t v[kTrMaxVecPerThread];
+    // Straight-line code: every load is issued before the first is used.
+    // Slots past the end take the last vector again and write the same
+    // values to the same LDS places as its owner (no branch, no race: the
+    // bits are identical).
+    u32x4_t v[U];
 #pragma unroll
-    for (int k = 0; k < kTrMaxVecPerThread; ++k) {
+    for (int k = 0; k < U; ++k) {
       const int iv = static_cast<int>(threadIdx.x) + k * kTrThreads;
-      if (iv < nvec) v[k] = __builtin_nontemporal_load(xv + iv);
+      v[k] = __builtin_nontemporal_load(xv + (iv < nvec ? iv : nvec - 1));
     }
 #pragma unroll
-    for (int k = 0; k < kTrMaxVecPerThread; ++k) {
-      const int iv = static_cast<int>(threadIdx.x) + k * kTrThreads;
-      if (iv >= nvec) break;
-      // Input vector iv: matrix gi, row r, columns c0 .. c0 + V - 1 (one row).
+    for (int k = 0; k < U; ++k) {
+      const int iv0 = static_cast<int>(threadIdx.x) + k * kTrThreads;
+      const int iv = iv0 < nvec ? iv0 : nvec - 1;
+      // Input vector iv: matrix gi, row r, columns c0 .. c0 + V - 1 (one row);
+      // output rows row0 .. row0 + V - 1 of the block, all in one pad group
+      // (row0 is a multiple of V).
       const uint32_t f = static_cast<uint32_t>(iv) * V;
       const uint32_t gi = div_by(f, g.by_m);
       const uint32_t rem = f - gi * static_cast<uint32_t>(g.M);
       const uint32_t r = div_by(rem, g.by_c);
       const uint32_t c0 = rem - r * static_cast<uint32_t>(g.C);
-      const uint32_t row0 = gi * static_cast<uint32_t>(g.C) + c0;  // output row in the block
+      const uint32_t row0 = gi * static_cast<uint32_t>(g.C) + c0;
+      const uint32_t e0 = row0 * static_cast<uint32_t>(g.R) + r + (g.pad ? row0 : 0u);
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        const uint32_t fo = (row0 + j) * static_cast<uint32_t>(g.R) + r;
-        const uint32_t pad = g.pad ? (row0 + j) / V : 0u;  // V is a power of two
-        lds[fo + pad * V] = word_elem<T>(v[k], j);
-      }
+      for (int j = 0; j < V; ++j) lds[e0 + j * static_cast<uint32_t>(g.R)] = word_elem<T>(v[k], j);
     }
     __syncthreads();
     const int nslots = elems / V;
@@ -170,10 +175,17 @@ int launch_transpose(const void* xp, void* yp, int64_t batch, int64_t R, int64_t
     const int64_t blocks = (batch + G - 1) / G;
     HIPO_REQUIRE(blocks < (int64_t{1} << 31), "transpose: too many matrices");
     const dim3 grid(static_cast<unsigned>(blocks)), block(kTrThreads);
-    if (vec) {
-      transpose_whole<T, true><<<grid, block, lds_bytes, stream>>>(x, y, g);
+    const int64_t per_thread = (slots_used + kTrThreads - 1) / kTrThreads;
+    if (!vec) {
+      transpose_whole<T, 0><<<grid, block, lds_bytes, stream>>>(x, y, g);
+    } else if (per_thread <= 1) {
+      transpose_whole<T, 1><<<grid, block, lds_bytes, stream>>>(x, y, g);
+    } else if (per_thread <= 2) {
+      transpose_whole<T, 2><<<grid, block, lds_bytes, stream>>>(x, y, g);
+    } else if (per_thread <= 4) {
+      transpose_whole<T, 4><<<grid, block, lds_bytes, stream>>>(x, y, g);
     } else {
-      transpose_whole<T, false><<<grid, block, lds_bytes, stream>>>(x, y, g);
+      transpose_whole<T, kTrMaxVecPerThread><<<grid, block, lds_bytes, stream>>>(x, y, g);
     }
   } else {
     const int64_t r_tiles = (R + kTile - 1) / kTile;

@@ -776,7 +776,8 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
                  numerics_optout: dict | None = None, disable_gpu_lock: bool = False,
                  compare_compile: bool = True, coordinate_descent: bool = True,
                  flush_bytes: int = DEFAULT_FLUSH_BYTES,
-                 cpu_eager: bool = False, hardware: str | None = None) -> dict:
+                 cpu_eager: bool = False, flat_copy_ceiling: bool = False,
+                 hardware: str | None = None) -> dict:
     """Time one oracle point on the GPU (reference :1057-1287, ROCm path).
 
     Steps: resolve dispatch; torch.compile comparator (Inductor, coordinate
@@ -795,7 +796,11 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
     peak after a read flush (`clean_cache_*`: the Infinity Cache is clean then
     and can absorb part of the writes, so these flatter write-heavy kernels).
     A fault recorded by a kernel (hip_oracles.device_faults) gives
-    ORACLE_DEVICE_FAULT.
+    ORACLE_DEVICE_FAULT.  With `flat_copy_ceiling`, a flat stream copy of
+    the point's read and write bytes (hip_oracles.flat_copy: the oracle
+    kernels' access style) is timed the same two ways, and `vs_flat_copy`
+    (copy time / oracle time, direct launches) says how close the oracle
+    runs to what the memory system delivers for that many bytes.
     """
     from byte_accounting import HBM_PEAK_BYTES_PER_S, achieved_gbps, sol_fraction
     dispatch_info = None
@@ -987,8 +992,42 @@ def bench_oracle(oracle_forward, instance, inputs, repro_id: str, *, warmup: int
                                      "annotation": numerics_optout}
     if cpu_eager:
         result.update(time_cpu_eager(instance, inputs))
+    if flat_copy_ceiling and nbytes:
+        with _gpu_exclusive_lock(repro_id, disabled=disable_gpu_lock):
+            ceiling = _flat_copy_ceiling(inputs, nbytes, device, warmup, rep, flush)
+        result.update(ceiling)
+        if best_launch > 0:
+            result["vs_flat_copy"] = round(ceiling["flat_copy_launch_us"] / best_launch, 3)
     print(json.dumps(with_dispatch(result, full=True), default=str))
     return result
+
+
+def _flat_copy_ceiling(inputs, nbytes, device, warmup, rep, flush) -> dict:
+    """hipo_flat_copy moving the point's bytes -- every input tensor's bytes
+    read, the rest of the effective bytes written, each rounded to 1 KiB --
+    timed as the oracle is: direct launches and graph replays, a cache flush
+    before each, min over `rep`."""
+    import hip_oracles
+    seen, rd = set(), 0
+    for t in inputs:
+        if isinstance(t, torch.Tensor) and id(t) not in seen:
+            seen.add(id(t))
+            rd += t.numel() * t.element_size()
+    wr = max(nbytes - rd, 0)
+    rb = max(1024, int(round(rd / 1024)) * 1024)
+    wb = max(1024, int(round(wr / 1024)) * 1024)
+    src = torch.ones(rb // 4, dtype=torch.float32, device=device)
+    dst = torch.empty(wb // 4, dtype=torch.float32, device=device)
+
+    def copy():
+        hip_oracles.flat_copy(src, dst)
+
+    launch_us, _ = _time_launches(copy, warmup, rep, flush=flush)
+    g, _warns = _capture_graph_checked(copy)
+    graph_us, _ = _time_graph(g, warmup, rep, flush=flush)
+    del g, src, dst
+    return {"flat_copy_read_bytes": rb, "flat_copy_write_bytes": wb,
+            "flat_copy_launch_us": round(launch_us, 2), "flat_copy_us": round(graph_us, 2)}
 
 
 def _bench_oracle_cpu(oracle_forward, instance, inputs, repro_id, *, warmup, rep):
@@ -1402,6 +1441,8 @@ def _runner_main(argv=None):
                     help="skip the torch.compile comparator (status ORACLE_ONLY)")
     ap.add_argument("--cpu-eager", action="store_true",
                     help="also time the eager repro on the host CPU")
+    ap.add_argument("--flat-copy", action="store_true",
+                    help="also time a flat copy of the point's bytes (vs_flat_copy)")
     ap.add_argument("--device", default=None,
                     help="override the input device for --check (e.g. cpu)")
     args = ap.parse_args(argv)
@@ -1428,7 +1469,8 @@ def _runner_main(argv=None):
         chk = out.get("check", {})
         kw = dict(warmup=args.warmup, rep=args.rep, numerics_optout=optout,
                   disable_gpu_lock=args.disable_gpu_lock,
-                  compare_compile=not args.no_compile, cpu_eager=args.cpu_eager)
+                  compare_compile=not args.no_compile, cpu_eager=args.cpu_eager,
+                  flat_copy_ceiling=args.flat_copy)
         results = []
         items = list(configs.items()) or [("default", None)]
         for label, cfg in items:

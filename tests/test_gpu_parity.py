@@ -873,7 +873,7 @@ def test_batchnorm_nhwc_act_pad(n, c, h, w, pb, pr, act, rocm_device):
 
 BN_NCHW_CASES = [  # n, c, h, w, act
     (5, 72, 7, 7, "relu"), (3, 20, 7, 7, "relu"), (4, 16, 10, 10, "silu"), (2, 64, 1, 1, None),
-    (9, 128, 3, 5, "relu"), (8, 1024, 7, 7, "relu"),
+    (9, 128, 3, 5, "relu"), (8, 1024, 7, 7, "relu"), (2, 16, 12, 12, "relu"),
 ]
 
 
