@@ -36,8 +36,10 @@ enum { kActNone = 0, kActRelu = 1, kActSilu = 2 };
 
 // act(bf16(((x - mean) * rstd) * gamma + beta)), fp32 ops in the eager order
 // (no contraction).  SiLU is t / (1 + exp(-t)) as eager, with the
-// extended-precision exp_f32 and an IEEE division; the caller rounds the
-// result to bf16.
+// extended-precision exp_f32 and an IEEE division; callers round the result
+// to bf16 (eager's activation output) before storing or summing it.  (A
+// correctly rounded bf16 SiLU table staged in LDS, like the GELU kernels',
+// measured 2-5 % slower in the channels-last epilogue.)
 __device__ __forceinline__ float bn_act(float x, float mean, float rstd, float g, float b,
                                         int act) {
   float y = __fmul_rn(__fsub_rn(x, mean), rstd);
@@ -365,7 +367,8 @@ __global__ __launch_bounds__(kNchwImages * kWave) void bn_nchw_small_hw(
     if (!valid) return;
     const float gc = gamma[c], bc = beta[c];
     float sum = 0.f;
-    for (int64_t j = 0; j < HW; ++j) sum += bn_act(bf16_to_f32(seg[j]), mc, rc, gc, bc, act);
+    for (int64_t j = 0; j < HW; ++j)
+      sum += round_bf16(bn_act(bf16_to_f32(seg[j]), mc, rc, gc, bc, act));
     out[img * C + c] = static_cast<uint16_t>(pack_bf16x2(sum / static_cast<float>(HW), 0.f) & 0xffffu);
   }
 }
@@ -535,7 +538,7 @@ __global__ __launch_bounds__(kPlaneWaves * kWave) void bn_nchw_planes(
       float sum = 0.f;
 #pragma unroll
       for (int t = 0; t < kVals; ++t)
-        sum += k + 8 * t < HW ? bn_act(val[im][t], mc, rc, gc, bc, act) : 0.f;
+        sum += k + 8 * t < HW ? round_bf16(bn_act(val[im][t], mc, rc, gc, bc, act)) : 0.f;
       sum = sum8(sum);
       if (k == 0)
         out[(n0 + im) * C + c] =

@@ -129,11 +129,10 @@ __global__ __launch_bounds__(kBlockThreads) void bias_gelu_nchw_to_nhwc_tiles(
         const float x0 = (i & 1) ? bf16hi(w0) : bf16lo(w0);
         const float x1 = (i & 1) ? bf16hi(w1) : bf16lo(w1);
         tt[k] = pack_bf16x2(x0 + b[2 * k], x1 + b[2 * k + 1]);
-        o[k] = gelu_bits_common(tt[k] & 0xffffu, lut) |
-               (gelu_bits_common(tt[k] >> 16, lut) << 16);
-        rare |= gelu_rare(tt[k] & 0xffffu) | gelu_rare(tt[k] >> 16);
+        o[k] = gelu_pair_common(tt[k], lut);
+        rare |= gelu_pair_rare(tt[k]);
       }
-      if (rare) {  // one branch per 8 values, not taken for ordinary data
+      if (rare) {  // one branch per 8 values, rarely taken for ordinary data
 #pragma unroll
         for (int k = 0; k < 4; ++k) o[k] = gelu_bits(tt[k] & 0xffffu, lut) |
                                            (gelu_bits(tt[k] >> 16, lut) << 16);

@@ -22,45 +22,43 @@
 
 namespace hipo {
 
-constexpr uint32_t kGeluLo = static_cast<uint32_t>(kGeluTableExpLo) << 7;      // |t| = 2^-10
-constexpr uint32_t kGeluHi = static_cast<uint32_t>(kGeluTableExpHi + 1) << 7;  // |t| = 16
+constexpr uint32_t kGeluLo = static_cast<uint32_t>(kGeluTableExpLo) << 7;  // |t| = 2^-10
 
 // The table's 16-byte chunks, for staging it into LDS.
 constexpr int kGeluTableChunks = kGeluTableSize * 2 / 16;
 
-// The common inputs (2^-125 <= |t| < 16): the table or t / 2.  Branch-free:
-// the LDS index is clamped into the table, the read is unconditional, and a
-// select picks the result.  `lut` holds kGeluTable.
-__device__ __forceinline__ uint32_t gelu_bits_common(uint32_t tb, const uint16_t* lut) {
-  const uint32_t mag = tb & 0x7fffu;
-  const uint32_t off = mag - kGeluLo;  // wraps below the table
+// The table's inputs (2^-10 <= |t| < 16): a pure lookup.  Branch-free: the
+// LDS index is clamped into the table (inputs outside it read an arbitrary
+// entry, which gelu_rare() flags for replacement).  `lut` holds kGeluTable.
+__device__ __forceinline__ uint32_t gelu_lookup(uint32_t tb, const uint16_t* lut) {
+  const uint32_t off = (tb & 0x7fffu) - kGeluLo;  // wraps below the table
   const uint32_t idx = __builtin_elementwise_min(off, static_cast<uint32_t>(kGeluTablePerSign - 1)) +
                        (tb >> 15) * static_cast<uint32_t>(kGeluTablePerSign);
-  const uint32_t looked = lut[idx];
-  return off < static_cast<uint32_t>(kGeluTablePerSign) ? looked : tb - 0x80u;
+  return lut[idx];
 }
 
-// Inputs gelu_bits_common does not cover: |t| >= 16, inf, NaN, |t| <
-// 2^-125 (zero included).
+// Inputs outside the table: |t| < 2^-10 (zero included), |t| >= 16, inf,
+// NaN -- the same offset test as the lookup's clamp.
 __device__ __forceinline__ bool gelu_rare(uint32_t tb) {
-  return ((tb & 0x7fffu) - 0x100u) >= (kGeluHi - 0x100u);
+  return ((tb & 0x7fffu) - kGeluLo) >= static_cast<uint32_t>(kGeluTablePerSign);
 }
 
 __device__ __forceinline__ uint32_t gelu_bits_rare(uint32_t tb) {
   const uint32_t mag = tb & 0x7fffu;
   if (mag < 0x100u)  // +-0 and subnormal results: t / 2 rounded to nearest even
     return pack_bf16x2(0.5f * bf16_to_f32(static_cast<uint16_t>(tb)), 0.0f) & 0xffffu;
+  if (mag < kGeluLo) return tb - 0x80u;                  // t / 2, an exponent decrement
   if ((tb & 0x8000u) == 0 || mag > 0x7f80u) return tb;  // t >= 16, +inf, NaN
   return mag == 0x7f80u ? 0x7fc0u : 0x8000u;             // -inf -> NaN; t <= -16 -> -0
 }
 
 __device__ __forceinline__ uint32_t gelu_bits(uint32_t tb, const uint16_t* lut) {
-  return gelu_rare(tb) ? gelu_bits_rare(tb) : gelu_bits_common(tb, lut);
+  return gelu_rare(tb) ? gelu_bits_rare(tb) : gelu_lookup(tb, lut);
 }
 
 // Both halves of a word of two bf16 values.
 __device__ __forceinline__ uint32_t gelu_pair_common(uint32_t w, const uint16_t* lut) {
-  return gelu_bits_common(w & 0xffffu, lut) | (gelu_bits_common(w >> 16, lut) << 16);
+  return gelu_lookup(w & 0xffffu, lut) | (gelu_lookup(w >> 16, lut) << 16);
 }
 __device__ __forceinline__ bool gelu_pair_rare(uint32_t w) {
   return gelu_rare(w & 0xffffu) | gelu_rare(w >> 16);

@@ -71,7 +71,7 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_bf16_flat(
       o[k] = gelu_pair_common(v[u][k], lut);
       rare |= gelu_pair_rare(v[u][k]);
     }
-    if (rare) {  // one branch per 8 values, not taken for ordinary data
+    if (rare) {  // one branch per 8 values, rarely taken for ordinary data
 #pragma unroll
       for (int k = 0; k < 4; ++k) o[k] = gelu_pair(v[u][k], lut);
     }
