@@ -39,6 +39,7 @@ from __future__ import annotations
 
 import argparse
 import collections
+import contextlib
 import json
 import math
 import os
@@ -366,10 +367,13 @@ def per_config(want_cpu, steady_steps=64, compare_compile=True, coordinate_desce
         use_compile = compare_compile and elapsed < COMPILE_BUDGET_S
         log(f"config {tag}: bench_oracle (compile comparator: {use_compile}, "
             f"{elapsed:.0f} s elapsed)")
-        r = oh.bench_oracle(fn, oh.get_repro_instance(d), inputs, f"{rid}_{label}",
-                            warmup=10, rep=100, rounds=5, compare_compile=use_compile,
-                            coordinate_descent=coordinate_descent, cpu_eager=want_cpu,
-                            numerics_optout=oh.load_numerics_optout(d))
+        # bench_oracle prints its own JSON record per point (the runner's
+        # output); stdout carries this script's one line only.
+        with contextlib.redirect_stdout(sys.stderr):
+            r = oh.bench_oracle(fn, oh.get_repro_instance(d), inputs, f"{rid}_{label}",
+                                warmup=10, rep=100, rounds=5, compare_compile=use_compile,
+                                coordinate_descent=coordinate_descent, cpu_eager=want_cpu,
+                                numerics_optout=oh.load_numerics_optout(d))
         entry = {"config": tag, "repro": rid, "status": r.get("status"),
                  "bytes": r.get("bytes"), "read_bytes": rd, "write_bytes": wr,
                  "steady_us": ss["device_us_per_step"], "steady_gbps": ss["achieved"],

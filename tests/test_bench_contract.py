@@ -23,7 +23,9 @@ def test_bench_json_line_contract():
                            "--steps", "16", "--warmup", "4"],
                           cwd=ROOT, capture_output=True, text=True, timeout=220)
     assert proc.returncode == 0, proc.stderr[-3000:]
-    line = json.loads(proc.stdout.strip().splitlines()[-1])
+    lines = proc.stdout.strip().splitlines()
+    assert len(lines) == 1, f"stdout must carry one JSON line, got {len(lines)}"
+    line = json.loads(lines[0])
     missing = [k for k in REQUIRED if k not in line]
     assert not missing, missing
     assert line["n_gpus"] == 1 and line["steps"] == 16 and line["warmup"] == 4
