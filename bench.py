@@ -154,14 +154,21 @@ def cpu_baseline(rid, cpu_inputs, nbytes) -> dict:
 STEPS_PER_GRAPH = 64
 
 
-def steady_state(rid, steps, warmup):
-    """Back-to-back steps over rotating input sets (see module docstring)."""
+def steady_state(rid, steps, warmup, point=None):
+    """Back-to-back steps over rotating input sets (see module docstring);
+    `point` picks another shapes.json point of the dir (by shape hash) than
+    the BASELINE one."""
     import torch
     import oracle_harness as oh
-    from repro_harness import make_inputs_from_config
+    from repro_harness import load_shape_configs, make_inputs_from_config
 
     dev = torch.device("cuda:0")
-    label, cfg = _baseline_point(rid)
+    if point is None:
+        label, cfg = _baseline_point(rid)
+    else:
+        label, cfg = next((k, v) for k, v in
+                          load_shape_configs(str(CANONICAL / rid / "repro.py")).items()
+                          if k == point or k.endswith(f"_{point}"))
     _, fn, d = oh._load_oracle_module(CANONICAL / rid)
     instance = oh.get_repro_instance(d)
     oh._seed_input_generation(1)

@@ -189,7 +189,7 @@ def bias_gelu_nchw_to_nhwc(x: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
 def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
     """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) of a contiguous bf16
     or fp32 tensor, same shape: bf16 correctly rounded per element, fp32 as
-    eager's sequence of fp32 operations."""
+    x / (1 + e^(-2u)) to a few ulps."""
     lib = load_library()
     dev = _require_rocm(x)
     _require(x.dtype in (torch.bfloat16, torch.float32), "gelu_tanh: bf16 or fp32 x required")

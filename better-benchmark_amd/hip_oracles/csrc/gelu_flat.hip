@@ -7,16 +7,24 @@
 //   cancels in the negative tail); Inductor and the reference's Triton
 //   oracle evaluate the chain in fp32 and round once -- the exact result is
 //   what both approximate.
-// fp32: eager's own sequence of fp32 operations, each rounded to fp32 and
-//   not contracted into FMAs:
-//     a = x * 0.5;  x3 = (x * x) * x;  b = x3 * 0.044715;  c = x + b;
-//     d = c * 0.7978845608028654;  e = tanh(d) + 1;  y = a * e
-//   with tanh from the device library (what eager and Inductor call).
+// fp32: the same function in its non-cancelling form,
+//     y = x / (1 + e^(-2u)),  u = 0.7978845608028654 (x + 0.044715 x^3)
+//   (0.5 x (1 + tanh u) = x sigmoid(2u), exactly), with the
+//   extended-precision exp_f32 and an IEEE division: a few fp32 ulps from
+//   the exact value everywhere, where eager's and Inductor's 1 + tanh(u)
+//   cancels in the negative tail.  The device library's tanhf (what they
+//   call) costs about twice the instructions, and without packed FP32 math
+//   that made this kernel VALU-bound (65.8 us at the FNet point against
+//   Inductor's 67.6 us graph replay, whose kernel uses packed fp32 ops).
 //
 // Layout: each wave64 moves a contiguous run of U KiB (U 1 KiB sub-chunks,
 // lane l taking the 16-byte vector l of each), loads issued together, four
-// waves per 256-thread workgroup, a one-shot grid in memory order; loads and
-// stores are non-temporal.  Elements past the last whole 16-byte vector are
+// waves per 256-thread workgroup, a one-shot grid in memory order; loads are
+// non-temporal, and so are the bf16 kernel's stores.  The fp32 kernel's
+// stores are cached: at the FNet point [16384, 3072] they take the
+// reference harness's clean-cache launch from 73.7 to 69.0 us (graph
+// replay; Inductor 67.6), at a cost in the back-to-back loop (67.0 -> 70.0
+// us), where non-temporal stores win.  Elements past the last whole 16-byte vector are
 // done one by one by a second, one-workgroup launch.
 // HBM-bound: algorithmic bytes per element = 2 x sizeof(element).
 #include "gelu_bf16.h"
@@ -89,15 +97,11 @@ __global__ __launch_bounds__(kWave) void gelu_bf16_tail(const uint16_t* __restri
   }
 }
 
-__device__ __forceinline__ float gelu_tanh_eager_f32(float x) {
-#pragma clang fp contract(off)
-  const float a = x * 0.5f;
-  const float x3 = (x * x) * x;
-  const float b = x3 * 0.044715f;
-  const float c = x + b;
-  const float d = c * 0.7978845608028654f;
-  const float e = tanhf(d) + 1.0f;
-  return a * e;
+// x / (1 + e^(-2u)); e^-2u saturates to 0 (x -> +inf: y = x) and to inf
+// (x -> -inf: y = -0, and -inf / inf = NaN as eager's -inf * 0); NaN stays NaN.
+__device__ __forceinline__ float gelu_tanh_f32(float x) {
+  const float m2u = -1.5957691216057308f * __builtin_fmaf(0.044715f * x, x * x, x);
+  return x / (1.0f + exp_f32(exp_domain(m2u)));
 }
 
 template <int U>
@@ -119,8 +123,8 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_f32_flat(
     const int64_t i = v0 + u * kWave;
     f32x4_t o;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) o[k] = gelu_tanh_eager_f32(v[u][k]);
-    if (i < nvec) __builtin_nontemporal_store(o, yv + i);
+    for (int k = 0; k < 4; ++k) o[k] = gelu_tanh_f32(v[u][k]);
+    if (i < nvec) yv[i] = o;  // cached stores (see the header comment)
   }
 }
 
@@ -129,7 +133,7 @@ __global__ __launch_bounds__(kWave) void gelu_f32_tail(const float* __restrict__
                                                        int count) {
   if (static_cast<int>(threadIdx.x) < count) {
     const int64_t e = first + threadIdx.x;
-    y[e] = gelu_tanh_eager_f32(x[e]);
+    y[e] = gelu_tanh_f32(x[e]);
   }
 }
 

@@ -1,13 +1,17 @@
 // Scaled, additively masked softmax over the last dim, bf16 in / bf16 out.
 //
-// Semantics (eager op order of softmax(x * scale + mask, -1) on bf16):
-//   s = bf16(bf16(x * scale) + mask[q, :])       (each eager bf16 op rounds)
+// Semantics (softmax(x * scale + mask, -1) on bf16, scores formed in fp32
+// as the reference's Triton oracles and Inductor form them):
+//   s = fma(x, scale, mask[q, :])                  (fp32, one rounding)
 //   out = bf16(exp(s - max(s)) / sum(exp(s - max(s))))   (fp32 max and sum)
 // exp is natural exp of the fp32 difference s - max(s) (as aten.exp and
 // Inductor's libdevice.exp), evaluated to about one ulp by exp_f32, the
-// device library's extended-precision reduction (no exp2 rewrite).
-// When `scale` is a power of two, x * scale is exact in fp32 and the first
-// rounding is the identity, so it is skipped.
+// device library's extended-precision reduction (no exp2 rewrite).  Eager
+// rounds x * scale and the sum to bf16 first; with a power-of-two scale and
+// a 0 / -inf mask (the causal softmax) both roundings are exact, so the
+// scores are eager's; with a general bias (TrOCR) the fp32 scores are the
+// reference oracle's (its oracle.py builds them from fp32 x + bias) and
+// several times closer to fp64 than eager's rounded ones.
 //
 // Layout: rows held in registers, non-temporal 16-byte streaming accesses
 // for x and out; the mask row (mask[q, :], q = row % Q) is re-read by every
@@ -31,15 +35,13 @@ namespace {
 
 // exp(s - m): masked entries (s = -inf) give exactly 0; (-inf) - (-inf)
 // gives NaN for an all-masked row, exactly as the eager formula.
-constexpr uint32_t kNegInfPair = 0xFF80FF80u;  // two bf16 -inf
-
 __device__ __forceinline__ float exp_shifted(float s, float m) {
   // s - m <= 0 (m is the row max) or NaN, so only exp_f32's lower bound
   // needs the clamp (IEEE maximum: NaN stays NaN).
   return exp_f32(__builtin_elementwise_maximum(s - m, -104.0f));
 }
 
-template <int U, int WT, bool ROUND_SCALE>
+template <int U, int WT>
 __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
     uint16_t* __restrict__ out, int64_t rows, int64_t Q, int64_t K,
@@ -70,16 +72,10 @@ __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
     const bool in = row_group_col(u, waves_per_row, p) < K;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      float a0 = bf16lo(xv[u][d]) * scale;
-      float a1 = bf16hi(xv[u][d]) * scale;
-      if (ROUND_SCALE) {
-        const uint32_t r = pack_bf16x2(a0, a1);
-        a0 = bf16lo(r);
-        a1 = bf16hi(r);
-      }
-      const uint32_t t = pack_bf16x2(a0 + bf16lo(mv[u][d]), a1 + bf16hi(mv[u][d]));
-      s[u][2 * d] = in ? bf16lo(t) : -__builtin_inff();
-      s[u][2 * d + 1] = in ? bf16hi(t) : -__builtin_inff();
+      s[u][2 * d] = in ? __builtin_fmaf(bf16lo(xv[u][d]), scale, bf16lo(mv[u][d]))
+                       : -__builtin_inff();
+      s[u][2 * d + 1] = in ? __builtin_fmaf(bf16hi(xv[u][d]), scale, bf16hi(mv[u][d]))
+                           : -__builtin_inff();
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) m = fmaxf(m, s[u][e]);
@@ -143,7 +139,7 @@ __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
 constexpr int kShortV = 2;
 constexpr int kShortThreads = 256;
 
-template <int L, bool ROUND_SCALE>
+template <int L>
 __global__ __launch_bounds__(kShortThreads) void masked_softmax_short_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
     uint16_t* __restrict__ out, uint32_t rows, uint32_t Q, DivMagic q_div, int K,
@@ -176,16 +172,10 @@ __global__ __launch_bounds__(kShortThreads) void masked_softmax_short_rows(
     float m = -__builtin_inff();
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      float a0 = bf16lo(xv[v][d]) * scale;
-      float a1 = bf16hi(xv[v][d]) * scale;
-      if (ROUND_SCALE) {
-        const uint32_t t = pack_bf16x2(a0, a1);
-        a0 = bf16lo(t);
-        a1 = bf16hi(t);
-      }
-      const uint32_t t = pack_bf16x2(a0 + bf16lo(mv[v][d]), a1 + bf16hi(mv[v][d]));
-      s[2 * d] = col_in ? bf16lo(t) : -__builtin_inff();
-      s[2 * d + 1] = col_in ? bf16hi(t) : -__builtin_inff();
+      s[2 * d] = col_in ? __builtin_fmaf(bf16lo(xv[v][d]), scale, bf16lo(mv[v][d]))
+                        : -__builtin_inff();
+      s[2 * d + 1] = col_in ? __builtin_fmaf(bf16hi(xv[v][d]), scale, bf16hi(mv[v][d]))
+                            : -__builtin_inff();
       m = fmaxf(m, fmaxf(s[2 * d], s[2 * d + 1]));
     }
     m = seg_max<L>(m);
@@ -206,21 +196,14 @@ __global__ __launch_bounds__(kShortThreads) void masked_softmax_short_rows(
 }
 
 template <int L>
-void launch_short(bool round_scale, dim3 grid, hipStream_t stream, const uint16_t* x,
-                  const uint16_t* mask, uint16_t* out, int64_t rows, int64_t Q, int64_t K,
-                  int64_t ms, int64_t mbs, int64_t heads, float scale) {
-  const dim3 block(kShortThreads);
+void launch_short(dim3 grid, hipStream_t stream, const uint16_t* x, const uint16_t* mask,
+                  uint16_t* out, int64_t rows, int64_t Q, int64_t K, int64_t ms, int64_t mbs,
+                  int64_t heads, float scale) {
   const auto r = static_cast<uint32_t>(rows);
   const auto q = static_cast<uint32_t>(Q);
   const DivMagic qd = div_magic(q), hd = div_magic(static_cast<uint32_t>(heads));
-  const int k = static_cast<int>(K);
-  if (round_scale) {
-    masked_softmax_short_rows<L, true><<<grid, block, 0, stream>>>(x, mask, out, r, q, qd, k, ms,
-                                                                   mbs, hd, scale);
-  } else {
-    masked_softmax_short_rows<L, false><<<grid, block, 0, stream>>>(x, mask, out, r, q, qd, k,
-                                                                    ms, mbs, hd, scale);
-  }
+  masked_softmax_short_rows<L><<<grid, dim3(kShortThreads), 0, stream>>>(
+      x, mask, out, r, q, qd, static_cast<int>(K), ms, mbs, hd, scale);
 }
 
 // Rows of exactly K = 1024 or 2048 (KC, a compile-time constant):
@@ -253,7 +236,7 @@ void launch_short(bool round_scale, dim3 grid, hipStream_t stream, const uint16_
 // 260-267 us.  [192, 1024, 2048]: 258.7-260.1 us against 253.3 us.  With a
 // runtime K and idle lanes (K = 776, 1032) the layout lost 8-15 % to the
 // row-plan kernel, so other row lengths stay there.
-template <int KC, bool ROUND_SCALE, int RPW>
+template <int KC, int RPW>
 __global__ __launch_bounds__(256) void masked_softmax_shared_mask(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
     uint16_t* __restrict__ out, uint32_t batch, uint32_t Q, uint32_t gy,
@@ -307,24 +290,15 @@ __global__ __launch_bounds__(256) void masked_softmax_shared_mask(
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     float s[8];
-    uint32_t tw[4];  // the rounded scores as bf16 pairs
-    float m = -__builtin_inff();
+    float lmax = -__builtin_inff();  // NaN-propagating: NaN if any score is
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      float a0 = bf16lo(xv[i][d]) * scale;
-      float a1 = bf16hi(xv[i][d]) * scale;
-      if (ROUND_SCALE) {
-        const uint32_t r = pack_bf16x2(a0, a1);
-        a0 = bf16lo(r);
-        a1 = bf16hi(r);
-      }
-      const uint32_t t = pack_bf16x2(a0 + bf16lo(mv[d]), a1 + bf16hi(mv[d]));
-      tw[d] = t;
-      s[2 * d] = bf16lo(t);
-      s[2 * d + 1] = bf16hi(t);
-      m = fmaxf(m, fmaxf(s[2 * d], s[2 * d + 1]));
+      s[2 * d] = __builtin_fmaf(bf16lo(xv[i][d]), scale, bf16lo(mv[d]));
+      s[2 * d + 1] = __builtin_fmaf(bf16hi(xv[i][d]), scale, bf16hi(mv[d]));
+      lmax = __builtin_elementwise_maximum(
+          lmax, __builtin_elementwise_maximum(s[2 * d], s[2 * d + 1]));
     }
-    m = wave_max(m);
+    float m = wave_max(lmax);  // fmaxf: the row max of the non-NaN scores
     if (lane == 0) pmax[i][wave] = m;
     __syncthreads();
     m = pmax[i][rr * W];
@@ -333,11 +307,10 @@ __global__ __launch_bounds__(256) void masked_softmax_shared_mask(
 
     // A lane whose 8 scores are all -inf (a fully masked group: the causal
     // mask's upper triangle makes whole waves of them) has exp = 0 for each;
-    // the test is on the rounded score words, so a NaN score still goes
-    // through exp and poisons the row as in eager.
+    // a NaN score makes lmax NaN, so it still goes through exp and poisons
+    // the row as in eager.
     float sum = 0.f;
-    if ((tw[0] & tw[1] & tw[2] & tw[3]) == kNegInfPair &&
-        (tw[0] | tw[1] | tw[2] | tw[3]) == kNegInfPair) {
+    if (lmax == -__builtin_inff()) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) s[e] = 0.f;
     } else {
@@ -400,18 +373,12 @@ SharedMaskPlan shared_mask_plan(int64_t batch, int64_t Q, int64_t K, int64_t mbs
 }
 
 template <int KC>
-void launch_shared_mask(bool round_scale, const SharedMaskPlan& plan, hipStream_t stream,
-                        const uint16_t* x, const uint16_t* mask, uint16_t* out,
-                        int64_t batch, int64_t Q, int64_t ms, int64_t mbs, float scale) {
-  const auto bt = static_cast<uint32_t>(batch);
-  const auto q = static_cast<uint32_t>(Q);
-  if (round_scale) {
-    masked_softmax_shared_mask<KC, true, kSharedMaskRowsPerWave>
-        <<<plan.grid, dim3(256), 0, stream>>>(x, mask, out, bt, q, plan.gy, ms, mbs, scale);
-  } else {
-    masked_softmax_shared_mask<KC, false, kSharedMaskRowsPerWave>
-        <<<plan.grid, dim3(256), 0, stream>>>(x, mask, out, bt, q, plan.gy, ms, mbs, scale);
-  }
+void launch_shared_mask(const SharedMaskPlan& plan, hipStream_t stream, const uint16_t* x,
+                        const uint16_t* mask, uint16_t* out, int64_t batch, int64_t Q,
+                        int64_t ms, int64_t mbs, float scale) {
+  masked_softmax_shared_mask<KC, kSharedMaskRowsPerWave><<<plan.grid, dim3(256), 0, stream>>>(
+      x, mask, out, static_cast<uint32_t>(batch), static_cast<uint32_t>(Q), plan.gy, ms, mbs,
+      scale);
 }
 
 // Any K / alignment: one wave per row, three passes over the row (max, sum,
@@ -419,8 +386,7 @@ void launch_shared_mask(bool round_scale, const SharedMaskPlan& plan, hipStream_
 __global__ __launch_bounds__(256) void masked_softmax_rows_scalar(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
     uint16_t* __restrict__ out, int64_t rows, int64_t Q, int64_t K,
-    int64_t mask_stride, int64_t mask_batch_stride, int64_t heads, float scale,
-    int round_scale) {
+    int64_t mask_stride, int64_t mask_batch_stride, int64_t heads, float scale) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row =
       static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -431,9 +397,7 @@ __global__ __launch_bounds__(256) void masked_softmax_rows_scalar(
   const uint16_t* mr = mask + (b / heads) * mask_batch_stride + q * mask_stride;
   uint16_t* orow = out + row * K;
   auto score = [&](int64_t j) {
-    float a = bf16_to_f32(xr[j]) * scale;
-    if (round_scale) a = round_bf16(a);
-    return round_bf16(a + bf16_to_f32(mr[j]));
+    return __builtin_fmaf(bf16_to_f32(xr[j]), scale, bf16_to_f32(mr[j]));
   };
   float m = -__builtin_inff();
   for (int64_t j = lane; j < K; j += kWave) m = fmaxf(m, score(j));
@@ -449,27 +413,12 @@ __global__ __launch_bounds__(256) void masked_softmax_rows_scalar(
   }
 }
 
-bool is_power_of_two(float v) {
-  if (!(v > 0.0f) || v == __builtin_inff()) return false;
-  int e = 0;
-  return __builtin_frexpf(v, &e) == 0.5f;
-}
-
 template <int U, int WT>
-void launch_vec(bool round_scale, dim3 grid, const RowPlan& plan, hipStream_t stream,
-                const uint16_t* x, const uint16_t* mask, uint16_t* out,
-                int64_t rows, int64_t Q, int64_t K, int64_t ms, int64_t mbs,
-                int64_t heads, float scale) {
-  const dim3 block(plan.threads());
-  if (round_scale) {
-    masked_softmax_rows<U, WT, true><<<grid, block, 0, stream>>>(
-        x, mask, out, rows, Q, K, ms, mbs, heads, scale, plan.waves_per_row,
-        plan.rows_per_block);
-  } else {
-    masked_softmax_rows<U, WT, false><<<grid, block, 0, stream>>>(
-        x, mask, out, rows, Q, K, ms, mbs, heads, scale, plan.waves_per_row,
-        plan.rows_per_block);
-  }
+void launch_vec(dim3 grid, const RowPlan& plan, hipStream_t stream, const uint16_t* x,
+                const uint16_t* mask, uint16_t* out, int64_t rows, int64_t Q, int64_t K,
+                int64_t ms, int64_t mbs, int64_t heads, float scale) {
+  masked_softmax_rows<U, WT><<<grid, dim3(plan.threads()), 0, stream>>>(
+      x, mask, out, rows, Q, K, ms, mbs, heads, scale, plan.waves_per_row, plan.rows_per_block);
 }
 
 }  // namespace
@@ -489,7 +438,6 @@ int softmax_impl(const uint16_t* x, const uint16_t* mask, uint16_t* out, int64_t
   HIPO_REQUIRE(heads >= 1 && batch % heads == 0, "%s: heads must divide batch", what);
   HIPO_REQUIRE(mask_batch_stride >= 0, "%s: negative mask_batch_stride", what);
   const int64_t rows = batch * q;
-  const bool round_scale = !is_power_of_two(scale);
   RowPlan plan;
   const bool vec = (k % 8 == 0) && (mask_row_stride % 8 == 0) &&
                    (mask_batch_stride % 8 == 0) && row_plan(k, plan) && aligned16(x) &&
@@ -499,8 +447,8 @@ int softmax_impl(const uint16_t* x, const uint16_t* mask, uint16_t* out, int64_t
     const int64_t rows_per_block = int64_t{kShortV} * (kWave / lanes) * (kShortThreads / kWave);
     const dim3 grid(static_cast<unsigned>((rows + rows_per_block - 1) / rows_per_block));
 #define HIPO_SHORT(L_)                                                                  \
-  launch_short<L_>(round_scale, grid, stream, x, mask, out, rows, q, k, mask_row_stride, \
-                   mask_batch_stride, heads, scale)
+  launch_short<L_>(grid, stream, x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, \
+                   heads, scale)
     switch (lanes) {
       case 1: HIPO_SHORT(1); break;
       case 2: HIPO_SHORT(2); break;
@@ -516,10 +464,10 @@ int softmax_impl(const uint16_t* x, const uint16_t* mask, uint16_t* out, int64_t
                                             : SharedMaskPlan{};
              sp.k > 0) {
     if (sp.k == 1024) {
-      launch_shared_mask<1024>(round_scale, sp, stream, x, mask, out, batch, q, mask_row_stride,
+      launch_shared_mask<1024>(sp, stream, x, mask, out, batch, q, mask_row_stride,
                                mask_batch_stride, scale);
     } else {
-      launch_shared_mask<2048>(round_scale, sp, stream, x, mask, out, batch, q, mask_row_stride,
+      launch_shared_mask<2048>(sp, stream, x, mask, out, batch, q, mask_row_stride,
                                mask_batch_stride, scale);
     }
   } else if (vec) {
@@ -527,16 +475,15 @@ int softmax_impl(const uint16_t* x, const uint16_t* mask, uint16_t* out, int64_t
     HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);
     const dim3 grid(static_cast<unsigned>(blocks));
 #define HIPO_SOFTMAX(U_, W_)                                                            \
-  launch_vec<U_, W_>(round_scale, grid, plan, stream, x, mask, out, rows, q, k,          \
-                     mask_row_stride, mask_batch_stride, heads, scale)
+  launch_vec<U_, W_>(grid, plan, stream, x, mask, out, rows, q, k, mask_row_stride,   \
+                     mask_batch_stride, heads, scale)
     HIPO_ROW_DISPATCH(plan, HIPO_SOFTMAX);
 #undef HIPO_SOFTMAX
   } else {
     const int64_t blocks = (rows + 3) / 4;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);
     masked_softmax_rows_scalar<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
-        x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale,
-        round_scale ? 1 : 0);
+        x, mask, out, rows, q, k, mask_row_stride, mask_batch_stride, heads, scale);
   }
   return check_launch(what);
 }

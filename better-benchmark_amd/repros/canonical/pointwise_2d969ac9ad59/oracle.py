@@ -6,8 +6,8 @@ Kernels: hipo_gelu_tanh_bf16 -- the correctly rounded bf16 GELU of every
 bf16 input by bit pattern (a 7 KiB table of exactly rounded results staged
 in LDS, bit arithmetic outside its range; the eager graph's per-op bf16
 roundings and Inductor's fp32 chain both approximate this value);
-hipo_gelu_tanh_f32 -- eager's fp32 operation sequence, uncontracted, with
-the device library's tanh.  Flat streams of 16-byte non-temporal accesses,
+hipo_gelu_tanh_f32 -- x / (1 + e^(-2u)) with an extended-precision exp and
+an IEEE division (the same function, without 1 + tanh(u)'s cancellation).  Flat streams of 16-byte non-temporal accesses,
 8 KiB per wave.  Algorithmic bytes: 2 x numel x element size.
 Replaces the Triton body of the reference's
 repros/canonical/pointwise_2d969ac9ad59/oracle.py:44-62 (_tanh_gelu_kernel, :12).

@@ -73,8 +73,10 @@ int hipo_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x, const uint16_t* bias,
 
 /*
  * Scaled, additively masked softmax over the last dim (bf16 in/out):
- *   s[b,q,k] = bf16(bf16(x[b,q,k] * scale) + mask[q,k])
+ *   s[b,q,k] = fma(x[b,q,k], scale, mask[q,k])     (fp32 scores)
  *   out[b,q,:] = bf16(softmax_fp32(s[b,q,:]))
+ * (eager's bf16 roundings of x * scale and of the sum are exact for a
+ * power-of-two scale and a 0 / -inf mask, the causal softmax.)
  * x/out are [batch, q, k] contiguous; mask is [q, k] with row stride
  * `mask_row_stride` elements, broadcast over batch.
  * Replaces the Triton body of oracle_forward in
@@ -135,7 +137,8 @@ int hipo_rmsnorm_ex_bf16(const uint16_t* x, const uint16_t* residual,
 /*
  * Softmax over the last dim with an additive bias shared by groups of
  * `heads` consecutive batch entries:
- *   s[b,q,k] = bf16(bf16(x[b,q,k] * scale) + bias[b / heads][q, k])
+ *   s[b,q,k] = fma(x[b,q,k], scale, bias[b / heads][q, k])   (fp32 scores,
+ *              as the reference's Triton oracle builds them)
  *   out[b,q,:] = bf16(softmax_fp32(s[b,q,:]))
  * bias row of (b, q): bias + (b / heads) * bias_batch_stride
  *                          + q * bias_row_stride   (elements).
@@ -313,9 +316,9 @@ int hipo_flat_copy(const void* src, int64_t read_bytes, void* dst,
  * GELU(tanh) of a contiguous tensor of n elements, element by element:
  *   bf16: y = the correctly rounded bf16 of 0.5 x (1 + tanh(sqrt(2/pi)
  *         (x + 0.044715 x^3))) for every bf16 x (no intermediate rounding);
- *   fp32: eager's operation sequence in fp32, each op rounded, no FMA
- *         contraction: (x * 0.5) * (tanh((x + ((x * x) * x) * 0.044715) *
- *         0.7978845608028654) + 1), tanh from the device library.
+ *   fp32: the same function as x / (1 + e^(-2u)), u = sqrt(2/pi) (x +
+ *         0.044715 x^3), with an extended-precision exp and an IEEE division
+ *         (a few fp32 ulps from the exact value; no cancellation).
  * x and y are 16-byte aligned and do not overlap.
  * Replaces the Triton body of oracle_forward in
  * repros/canonical/pointwise_2d969ac9ad59/oracle.py:44-62 (_tanh_gelu_kernel,

@@ -142,8 +142,12 @@ void ref_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x, const uint16_t* bias,
 }
 
 /*
- * s = bf16(bf16(x * scale) + bias[b / heads, q, :]); out = bf16(softmax(s))
- * with the max, exp and sum in fp64.  x/out [batch, q, k]; the bias row of
+ * s = x * scale + bias[b / heads, q, :] (exact in fp64: no rounding of the
+ * scores, as the reference's Triton oracle forms them in fp32 --
+ * amax_sum_20ccc18dda60/oracle.py:44-46; eager's bf16 roundings of x * scale
+ * and of the sum are exact for the causal softmax's power-of-two scale and
+ * 0 / -inf mask); out = bf16(softmax(s)) with the max, exp and sum in fp64.
+ * x/out [batch, q, k]; the bias row of
  * (b, q) starts at (b / heads) * bias_batch_stride + q * bias_row_stride
  * elements.  The masked softmax is the case batch_stride = 0, heads = 1.
  */
@@ -164,8 +168,7 @@ void ref_scaled_bias_softmax_bf16(const uint16_t* x, const uint16_t* mask,
           mask + ((r / q) / heads) * mask_batch_stride + (r % q) * mask_stride;
       double m = -INFINITY;
       for (int64_t j = 0; j < k; ++j) {
-        const float a = round_bf16(bf16_to_f32(xr[j]) * scale);
-        const float v = round_bf16(a + bf16_to_f32(mr[j]));
+        const double v = (double)bf16_to_f32(xr[j]) * (double)scale + bf16_to_f32(mr[j]);
         s[j] = v;
         if (isnan(v) || isnan(m)) {
           m = NAN; /* amax propagates NaN */

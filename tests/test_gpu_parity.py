@@ -185,9 +185,12 @@ def _family_oracle(rid, i):
 #     checked below, of which the rounding boundaries allow a few);
 #   vs eager -- the decomposed GELU graph rounds each of its eight ops to
 #     bf16, and its 1 + tanh(u) loses up to half its digits in the negative
-#     tail (about 2e-3 absolute near x = -3), so eager is held to the
-#     reference harness's own comparison, allclose(atol=rtol=1e-2)
-#     (oracle_harness.py:865-923); the fp64 gate below still applies.
+#     tail (about 2e-3 absolute near x = -3); the TrOCR graph rounds its
+#     scores x + bias to bf16 (relative 2^-9 of |s|, carried into the
+#     probabilities), which the oracle -- as the reference's Triton oracle --
+#     does not.  Both are held to the reference harness's own comparison,
+#     allclose(atol=rtol=1e-2) (oracle_harness.py:865-923); the fp64 gate
+#     below still applies.
 # The ulp floor above which a family's bf16 output must be within one ulp of
 # the C oracle (families with no cancellation inside: the GELU table and
 # the fp64 oracle both round the exact value; a ReLU'd sum has no
@@ -195,6 +198,7 @@ def _family_oracle(rid, i):
 FAMILY_ORACLE_TOLS = {"pointwise_021e90d9c17d": {torch.bfloat16: EXACT},
                       "pointwise_2d969ac9ad59": {torch.bfloat16: PROB_TOL}}
 FAMILY_EAGER_TOLS = {"pointwise_2d969ac9ad59": {torch.bfloat16: (1e-2, 1e-2)},
+                     "amax_sum_20ccc18dda60": {torch.bfloat16: (1e-2, 1e-2)},
                      "pointwise_021e90d9c17d": {torch.bfloat16: EXACT}}
 FAMILY_ULP_FLOOR = {"pointwise_2d969ac9ad59": 0.0, "pointwise_021e90d9c17d": 0.0,
                     "mean_b402ee209d0b": 0.0}
@@ -382,8 +386,7 @@ def test_gelu_flat_every_input_and_sizes(rocm_device):
     """Flat GELU: bf16 bit for bit equal to the transposing kernel's mapping
     (the correctly rounded GELU) over all 65536 inputs, at sizes that leave
     a tail of 1..7 elements and below one vector; fp32 against the C oracle
-    (fp64) to fp32 error, and bit for bit against eager's op sequence on the
-    device."""
+    (fp64) and eager's op sequence on the device to the fp32 tolerance."""
     import hip_oracles
     import oracle as ref
     bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
@@ -409,15 +412,22 @@ def test_gelu_flat_every_input_and_sizes(rocm_device):
         assert_bf16_ulps(y, ref.gelu_tanh(x), 0.0, f"bf16 n={n}")
         xf = 4 * torch.randn(n, generator=g)
         yf = hip_oracles.gelu_tanh(xf.to(rocm_device))
-        # eager's fp32 sequence: 1 + tanh(u) cancels in the negative tail, so
-        # the error there is absolute (~1e-7), inside F32_TOL's floor
-        assert_close(yf, ref.gelu_tanh(xf), F32_TOL, f"fp32 n={n}")
+        want = ref.gelu_tanh(xf)
+        assert_close(yf, want, F32_TOL, f"fp32 n={n}")
+        # no cancellation anywhere: the relative error is that of e^(-2u),
+        # about |2u| fp32 roundings of the exponent plus a few ulps -- tail
+        # included (where eager's 1 + tanh(u) loses every digit)
+        xd64 = xf.double()
+        bound = 4e-7 * (1.5957691216057308 * (xd64 + 0.044715 * xd64 ** 3).abs() + 2)
+        err = (yf.cpu().double() - want.double()).abs()
+        sel = want.abs() > 1e-30
+        worst = (err[sel] / (want.double().abs()[sel] * bound[sel])).max().item() if sel.any() else 0
+        assert worst <= 1.0, f"fp32 n={n}: relative error {worst:.2f} x its bound"
         xd = xf.to(rocm_device)
         eager = (xd * 0.5) * (torch.tanh((xd + (xd * xd * xd) * 0.044715) * 0.7978845608028654) + 1)
         same = int((yf == eager).sum())
         print(f"gelu fp32 n={n}: {same} of {n} bit-identical to eager on the device", flush=True)
-        # the same fp32 operations in the same order, the same device tanh
-        assert same == n, f"fp32 n={n}: {n - same} values differ from eager's op sequence"
+        assert_close(yf, eager, F32_TOL, f"fp32 vs eager n={n}")
     with pytest.raises(RuntimeError, match="aligned"):
         hip_oracles.gelu_tanh(torch.zeros(17, dtype=torch.bfloat16, device=rocm_device)[1:])
 
@@ -495,7 +505,7 @@ def test_softmax_closed_forms(rocm_device):
     x = torch.randn(1, 4, 64).to(bf)
     out = hip_oracles.scaled_masked_softmax(x.to(rocm_device), full.to(rocm_device), 0.125).cpu()
     assert torch.isnan(out.float()).all()
-    # generic scale (rounded product), K off the vector path and K > 4096
+    # generic scale (fp32 scores), K off the vector path and K > 4096
     for (b_, q_, k_), scale in [((2, 8, 4096), 0.3), ((1, 3, 5000), 0.125), ((2, 5, 77), 1.7)]:
         g = torch.Generator().manual_seed(k_)
         x = (3 * torch.randn(b_, q_, k_, generator=g)).to(bf)
@@ -530,14 +540,14 @@ def test_softmax_short_rows(rocm_device):
         x = torch.randn(12, 9, k).to(bf)
         bias = torch.randn(3, 9, k).to(bf)
         got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), 1.0, 4)
-        want = torch.softmax((x.view(3, 4, 9, k) + bias.unsqueeze(1)).float(), -1).to(bf).view(12, 9, k)
+        want = torch.softmax((x.view(3, 4, 9, k).float() + bias.unsqueeze(1).float()), -1).to(bf).view(12, 9, k)
         assert_close(got, want, PROB_TOL, f"short bias softmax k={k}")
     # the TrOCR shape: 1024 rows of 256 per group of 16 heads
     g = torch.Generator().manual_seed(11)
     x = torch.randn(64, 256, 256, generator=g).to(bf)
     bias = torch.randn(4, 256, 256, generator=g).to(bf)
     got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), 1.0, 16)
-    want = torch.softmax((x.view(4, 16, 256, 256) + bias.unsqueeze(1)).float(), -1).to(bf).view(64, 256, 256)
+    want = torch.softmax((x.view(4, 16, 256, 256).float() + bias.unsqueeze(1).float()), -1).to(bf).view(64, 256, 256)
     assert_close(got, want, PROB_TOL, "trocr-like")
     assert_close(got.float().sum(-1), torch.ones(64, 256), 1e-2, "row sums")
 
@@ -546,7 +556,7 @@ def test_softmax_mid_rows(rocm_device):
     """512 < K <= 2048.  K = 1024 and 2048 take the shared-mask kernel (the
     rows of one q for 2 or 1 batch entries per workgroup, their mask row
     staged once through LDS), other K the row-plan kernel: odd batches that
-    leave the workgroup's last row empty, rounded scales, fully masked rows,
+    leave the workgroup's last row empty, inexact scales, fully masked rows,
     per-group biases that can share (heads even, or K = 2048) and that
     cannot (heads odd at K = 1024: the row-plan kernel)."""
     import hip_oracles
@@ -574,8 +584,8 @@ def test_softmax_mid_rows(rocm_device):
         got = hip_oracles.scaled_bias_softmax(x.to(rocm_device), bias.to(rocm_device), 1.0, heads)
         assert_close(got, ref.scaled_bias_softmax(x, bias, 1.0, heads), PROB_TOL, what)
         # each batch entry's rows against a direct fp32 softmax of its own bias group
-        want = torch.softmax((x.float().view(b // heads, heads, q, k) + bias.float().unsqueeze(1))
-                             .to(bf).float(), -1).to(bf).view(b, q, k)
+        want = torch.softmax(x.float().view(b // heads, heads, q, k) + bias.float().unsqueeze(1),
+                             -1).to(bf).view(b, q, k)
         assert_close(got, want, PROB_TOL, what + " vs torch")
         # the same bias as a padded view: row stride k + 8, batch stride q (k + 8)
         padded = torch.randn(b // heads, q, k + 8, generator=g).to(bf)
@@ -741,11 +751,11 @@ def test_scaled_bias_softmax_heads_and_strides(rocm_device):
     import hip_oracles
     bf = torch.bfloat16
 
-    def ref(x, bias, scale, heads):
+    def ref(x, bias, scale, heads):  # fp32 scores x * scale + bias
         b, q, k = x.shape
-        s = (x * scale) if scale != 1.0 else x
-        s = (s.view(b // heads, heads, q, k) + bias.unsqueeze(1)).view(b, q, k)
-        return torch.softmax(s.float(), -1).to(bf)
+        s = x.float() * scale
+        s = (s.view(b // heads, heads, q, k) + bias.float().unsqueeze(1)).view(b, q, k)
+        return torch.softmax(s, -1).to(bf)
 
     for b, heads, q, k, scale in [(12, 4, 17, 1032, 1.0), (8, 8, 5, 256, 0.125), (6, 2, 9, 100, 1.0),
                                   (4, 1, 3, 4104, 0.5), (2, 2, 2, 32768, 1.0)]:
