@@ -137,23 +137,33 @@ struct SpatialPlan {
   int64_t slice_len = 0;
 };
 
-// Channel blocks of 64 groups (1 KiB of each row) when the row has a
-// multiple of 64 groups and images x blocks already give about 256
+// Channel blocks of 64 groups (1 KiB of each row), or of 32 (512 bytes),
+// when the row divides into them and images x blocks give at least 256
 // workgroups: no position split, so no partial sums and no second kernel.
-// Measured on MI355X (oracle runner, cold cache), the eight 1536-channel
-// corpus points: 5-15 % faster than two position slices plus the finishing
-// kernel (e.g. [128, 1536, 8, 8] 11.2 -> 9.6 us, [128, 1536, 18, 18]
-// 26.7 -> 24.7 us).
+// The workgroup takes R rows per instruction, the smallest power of two
+// that covers the image's positions in four rounds of kUnroll loads per
+// thread, at most 512 threads.
+// Measured on MI355X (oracle runner, cold cache): 64-group blocks 5-15 %
+// faster than two position slices plus the finishing kernel on the eight
+// 1536-channel corpus points (e.g. [128, 1536, 8, 8] 11.2 -> 9.6 us,
+// [128, 1536, 18, 18] 26.7 -> 24.7 us); R sized to the positions instead
+// of a fixed 8 rows, [128, 1536, 6, 6] 15.4 -> 15.1 us and [128, 512, 24,
+// 24] (32-group blocks instead of slices) 25.1 -> 23.7 us (graph replays);
+// one round (R up to 16 rows, 1024 threads) was 4-6 % slower, cached loads
+// and 16- or 8-group blocks no faster.
 constexpr int kChannelBlock = 64;
 
 SpatialPlan spatial_plan(int64_t n, int64_t p, int64_t c) {
   SpatialPlan plan;
   if (c % 8 != 0 || c / 8 > kMaxThreads || n <= 0 || p <= 0) return plan;
-  if ((c / 8) % kChannelBlock == 0 && c / 8 > kChannelBlock &&
-      n * (c / 8 / kChannelBlock) >= 256) {
-    plan.group_block = kChannelBlock;
-    plan.cblocks = static_cast<int>(c / 8 / kChannelBlock);
-    plan.threads = kChannelBlock * 8;  // 8 rows per instruction
+  for (const int gb : {kChannelBlock, kChannelBlock / 2}) {
+    if ((c / 8) % gb != 0 || n * (c / 8 / gb) < 256) continue;
+    int64_t r = 1;
+    while (r * kUnroll * 4 < p && gb * r * 2 <= 512) r *= 2;
+    while (gb * r % kWave != 0) r *= 2;  // whole waves
+    plan.group_block = gb;
+    plan.cblocks = static_cast<int>(c / 8 / gb);
+    plan.threads = static_cast<int>(gb * r);
     plan.slices = 1;
     plan.slice_len = p;
     return plan;
