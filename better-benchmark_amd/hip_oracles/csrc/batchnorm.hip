@@ -2,9 +2,11 @@
 // (N, H, W), normalisation + affine (+ ReLU), running-stat update.
 //
 // Entry point.  The single-pass persistent kernel (batchnorm_fused.hip)
-// serves every shape it supports; the split-K path below serves the rest
-// (HW not a multiple of 4, unaligned pointers, very large tensors, more
-// than 64 workgroups per channel or 64 rounds).
+// serves every shape it supports.  Of the rest (HW not a multiple of 4,
+// unaligned pointers, very large tensors, more than 64 workgroups per
+// channel or 64 rounds), channels of at most 16384 values take one launch
+// with a workgroup per channel (bn_channel_whole), larger ones the split-K
+// path below.
 //
 // Split-K structure (two launches on the caller's stream):
 //   1. bn_partial_stats: grid (S, C).  Workgroup (s, c) reduces the planes
@@ -66,28 +68,37 @@ __device__ __forceinline__ void split_range(int64_t N, int64_t S, int64_t s,
   n1 = (N * (s + 1)) / S;
 }
 
-__global__ __launch_bounds__(kThreads) void bn_partial_stats_vec(
-    const float* __restrict__ x, float* __restrict__ ws, int64_t N, int64_t C,
-    int64_t HW, int64_t S) {
-  constexpr int U = 4;
-  const int64_t s = blockIdx.x;
-  const int64_t c = blockIdx.y;
-  int64_t n0, n1;
-  split_range(N, S, s, n0, n1);
-  const int64_t hw4 = HW / 4;
+// Welford triple of planes [n0, n1) of channel c over the workgroup: each
+// thread reduces its slice of every plane exactly (two-pass over registers)
+// and merges it into a running triple with Chan's formula; the wave merges
+// with DPP and the waves through LDS.  Thread 0 returns the total.
+template <bool VEC>
+__device__ Welford planes_welford(const float* __restrict__ x, int64_t n0, int64_t n1,
+                                  int64_t C, int64_t HW, int64_t c) {
   Welford acc{0.f, 0.f, 0.f};
-  for (int64_t n = n0; n < n1; ++n) {
-    const float4* plane = reinterpret_cast<const float4*>(x + (n * C + c) * HW);
-    for (int64_t base = 0; base < hw4; base += kThreads * U) {
-      float4 v[U];
-      bool ok[U];
+  if constexpr (VEC) {
+    constexpr int U = 4;
+    const int64_t hw4 = HW / 4;
+    for (int64_t n = n0; n < n1; ++n) {
+      const float4* plane = reinterpret_cast<const float4*>(x + (n * C + c) * HW);
+      for (int64_t base = 0; base < hw4; base += kThreads * U) {
+        float4 v[U];
+        bool ok[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t i = base + u * kThreads + threadIdx.x;
-        ok[u] = i < hw4;
-        v[u] = ok[u] ? plane[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int u = 0; u < U; ++u) {
+          const int64_t i = base + u * kThreads + threadIdx.x;
+          ok[u] = i < hw4;
+          v[u] = ok[u] ? plane[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        absorb<U>(acc, v, ok);
       }
-      absorb<U>(acc, v, ok);
+    }
+  } else {
+    for (int64_t n = n0; n < n1; ++n) {
+      const float* plane = x + (n * C + c) * HW;
+      for (int64_t i = threadIdx.x; i < HW; i += kThreads) {
+        acc = welford_merge(acc, Welford{1.f, plane[i], 0.f});
+      }
     }
   }
   acc = wave_welford(acc);
@@ -95,38 +106,19 @@ __global__ __launch_bounds__(kThreads) void bn_partial_stats_vec(
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = acc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    Welford t = welford_merge(welford_merge(part[0], part[1]),
-                              welford_merge(part[2], part[3]));
-    float* dst = ws + (c * S + s) * 3;
-    dst[0] = t.n;
-    dst[1] = t.mean;
-    dst[2] = t.m2;
-  }
+  return welford_merge(welford_merge(part[0], part[1]), welford_merge(part[2], part[3]));
 }
 
-__global__ __launch_bounds__(kThreads) void bn_partial_stats_scalar(
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void bn_partial_stats(
     const float* __restrict__ x, float* __restrict__ ws, int64_t N, int64_t C,
     int64_t HW, int64_t S) {
   const int64_t s = blockIdx.x;
   const int64_t c = blockIdx.y;
   int64_t n0, n1;
   split_range(N, S, s, n0, n1);
-  Welford acc{0.f, 0.f, 0.f};
-  for (int64_t n = n0; n < n1; ++n) {
-    const float* plane = x + (n * C + c) * HW;
-    for (int64_t i = threadIdx.x; i < HW; i += kThreads) {
-      acc = welford_merge(acc, Welford{1.f, plane[i], 0.f});
-    }
-  }
-  acc = wave_welford(acc);
-  __shared__ Welford part[kWavesPerBlock];
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = acc;
-  __syncthreads();
+  const Welford t = planes_welford<VEC>(x, n0, n1, C, HW, c);
   if (threadIdx.x == 0) {
-    Welford t = welford_merge(welford_merge(part[0], part[1]),
-                              welford_merge(part[2], part[3]));
     float* dst = ws + (c * S + s) * 3;
     dst[0] = t.n;
     dst[1] = t.mean;
@@ -154,43 +146,36 @@ __device__ void channel_stats(const float* __restrict__ ws, int64_t c,
   count = n;
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void bn_normalize(
-    const float* __restrict__ x, const float* __restrict__ gamma,
-    const float* __restrict__ beta, float* __restrict__ running_mean,
-    float* __restrict__ running_var, float* __restrict__ y,
-    float* __restrict__ save_mean, float* __restrict__ save_invstd,
-    const float* __restrict__ ws, int64_t N, int64_t C, int64_t HW, int64_t S,
-    float momentum, float eps, int relu) {
-  const int64_t s = blockIdx.x;
-  const int64_t c = blockIdx.y;
-  __shared__ float coef[2];
-  if (threadIdx.x == 0) {
-    double mean, m2, count;
-    channel_stats(ws, c, S, mean, m2, count);
-    const float meanf = static_cast<float>(mean);
-    const float var = static_cast<float>(m2 / count);
-    const float invstd = 1.0f / __builtin_sqrtf(var + eps);
-    const float alpha = invstd * gamma[c];
-    coef[0] = alpha;
-    coef[1] = beta[c] - meanf * alpha;
-    if (s == 0) {
-      save_mean[c] = meanf;
-      save_invstd[c] = invstd;
-      const double unbiased = count > 1.0 ? m2 / (count - 1.0)
-                                          : __builtin_nan("");
-      const double mom = momentum;
-      running_mean[c] = static_cast<float>(mom * mean +
-                                           (1.0 - mom) * running_mean[c]);
-      running_var[c] = static_cast<float>(mom * unbiased +
-                                          (1.0 - mom) * running_var[c]);
-    }
+// mean / invstd from the merged (mean, M2, count) of channel c -> the
+// affine coefficients (alpha = invstd * gamma, shift = beta - mean * alpha)
+// in coef[0..1]; with write_stats, save_mean / save_invstd and the running
+// statistics (unbiased variance, count / (count - 1)).
+__device__ void channel_coefs(double mean, double m2, double count, int64_t c,
+                              const float* __restrict__ gamma, const float* __restrict__ beta,
+                              float* __restrict__ running_mean, float* __restrict__ running_var,
+                              float* __restrict__ save_mean, float* __restrict__ save_invstd,
+                              float momentum, float eps, bool write_stats, float* coef) {
+  const float meanf = static_cast<float>(mean);
+  const float var = static_cast<float>(m2 / count);
+  const float invstd = 1.0f / __builtin_sqrtf(var + eps);
+  const float alpha = invstd * gamma[c];
+  coef[0] = alpha;
+  coef[1] = beta[c] - meanf * alpha;
+  if (write_stats) {
+    save_mean[c] = meanf;
+    save_invstd[c] = invstd;
+    const double unbiased = count > 1.0 ? m2 / (count - 1.0) : __builtin_nan("");
+    const double mom = momentum;
+    running_mean[c] = static_cast<float>(mom * mean + (1.0 - mom) * running_mean[c]);
+    running_var[c] = static_cast<float>(mom * unbiased + (1.0 - mom) * running_var[c]);
   }
-  __syncthreads();
-  const float alpha = coef[0];
-  const float shift = coef[1];
-  int64_t n0, n1;
-  split_range(N, S, s, n0, n1);
+}
+
+// y = relu?(x * alpha + shift) over planes [n0, n1) of channel c.
+template <bool VEC>
+__device__ void normalize_planes(const float* __restrict__ x, float* __restrict__ y,
+                                 int64_t n0, int64_t n1, int64_t C, int64_t HW, int64_t c,
+                                 float alpha, float shift, int relu) {
   for (int64_t n = n0; n < n1; ++n) {
     const int64_t off = (n * C + c) * HW;
     if (VEC) {
@@ -218,6 +203,55 @@ __global__ __launch_bounds__(kThreads) void bn_normalize(
       }
     }
   }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void bn_normalize(
+    const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float* __restrict__ running_mean,
+    float* __restrict__ running_var, float* __restrict__ y,
+    float* __restrict__ save_mean, float* __restrict__ save_invstd,
+    const float* __restrict__ ws, int64_t N, int64_t C, int64_t HW, int64_t S,
+    float momentum, float eps, int relu) {
+  const int64_t s = blockIdx.x;
+  const int64_t c = blockIdx.y;
+  __shared__ float coef[2];
+  if (threadIdx.x == 0) {
+    double mean, m2, count;
+    channel_stats(ws, c, S, mean, m2, count);
+    channel_coefs(mean, m2, count, c, gamma, beta, running_mean, running_var, save_mean,
+                  save_invstd, momentum, eps, s == 0, coef);
+  }
+  __syncthreads();
+  int64_t n0, n1;
+  split_range(N, S, s, n0, n1);
+  normalize_planes<VEC>(x, y, n0, n1, C, HW, c, coef[0], coef[1], relu);
+}
+
+// Small channels (N * HW <= kSmallChannel) the single-pass kernel does not
+// take: one workgroup per channel does everything in one launch -- the
+// split-K path's arithmetic with S = 1 (its single triple merged in fp64 is
+// that triple), the channel's second read served from cache.  At a ragged
+// parity point such as [3, 5, 7, 7] the launches, not the bytes, are the
+// time.
+constexpr int64_t kSmallChannel = 16384;
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void bn_channel_whole(
+    const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float* __restrict__ running_mean,
+    float* __restrict__ running_var, float* __restrict__ y,
+    float* __restrict__ save_mean, float* __restrict__ save_invstd, int64_t N, int64_t C,
+    int64_t HW, float momentum, float eps, int relu) {
+  const int64_t c = blockIdx.x;
+  const Welford t = planes_welford<VEC>(x, 0, N, C, HW, c);
+  __shared__ float coef[2];
+  if (threadIdx.x == 0)
+    channel_coefs(static_cast<double>(t.mean), static_cast<double>(t.m2),
+                  static_cast<double>(t.n), c, gamma, beta, running_mean, running_var,
+                  save_mean, save_invstd, momentum, eps, true, coef);
+  __syncthreads();
+  normalize_planes<VEC>(x, y, 0, N, C, HW, c, coef[0], coef[1], relu);
 }
 
 // Number of plane splits per channel for the split-K launches.
@@ -262,17 +296,30 @@ extern "C" int hipo_batchnorm_train_fwd_f32(
                                     eps, relu, workspace, stream);
   if (fused >= 0) return fused;
 
+  const bool vec = hw % 4 == 0 && aligned16(x) && aligned16(y);
+  if (n * hw <= kSmallChannel && c <= 0x7fffffff) {
+    const dim3 grid(static_cast<unsigned>(c));
+    if (vec) {
+      bn_channel_whole<true><<<grid, dim3(kThreads), 0, stream>>>(
+          x, gamma, beta, running_mean, running_var, y, save_mean, save_invstd, n, c, hw,
+          momentum, eps, relu);
+    } else {
+      bn_channel_whole<false><<<grid, dim3(kThreads), 0, stream>>>(
+          x, gamma, beta, running_mean, running_var, y, save_mean, save_invstd, n, c, hw,
+          momentum, eps, relu);
+    }
+    return check_launch("batchnorm_train_fwd_f32 (small channels)");
+  }
+
   HIPO_REQUIRE(c <= 65535, "batchnorm: too many channels");
   const int64_t S = num_splits(n, c);
   const dim3 grid(static_cast<unsigned>(S), static_cast<unsigned>(c));
   float* ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + kBnCtlBytes +
                                        bn_fused_slot_bytes(n, c, hw));
-  const bool vec = hw % 4 == 0 && aligned16(x) && aligned16(y);
   if (vec) {
-    bn_partial_stats_vec<<<grid, dim3(kThreads), 0, stream>>>(x, ws, n, c, hw, S);
+    bn_partial_stats<true><<<grid, dim3(kThreads), 0, stream>>>(x, ws, n, c, hw, S);
   } else {
-    bn_partial_stats_scalar<<<grid, dim3(kThreads), 0, stream>>>(x, ws, n, c, hw,
-                                                                 S);
+    bn_partial_stats<false><<<grid, dim3(kThreads), 0, stream>>>(x, ws, n, c, hw, S);
   }
   int rc = check_launch("batchnorm_train_fwd_f32 (stats)");
   if (rc) return rc;

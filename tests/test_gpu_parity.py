@@ -977,7 +977,9 @@ BN_PLAN_SHAPES = [
     (30, 100, 4000, "masked V=24, 3 slabs/channel, 2 rounds"),
     (2, 600, 16, "3 rounds (odd), tiny planes"),
     (2, 1000, 16, "4 rounds (even)"),
-    (3, 20000, 16, "more than 64 rounds: split-K path"),
+    (3, 20000, 16, "more than 64 rounds, small channels: one-launch path"),
+    (40, 3, 4001, "more than 64 rounds, HW % 4 != 0: split-K path"),
+    (3, 7, 49, "HW % 4 != 0, small channels: one-launch path"),
     (4, 9, 60, "HW % 4 == 0 but F not a power of two"),
 ]
 

@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [
     (128, 256, 56, 56),  # the BASELINE config: the single-pass kernel
-    (16, 24, 7, 7),      # smaller, HW % 4 != 0: the split-K path
+    (16, 24, 7, 7),      # smaller, HW % 4 != 0: one workgroup per channel
     (32, 64, 28, 28),    # smaller again, single pass with another slab plan
 ]
 
