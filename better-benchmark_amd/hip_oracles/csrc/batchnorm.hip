@@ -1,12 +1,12 @@
 // BatchNorm training forward, fp32 NCHW: per-channel statistics over
 // (N, H, W), normalisation + affine (+ ReLU), running-stat update.
 //
-// Entry point.  The single-pass persistent kernel (batchnorm_fused.hip)
-// serves every shape it supports.  Of the rest (HW not a multiple of 4,
-// unaligned pointers, very large tensors, more than 64 workgroups per
-// channel or 64 rounds), channels of at most 16384 values take one launch
-// with a workgroup per channel (bn_channel_whole), larger ones the split-K
-// path below.
+// Entry point.  Channels of at most 16384 values take one launch with a
+// workgroup per channel that holds its channel in registers
+// (bn_channel_small).  Larger channels take the single-pass persistent
+// kernel (batchnorm_fused.hip) wherever it applies, and the split-K path
+// below otherwise (HW not a multiple of 4, unaligned pointers, very large
+// tensors, more than 64 workgroups per channel or 64 rounds).
 //
 // Split-K structure (two launches on the caller's stream):
 //   1. bn_partial_stats: grid (S, C).  Workgroup (s, c) reduces the planes
@@ -24,6 +24,7 @@
 //      statistics (unbiased variance, count / (count - 1)).
 // This path reads x twice (once per launch).
 #include <mutex>
+#include <type_traits>
 
 #include "welford.h"
 
@@ -61,11 +62,43 @@ __device__ __forceinline__ void absorb(Welford& acc, const float4 (&v)[U],
   acc = welford_merge(acc, Welford{cnt, m, q});
 }
 
+// The same for up to U single values.
+template <int U>
+__device__ __forceinline__ void absorb(Welford& acc, const float (&v)[U], const bool (&ok)[U]) {
+  float cnt = 0.f, s = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (ok[u]) {
+      cnt += 1.f;
+      s += v[u];
+    }
+  }
+  if (cnt == 0.f) return;
+  const float m = s / cnt;
+  float q = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (ok[u]) q += (v[u] - m) * (v[u] - m);
+  }
+  acc = welford_merge(acc, Welford{cnt, m, q});
+}
+
 // Planes handled by split s of S over N planes.
 __device__ __forceinline__ void split_range(int64_t N, int64_t S, int64_t s,
                                             int64_t& n0, int64_t& n1) {
   n0 = (N * s) / S;
   n1 = (N * (s + 1)) / S;
+}
+
+// Merge the threads' triples: DPP across the wave, LDS across the waves.
+// Every thread returns the workgroup's total.
+__device__ __forceinline__ Welford block_welford(Welford acc) {
+  acc = wave_welford(acc);
+  __shared__ Welford part[kWavesPerBlock];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = acc;
+  __syncthreads();
+  return welford_merge(welford_merge(part[0], part[1]), welford_merge(part[2], part[3]));
 }
 
 // Welford triple of planes [n0, n1) of channel c over the workgroup: each
@@ -101,12 +134,7 @@ __device__ Welford planes_welford(const float* __restrict__ x, int64_t n0, int64
       }
     }
   }
-  acc = wave_welford(acc);
-  __shared__ Welford part[kWavesPerBlock];
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = acc;
-  __syncthreads();
-  return welford_merge(welford_merge(part[0], part[1]), welford_merge(part[2], part[3]));
+  return block_welford(acc);
 }
 
 template <bool VEC>
@@ -150,25 +178,37 @@ __device__ void channel_stats(const float* __restrict__ ws, int64_t c,
 // affine coefficients (alpha = invstd * gamma, shift = beta - mean * alpha)
 // in coef[0..1]; with write_stats, save_mean / save_invstd and the running
 // statistics (unbiased variance, count / (count - 1)).
-__device__ void channel_coefs(double mean, double m2, double count, int64_t c,
-                              const float* __restrict__ gamma, const float* __restrict__ beta,
-                              float* __restrict__ running_mean, float* __restrict__ running_var,
-                              float* __restrict__ save_mean, float* __restrict__ save_invstd,
-                              float momentum, float eps, bool write_stats, float* coef) {
+// channel_coefs with gamma[c], beta[c] and the running statistics already
+// loaded (g, b, rm, rv).
+__device__ void channel_coefs_of(double mean, double m2, double count, int64_t c, float g,
+                                 float b, float rm, float rv, float* __restrict__ running_mean,
+                                 float* __restrict__ running_var, float* __restrict__ save_mean,
+                                 float* __restrict__ save_invstd, float momentum, float eps,
+                                 bool write_stats, float* coef) {
   const float meanf = static_cast<float>(mean);
   const float var = static_cast<float>(m2 / count);
   const float invstd = 1.0f / __builtin_sqrtf(var + eps);
-  const float alpha = invstd * gamma[c];
+  const float alpha = invstd * g;
   coef[0] = alpha;
-  coef[1] = beta[c] - meanf * alpha;
+  coef[1] = b - meanf * alpha;
   if (write_stats) {
     save_mean[c] = meanf;
     save_invstd[c] = invstd;
     const double unbiased = count > 1.0 ? m2 / (count - 1.0) : __builtin_nan("");
     const double mom = momentum;
-    running_mean[c] = static_cast<float>(mom * mean + (1.0 - mom) * running_mean[c]);
-    running_var[c] = static_cast<float>(mom * unbiased + (1.0 - mom) * running_var[c]);
+    running_mean[c] = static_cast<float>(mom * mean + (1.0 - mom) * rm);
+    running_var[c] = static_cast<float>(mom * unbiased + (1.0 - mom) * rv);
   }
+}
+
+__device__ void channel_coefs(double mean, double m2, double count, int64_t c,
+                              const float* __restrict__ gamma, const float* __restrict__ beta,
+                              float* __restrict__ running_mean, float* __restrict__ running_var,
+                              float* __restrict__ save_mean, float* __restrict__ save_invstd,
+                              float momentum, float eps, bool write_stats, float* coef) {
+  channel_coefs_of(mean, m2, count, c, gamma[c], beta[c], write_stats ? running_mean[c] : 0.f,
+                   write_stats ? running_var[c] : 0.f, running_mean, running_var, save_mean,
+                   save_invstd, momentum, eps, write_stats, coef);
 }
 
 // y = relu?(x * alpha + shift) over planes [n0, n1) of channel c.
@@ -228,30 +268,130 @@ __global__ __launch_bounds__(kThreads) void bn_normalize(
   normalize_planes<VEC>(x, y, n0, n1, C, HW, c, coef[0], coef[1], relu);
 }
 
-// Small channels (N * HW <= kSmallChannel) the single-pass kernel does not
-// take: one workgroup per channel does everything in one launch -- the
-// split-K path's arithmetic with S = 1 (its single triple merged in fp64 is
-// that triple), the channel's second read served from cache.  At a ragged
-// parity point such as [3, 5, 7, 7] the launches, not the bytes, are the
-// time.
+// Small channels (N * HW <= kSmallChannel values): one launch, a workgroup
+// per channel holding the channel in registers -- U float4 (or U single
+// values when HW % 4 != 0 or x, y are unaligned) per thread, every load in
+// flight at once, with gamma, beta and the running statistics loaded beside
+// them.  Exact per-thread statistics (two-pass over the registers), Chan
+// merges across the wave and the workgroup, fp64 coefficients (the split-K
+// path's arithmetic with one split), then y written from the registers: x
+// is read once, and the chain from launch to the last store holds a single
+// memory round trip for the data.  At ragged points such as [3, 5, 7, 7]
+// or [4, 24, 10, 10] that chain, not the bytes, is the time (the
+// single-pass kernel adds an epoch read and a slab exchange to it).
 constexpr int64_t kSmallChannel = 16384;
 
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void bn_channel_whole(
+struct SmallGeom {
+  int total;      // float4 (VEC) or values per channel
+  int per_plane;  // HW / 4 (VEC) or HW
+  DivMagic by_plane;
+};
+
+template <bool VEC, int U>
+__global__ __launch_bounds__(kThreads) void bn_channel_small(
     const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, float* __restrict__ running_mean,
     float* __restrict__ running_var, float* __restrict__ y,
-    float* __restrict__ save_mean, float* __restrict__ save_invstd, int64_t N, int64_t C,
-    int64_t HW, float momentum, float eps, int relu) {
+    float* __restrict__ save_mean, float* __restrict__ save_invstd, SmallGeom g, int64_t C,
+    float momentum, float eps, int relu) {
+  using Elem = std::conditional_t<VEC, float4, float>;
   const int64_t c = blockIdx.x;
-  const Welford t = planes_welford<VEC>(x, 0, N, C, HW, c);
+  float pg = 0.f, pb = 0.f, prm = 0.f, prv = 0.f;
+  if (threadIdx.x == 0) {
+    pg = gamma[c];
+    pb = beta[c];
+    prm = running_mean[c];
+    prv = running_var[c];
+  }
+  // Element i of the channel: plane i / per_plane, offset i % per_plane.
+  auto offset = [&](int i) {
+    const uint32_t n = div_by(static_cast<uint32_t>(i), g.by_plane);
+    return (static_cast<int64_t>(n) * C + c) * g.per_plane +
+           (i - static_cast<int>(n) * g.per_plane);
+  };
+  const Elem* xs = reinterpret_cast<const Elem*>(x);
+  Elem v[U];
+  bool ok[U];
+  // Unconditional loads (threads past the channel's end re-read its last
+  // element and store nothing), so all of them are in flight together.
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = static_cast<int>(threadIdx.x) + u * kThreads;
+    ok[u] = i < g.total;
+    v[u] = xs[offset(ok[u] ? i : g.total - 1)];
+  }
+  Welford acc{0.f, 0.f, 0.f};
+  absorb<U>(acc, v, ok);
+  const Welford t = block_welford(acc);
   __shared__ float coef[2];
   if (threadIdx.x == 0)
-    channel_coefs(static_cast<double>(t.mean), static_cast<double>(t.m2),
-                  static_cast<double>(t.n), c, gamma, beta, running_mean, running_var,
-                  save_mean, save_invstd, momentum, eps, true, coef);
+    channel_coefs_of(static_cast<double>(t.mean), static_cast<double>(t.m2),
+                     static_cast<double>(t.n), c, pg, pb, prm, prv, running_mean, running_var,
+                     save_mean, save_invstd, momentum, eps, true, coef);
   __syncthreads();
-  normalize_planes<VEC>(x, y, 0, N, C, HW, c, coef[0], coef[1], relu);
+  const float alpha = coef[0], shift = coef[1];
+  Elem* ys = reinterpret_cast<Elem*>(y);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (!ok[u]) continue;
+    Elem o = v[u];
+    if constexpr (VEC) {
+      o.x = __builtin_fmaf(o.x, alpha, shift);
+      o.y = __builtin_fmaf(o.y, alpha, shift);
+      o.z = __builtin_fmaf(o.z, alpha, shift);
+      o.w = __builtin_fmaf(o.w, alpha, shift);
+      if (relu) {
+        o.x = relu_f32(o.x);
+        o.y = relu_f32(o.y);
+        o.z = relu_f32(o.z);
+        o.w = relu_f32(o.w);
+      }
+    } else {
+      o = __builtin_fmaf(o, alpha, shift);
+      if (relu) o = relu_f32(o);
+    }
+    ys[offset(static_cast<int>(threadIdx.x) + u * kThreads)] = o;
+  }
+}
+
+template <bool VEC, int U>
+void launch_small(const float* x, const float* gamma, const float* beta, float* running_mean,
+                  float* running_var, float* y, float* save_mean, float* save_invstd,
+                  const SmallGeom& g, int64_t c, float momentum, float eps, int relu,
+                  hipStream_t stream) {
+  bn_channel_small<VEC, U><<<dim3(static_cast<unsigned>(c)), dim3(kThreads), 0, stream>>>(
+      x, gamma, beta, running_mean, running_var, y, save_mean, save_invstd, g, c, momentum,
+      eps, relu);
+}
+
+// U = the smallest instantiated count covering the channel.
+int small_launch(const float* x, const float* gamma, const float* beta, float* running_mean,
+                 float* running_var, float* y, float* save_mean, float* save_invstd, int64_t n,
+                 int64_t c, int64_t hw, float momentum, float eps, int relu,
+                 hipStream_t stream) {
+  const bool vec = hw % 4 == 0 && aligned16(x) && aligned16(y);
+  SmallGeom g;
+  g.per_plane = static_cast<int>(vec ? hw / 4 : hw);
+  g.total = static_cast<int>(n) * g.per_plane;
+  g.by_plane = div_magic(static_cast<uint32_t>(g.per_plane));
+  const int per_thread = (g.total + kThreads - 1) / kThreads;
+#define HIPO_BN_SMALL(V, U)                                                              \
+  launch_small<V, U>(x, gamma, beta, running_mean, running_var, y, save_mean, save_invstd, \
+                     g, c, momentum, eps, relu, stream)
+  if (vec) {
+    if (per_thread <= 1) HIPO_BN_SMALL(true, 1);
+    else if (per_thread <= 2) HIPO_BN_SMALL(true, 2);
+    else if (per_thread <= 4) HIPO_BN_SMALL(true, 4);
+    else if (per_thread <= 8) HIPO_BN_SMALL(true, 8);
+    else HIPO_BN_SMALL(true, 16);
+  } else {
+    if (per_thread <= 1) HIPO_BN_SMALL(false, 1);
+    else if (per_thread <= 4) HIPO_BN_SMALL(false, 4);
+    else if (per_thread <= 16) HIPO_BN_SMALL(false, 16);
+    else HIPO_BN_SMALL(false, 64);
+  }
+#undef HIPO_BN_SMALL
+  return check_launch("batchnorm_train_fwd_f32 (small channels)");
 }
 
 // Number of plane splits per channel for the split-K launches.
@@ -291,25 +431,15 @@ extern "C" int hipo_batchnorm_train_fwd_f32(
                need);
   HIPO_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 8 == 0,
                "batchnorm: workspace must be 8-byte aligned");
+  if (n * hw <= kSmallChannel && c <= 0x7fffffff)
+    return small_launch(x, gamma, beta, running_mean, running_var, y, save_mean, save_invstd,
+                        n, c, hw, momentum, eps, relu, stream);
   const int fused = bn_fused_launch(x, gamma, beta, running_mean, running_var, y,
                                     save_mean, save_invstd, n, c, hw, momentum,
                                     eps, relu, workspace, stream);
   if (fused >= 0) return fused;
 
   const bool vec = hw % 4 == 0 && aligned16(x) && aligned16(y);
-  if (n * hw <= kSmallChannel && c <= 0x7fffffff) {
-    const dim3 grid(static_cast<unsigned>(c));
-    if (vec) {
-      bn_channel_whole<true><<<grid, dim3(kThreads), 0, stream>>>(
-          x, gamma, beta, running_mean, running_var, y, save_mean, save_invstd, n, c, hw,
-          momentum, eps, relu);
-    } else {
-      bn_channel_whole<false><<<grid, dim3(kThreads), 0, stream>>>(
-          x, gamma, beta, running_mean, running_var, y, save_mean, save_invstd, n, c, hw,
-          momentum, eps, relu);
-    }
-    return check_launch("batchnorm_train_fwd_f32 (small channels)");
-  }
 
   HIPO_REQUIRE(c <= 65535, "batchnorm: too many channels");
   const int64_t S = num_splits(n, c);

@@ -434,8 +434,10 @@ __global__ __launch_bounds__(kThreads) void bn_train_fused(
 using FusedKernel = void (*)(const f32x4_t*, f32x4_t*, FusedArgs, FusedGeom);
 
 // Instantiations: exact slabs of 28 float4 per thread, and masked slabs of
-// up to 4 / 8 / 16 / 24 float4 (two buffers of 28 masked float4 would not
-// fit in 256 VGPRs).
+// up to 16 / 24 float4 (two buffers of 28 masked float4 would not fit in
+// 256 VGPRs).  Channels this kernel is given hold more than 16384 values
+// (smaller ones take the register-held one-launch kernel), so a masked slab
+// has at least 10 float4 per thread.
 struct Variant {
   int v;
   bool full;
@@ -443,8 +445,6 @@ struct Variant {
 };
 const Variant kVariants[] = {
     {28, true, bn_train_fused<28, true, true>, bn_train_fused<28, true, false>},
-    {4, false, bn_train_fused<4, false, true>, bn_train_fused<4, false, false>},
-    {8, false, bn_train_fused<8, false, true>, bn_train_fused<8, false, false>},
     {16, false, bn_train_fused<16, false, true>, bn_train_fused<16, false, false>},
     {24, false, bn_train_fused<24, false, true>, bn_train_fused<24, false, false>},
 };

@@ -23,7 +23,9 @@
 // order keep the chip's in-flight address window compact, which measured
 // 67.5 us for config 2 against 71 us for a persistent one-workgroup-per-CU
 // version of this kernel with the GELU read from a 128 KiB LDS table.
-// Loads and stores are non-temporal.
+// Loads and stores are non-temporal.  Launches of at most 2^19 elements
+// (and shapes off the 16-byte vector path) take a one-element-per-thread
+// kernel instead.
 // HBM-bound: algorithmic bytes per element = 2 (read) + 2 (write).
 #include "gelu_bf16.h"
 #include "hipo_common.h"
@@ -36,6 +38,7 @@ constexpr int kTileC = 64;   // channels per wave tile
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlockThreads = kWavesPerBlock * kWave;
 constexpr int kTilesPerWave = 1;  // consecutive position tiles per wave (3-D grid)
+constexpr int64_t kTileMinElems = int64_t{1} << 19;  // smaller launches: scalar kernel
 
 struct TileGeom {
   int64_t C, HW;
@@ -191,8 +194,14 @@ extern "C" int hipo_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x,
   HIPO_REQUIRE(n >= 0 && c >= 0 && hw >= 0, "bias_gelu: negative size");
   if (n == 0 || c == 0 || hw == 0) return 0;
   HIPO_REQUIRE(x && bias && out, "bias_gelu: null pointer");
-  const bool vec = (c % 8 == 0) && (hw % 8 == 0) && aligned16(x) &&
-                   aligned16(bias) && aligned16(out);
+  // Up to kTileMinElems elements the one-element-per-thread kernel is the
+  // faster one: a tile wave maps its 4096 values serially (64 per lane), so
+  // a launch of few tiles is bound by one wave's instruction stream, not by
+  // memory (steady-state: 5.4 against 2.5 us at [3, 320, 8, 10], 5.9
+  // against 3.2 us at [4, 128, 28, 28]; 6.7 against 10.8 us at
+  // [2, 256, 56, 56], where the tiles win).
+  const bool vec = n * c * hw > kTileMinElems && (c % 8 == 0) && (hw % 8 == 0) &&
+                   aligned16(x) && aligned16(bias) && aligned16(out);
   if (vec) {
     const int64_t c_tiles = (c + kTileC - 1) / kTileC;
     const int64_t hw_tiles = (hw + kTileHw - 1) / kTileHw;

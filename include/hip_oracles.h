@@ -248,8 +248,10 @@ size_t hipo_batchnorm_workspace_bytes(int64_t n, int64_t c, int64_t hw);
  *   running_var  = (1 - momentum) running_var
  *                  + momentum var * count / (count - 1)     (in place)
  * x, y are contiguous [n, c, hw]; gamma, beta, running_*, save_* are [c].
- * Supported shapes run as one persistent kernel that reads x once (HW a
- * multiple of 4, 16-byte aligned x / y, x under 4 GiB); others as two
+ * Channels of at most 16384 values (n * hw) run as one launch with a
+ * workgroup per channel that holds it in registers (reads x once, uses no
+ * workspace); larger ones as one persistent kernel that reads x once (HW a
+ * multiple of 4, 16-byte aligned x / y, x under 4 GiB), others as two
  * split-K launches that read x twice.
  * `workspace` is caller-allocated device memory, 8-byte aligned, of at
  * least hipo_batchnorm_workspace_bytes(n, c, hw) bytes.  It must be
