@@ -259,6 +259,38 @@ def scaled_masked_softmax(x: torch.Tensor, mask: torch.Tensor, scale: float) -> 
     return out
 
 
+# bf16 zeros [K] per (device, K): the mask row of softmax_lastdim.
+_zero_rows: dict = {}
+
+
+def softmax_lastdim(x: torch.Tensor) -> torch.Tensor:
+    """softmax(x, -1) of a contiguous bf16 tensor (fp32 max, exp, sum and
+    division, bf16 out): hipo_scaled_masked_softmax_bf16 over [rows, 1, K]
+    with scale 1 and one zero mask row (s = fma(x, 1, 0) = x exactly).  The
+    zero row is allocated on a device's first call with that K, which
+    therefore must not be inside a graph capture."""
+    lib = load_library()
+    dev = _require_rocm(x)
+    _require(x.dtype == torch.bfloat16, "softmax: bf16 operand required")
+    _require(x.dim() >= 1 and x.is_contiguous(), "softmax: x must be contiguous")
+    k = x.shape[-1]
+    out = torch.empty_like(x)
+    if x.numel() == 0:
+        return out
+    key = (dev.index, k)
+    zero = _zero_rows.get(key)
+    if zero is None:
+        _require(not torch.cuda.is_current_stream_capturing(),
+                 "softmax: the first call for this K must run outside graph capture")
+        zero = _zero_rows[key] = torch.zeros(k, dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib.hipo_scaled_masked_softmax_bf16(_ptr(x), _ptr(zero), _ptr(out),
+                                                   x.numel() // k, 1, k, k, 1.0,
+                                                   _stream(dev)),
+               "softmax_lastdim")
+    return out
+
+
 def residual_layernorm(x, residual, gamma, beta, eps: float, *, outputs: str = "all"):
     """(h, y, mean, rstd) of LayerNorm(x + residual) over the last dim;
     outputs="y" returns y alone and writes nothing else."""

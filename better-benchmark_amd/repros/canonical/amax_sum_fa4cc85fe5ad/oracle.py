@@ -1,0 +1,30 @@
+"""
+MI355X oracle for amax_sum_fa4cc85fe5ad: the plain attention softmax of T5 /
+MT5 (no bias, no scale), bf16 in and out, fp32 statistics.
+
+Kernel: hipo_scaled_masked_softmax_bf16 with scale 1 and one zero mask row
+for every row (hip_oracles.softmax_lastdim) -- K = 1024 rows go to the
+shared-row kernel (the row's mask staged once per workgroup in LDS, four
+rows' loads in flight per wave), K = 128 rows to the short-row kernel (16
+lanes per row).  Algorithmic bytes: 2 B Q K (read) + 2 B Q K (write).
+Replaces the Triton body of the reference's
+repros/canonical/amax_sum_fa4cc85fe5ad/oracle.py:68 (_bf16_softmax_kernel, :12).
+"""
+import sys
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+import hip_oracles  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
+
+
+@oracle_impl(hardware="MI355X", point="215d1cc0", description="softmax, 16 lanes per row")
+@oracle_impl(hardware="MI355X", point="5b248c57", description="softmax, shared-row kernel")
+@oracle_impl(hardware="MI355X", description="softmax, shape-general")
+def oracle_forward(inputs):
+    scores, _grouped, _expanded, flat_shape = inputs
+    return hip_oracles.softmax_lastdim(scores).view(tuple(int(d) for d in flat_shape))
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

@@ -81,7 +81,10 @@ int hipo_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x, const uint16_t* bias,
  * `mask_row_stride` elements, broadcast over batch.
  * Replaces the Triton body of oracle_forward in
  * repros/canonical/amax_sum_20ccc18dda60/oracle.py:63
- * (_broadcast_add_softmax_kernel, same file :12).
+ * (_broadcast_add_softmax_kernel, same file :12), and -- with q = 1, one
+ * zero mask row and scale 1 -- the plain softmax of
+ * repros/canonical/amax_sum_fa4cc85fe5ad/oracle.py:68 (_bf16_softmax_kernel,
+ * same file :12).
  */
 int hipo_scaled_masked_softmax_bf16(const uint16_t* x, const uint16_t* mask,
                                     uint16_t* out, int64_t batch, int64_t q,

@@ -35,6 +35,7 @@ VARIANT_IDS = [
     "pointwise_2d969ac9ad59",
     "pointwise_021e90d9c17d",
     "mean_b402ee209d0b",
+    "amax_sum_fa4cc85fe5ad",
 ]
 
 

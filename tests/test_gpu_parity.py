@@ -169,6 +169,11 @@ def _family_oracle(rid, i):
     if rid == "mean_b402ee209d0b":
         x = i[0]
         return [ref.row_mean_bf16(x.reshape(x.shape[0] * x.shape[1], -1), relu=True)]
+    if rid == "amax_sum_fa4cc85fe5ad":
+        x = i[0]
+        k = x.shape[-1]
+        zero = torch.zeros(1, k, dtype=torch.bfloat16)
+        return [ref.scaled_masked_softmax(x.reshape(-1, 1, k), zero, 1.0).reshape(x.shape)]
     if rid == "var_mean_ceb5c315290a":
         x, rm, rv, g, b = i
         return list(ref.batchnorm_nhwc_act_pad(x, g, b, rm, rv, momentum=0.1, eps=1e-3,

@@ -606,6 +606,12 @@ def test_oracle_matches_family_repros():
     x = torch.randn(2, 3, 4, 8, generator=g).to(BF)
     want = get_repro_instance(CANONICAL / "pointwise_021e90d9c17d")(x, [2, 24, 2, 2])
     assert torch.equal(ref.transpose_last2(x).view(2, 24, 2, 2), want)
+    x = torch.randn(6, 5, 12, generator=g).to(BF)
+    want = get_repro_instance(CANONICAL / "amax_sum_fa4cc85fe5ad")(
+        x, [2, 3, 5, 12], [2, 3, 5, 12], [6, 5, 12])
+    zero = torch.zeros(1, 12, dtype=BF)
+    assert close(ref.scaled_masked_softmax(x.reshape(30, 1, 12), zero, 1.0).view(6, 5, 12),
+                 want, 1.6e-2)
     x = torch.randn(2, 5, 3, 3, generator=g).to(BF)
     want = get_repro_instance(CANONICAL / "mean_b402ee209d0b")(x, [2, 5])
     assert close(ref.row_mean_bf16(x.reshape(10, 9), relu=True).view(2, 5), want, 1.6e-2)

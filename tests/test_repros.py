@@ -118,6 +118,15 @@ def test_bias_softmax_family_repro():
     assert torch.equal(y, want)
 
 
+def test_plain_softmax_family_repro():
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(6, 5, 12, generator=g).to(bf)      # viewed [2, 3, 5, 12]
+    y = get_repro_instance(CANONICAL / "amax_sum_fa4cc85fe5ad")(
+        x, [2, 3, 5, 12], [2, 3, 5, 12], [6, 5, 12])
+    assert y.shape == (6, 5, 12) and y.dtype == bf
+    assert torch.equal(y, torch.softmax(x.float(), -1).to(bf))
+
+
 def test_longformer_layernorm_family_repro():
     g = torch.Generator().manual_seed(8)
     x = torch.randn(6, 32, generator=g).to(bf)
