@@ -293,7 +293,8 @@ def softmax_lastdim(x: torch.Tensor) -> torch.Tensor:
 
 def residual_layernorm(x, residual, gamma, beta, eps: float, *, outputs: str = "all"):
     """(h, y, mean, rstd) of LayerNorm(x + residual) over the last dim;
-    outputs="y" returns y alone and writes nothing else."""
+    outputs="y" returns y alone and writes nothing else, outputs="hy"
+    returns (h, y) and writes no statistics."""
     lib = load_library()
     dev = _require_rocm(x, residual, gamma, beta)
     for t in (x, residual, gamma, beta):
@@ -302,13 +303,17 @@ def residual_layernorm(x, residual, gamma, beta, eps: float, *, outputs: str = "
     _require(x.dim() == 2 and residual.shape == x.shape, "residual_layernorm: x, residual [R, C]")
     rows, cols = x.shape
     _require(gamma.shape == (cols,) and beta.shape == (cols,), "residual_layernorm: gamma/beta [C]")
-    _require(outputs in ("all", "y"), "residual_layernorm: outputs must be 'all' or 'y'")
+    _require(outputs in ("all", "y", "hy"),
+             "residual_layernorm: outputs must be 'all', 'y' or 'hy'")
     y = torch.empty_like(x)
     if outputs == "all":
         h = torch.empty_like(x)
         mean = torch.empty(rows, dtype=torch.float32, device=dev)
         rstd = torch.empty(rows, dtype=torch.float32, device=dev)
         ptrs = (_ptr(h), _ptr(mean), _ptr(rstd))
+    elif outputs == "hy":
+        h = torch.empty_like(x)
+        ptrs = (_ptr(h), None, None)
     else:
         ptrs = (None, None, None)
     with torch.cuda.device(dev):
@@ -316,7 +321,9 @@ def residual_layernorm(x, residual, gamma, beta, eps: float, *, outputs: str = "
             _ptr(x), _ptr(residual), _ptr(gamma), _ptr(beta), ptrs[0], _ptr(y),
             ptrs[1], ptrs[2], rows, cols, float(eps), _stream(dev)),
             "residual_layernorm")
-    return (h, y, mean, rstd) if outputs == "all" else y
+    if outputs == "all":
+        return h, y, mean, rstd
+    return (h, y) if outputs == "hy" else y
 
 
 def rmsnorm(x, gamma, eps: float):

@@ -400,6 +400,153 @@ __global__ __launch_bounds__(256) void residual_layernorm_k(
   }
 }
 
+// Rows of at most 1536 values held by L consecutive lanes (L a power of
+// two, 8..64): a wave covers 64 / L rows, a 256-thread workgroup 256 / L
+// consecutive rows.  Lane l of a row owns the 16-byte groups g = u * L + l
+// (u < U), so each load instruction of a wave reads L * 16 contiguous bytes
+// of every one of its rows.  Groups past the row end re-read the row's last
+// group and count for nothing.  Statistics: the exact two-pass over the
+// row's bf16 h (sum -> mean, then the sum of squared deviations from it),
+// each reduced over the row's L lanes by seg_sum in a fixed order.  gamma
+// and beta of a lane's groups are the same for every row, loaded once.
+// Plans (seg_plan): rows of up to 512 values take one group per lane (L =
+// the row's groups rounded up to a power of two, at least 8), rows of
+// 520..1536 values 64 lanes with 2 or 3 groups when there are at least 16384
+// of them; the rest take the row kernel.  Measured on MI355X (oracle runner,
+// graph replays after a cache flush; the row kernel's time first):
+// [131072, 144] 58.4 -> 36.9 us (8 lanes x 3 groups: 53.8), [25216, 192]
+// 21.4 -> 18.4, [32768, 256] 23.6 -> 20.0, [16384, 768] 24.6 -> 23.8,
+// [32768, 768] 35.8 -> 34.9, [16384, 1024] 28.4 -> 27.6; but [8192, 1024]
+// 19.2 -> 20.0 and [8192, 768] 17.6 -> 18.0 (also with 8-row workgroups or
+// DPP-and-readlane sums: 19.7, 19.9), and at 2048 values one wave per row
+// with 4 groups lost to the row kernel's two waves with 2 (20.4 against
+// 19.2 us).
+template <int L, int U>
+__global__ __launch_bounds__(256) void residual_layernorm_seg(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
+    const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
+    uint16_t* __restrict__ h, uint16_t* __restrict__ y, float* __restrict__ mean_out,
+    float* __restrict__ rstd_out, int64_t rows, int cols, float eps) {
+  constexpr int kRowsPerBlock = 256 / L;
+  const int l = static_cast<int>(threadIdx.x) & (L - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / L;
+  const bool valid = row < rows;
+  const int64_t base = (valid ? row : rows - 1) * cols;
+  const int groups = cols / kRowGroup;
+
+  u32x4_t hv[U], rv[U], gv[U], bv[U];
+  bool in[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int g = u * L + l;
+    in[u] = g < groups;
+    const int col = (in[u] ? g : groups - 1) * kRowGroup;
+    hv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + base + col));
+    rv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(res + base + col));
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int col = (in[u] ? u * L + l : groups - 1) * kRowGroup;
+    gv[u] = *reinterpret_cast<const u32x4_t*>(gamma + col);
+    bv[u] = *reinterpret_cast<const u32x4_t*>(beta + col);
+  }
+
+  // h = bf16(x + residual); the statistics use the bf16-rounded h.
+  float sum = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      hv[u][d] = pack_bf16x2(bf16lo(hv[u][d]) + bf16lo(rv[u][d]),
+                             bf16hi(hv[u][d]) + bf16hi(rv[u][d]));
+      if (in[u]) sum += bf16lo(hv[u][d]) + bf16hi(hv[u][d]);
+    }
+    if (h != nullptr && valid && in[u])
+      row_store_stream(h + base, static_cast<int64_t>(u * L + l) * kRowGroup, hv[u]);
+  }
+  const float inv_n = 1.0f / static_cast<float>(cols);
+  const float mean = seg_sum<L>(sum) * inv_n;
+  float sq = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const float a = bf16lo(hv[u][d]) - mean;
+      const float b = bf16hi(hv[u][d]) - mean;
+      if (in[u]) sq = __builtin_fmaf(a, a, __builtin_fmaf(b, b, sq));
+    }
+  }
+  const float rstd = 1.0f / __builtin_sqrtf(seg_sum<L>(sq) * inv_n + eps);
+  const float shift = -mean * rstd;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    u32x4_t o;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const float n0 = __builtin_fmaf(bf16lo(hv[u][d]), rstd, shift);
+      const float n1 = __builtin_fmaf(bf16hi(hv[u][d]), rstd, shift);
+      o[d] = pack_bf16x2(__builtin_fmaf(n0, bf16lo(gv[u][d]), bf16lo(bv[u][d])),
+                         __builtin_fmaf(n1, bf16hi(gv[u][d]), bf16hi(bv[u][d])));
+    }
+    if (valid && in[u]) row_store_stream(y + base, static_cast<int64_t>(u * L + l) * kRowGroup, o);
+  }
+  if (valid && l == 0) {
+    if (mean_out != nullptr) mean_out[row] = mean;
+    if (rstd_out != nullptr) rstd_out[row] = rstd;
+  }
+}
+
+struct SegPlan {
+  int lanes = 0, groups = 0;  // 0: not this kernel
+};
+
+SegPlan seg_plan(int64_t rows, int64_t cols) {
+  SegPlan p;
+  if (cols % kRowGroup != 0 || cols <= 0 || cols > 1536) return p;
+  const int g = static_cast<int>(cols / kRowGroup);
+  if (g > kWave && rows < 16384) return p;  // the row kernel's 8-row workgroups win there
+  if (g <= kWave) {
+    p.lanes = 8;
+    while (p.lanes < g) p.lanes *= 2;
+    p.groups = 1;
+  } else {
+    p.lanes = kWave;
+    p.groups = (g + kWave - 1) / kWave;
+  }
+  return p;
+}
+
+template <int L, int U>
+void launch_seg(int64_t rows, hipStream_t stream, const uint16_t* x, const uint16_t* residual,
+                const uint16_t* gamma, const uint16_t* beta, uint16_t* h, uint16_t* y,
+                float* mean, float* rstd, int cols, float eps) {
+  constexpr int kRowsPerBlock = 256 / L;
+  residual_layernorm_seg<L, U>
+      <<<dim3(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock)), dim3(256), 0,
+         stream>>>(x, residual, gamma, beta, h, y, mean, rstd, rows, cols, eps);
+}
+
+// Dispatch over the (L, U) pairs seg_plan returns.
+void launch_seg_plan(const SegPlan& sp, int64_t rows, hipStream_t stream, const uint16_t* x,
+                     const uint16_t* residual, const uint16_t* gamma, const uint16_t* beta,
+                     uint16_t* h, uint16_t* y, float* mean, float* rstd, int cols, float eps) {
+#define HIPO_SEG(L_, U_) \
+  launch_seg<L_, U_>(rows, stream, x, residual, gamma, beta, h, y, mean, rstd, cols, eps)
+  if (sp.groups == 1) {
+    switch (sp.lanes) {
+      case 8: HIPO_SEG(8, 1); break;
+      case 16: HIPO_SEG(16, 1); break;
+      case 32: HIPO_SEG(32, 1); break;
+      default: HIPO_SEG(64, 1); break;
+    }
+  } else if (sp.groups == 2) {
+    HIPO_SEG(64, 2);
+  } else {
+    HIPO_SEG(64, 3);
+  }
+#undef HIPO_SEG
+}
+
 // Rows per slot of residual_layernorm_k.  Measured at [16384, 4096], one
 // process: 1 row 90.2-90.8 us, 2 rows 93.4 us, 4 rows 100.6-102.8 us (each
 // wave already keeps 8 KiB in flight per row; the masked softmax, at 1 KiB
@@ -430,6 +577,10 @@ extern "C" int hipo_residual_layernorm_bf16(
     residual_layernorm_k<4096, kLayerNormRowsPerWave>
         <<<dim3(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock)), dim3(256), 0,
            stream>>>(x, residual, gamma, beta, h, y, mean, rstd, rows, eps);
+  } else if (const SegPlan sp = vec ? seg_plan(rows, cols) : SegPlan{};
+             sp.lanes > 0 && (rows + 256 / sp.lanes - 1) / (256 / sp.lanes) <= 0x7fffffff) {
+    launch_seg_plan(sp, rows, stream, x, residual, gamma, beta, h, y, mean, rstd,
+                    static_cast<int>(cols), eps);
   } else if (vec) {
     const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "residual_layernorm: too many rows");

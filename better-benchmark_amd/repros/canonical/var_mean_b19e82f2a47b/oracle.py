@@ -1,0 +1,55 @@
+"""
+MI355X oracle for var_mean_b19e82f2a47b: residual add + LayerNorm over the
+last dim (eps 1e-05), returning the bf16 sum h and three [R, C] views of y.
+
+Kernel: hipo_residual_layernorm_bf16 -- h = bf16(x + residual), exact fp32
+statistics of the bf16 h held in registers, y = bf16((h - mean) rstd gamma +
+beta); rows of 4096 take the row-length kernel (2 waves per row, gamma and
+beta staged in LDS), others the row-plan kernel (W waves per row, about
+2 KiB of each stream per wave).  Algorithmic bytes per row of C: 2C (x) +
+2C (residual) + 2C (y) + 2C (h).
+Replaces the Triton body of the reference's
+repros/canonical/var_mean_b19e82f2a47b/oracle.py:99.
+"""
+import sys
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+import hip_oracles  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
+
+EPS = 1e-05
+
+
+@oracle_impl(hardware="MI355X", point="c4bf51cc",
+             description="residual LayerNorm, 4096 x 2560")
+@oracle_impl(hardware="MI355X", point="7f824027",
+             description="residual LayerNorm, 2048 x 2560")
+@oracle_impl(hardware="MI355X", point="f2c837cd",
+             description="residual LayerNorm, 4096 x 2048")
+@oracle_impl(hardware="MI355X", point="17affd46",
+             description="residual LayerNorm, 8192 x 1024")
+@oracle_impl(hardware="MI355X", point="0b3dc49f",
+             description="residual LayerNorm, 8192 x 1024")
+@oracle_impl(hardware="MI355X", point="ceab07f0",
+             description="residual LayerNorm, 8192 x 1024")
+@oracle_impl(hardware="MI355X", point="a3e95c29",
+             description="residual LayerNorm, 16384 x 1024")
+@oracle_impl(hardware="MI355X", point="f2e11670",
+             description="residual LayerNorm, 4096 x 1024")
+@oracle_impl(hardware="MI355X", point="324149d9",
+             description="residual LayerNorm, 1 x 384")
+@oracle_impl(hardware="MI355X", description="residual LayerNorm, shape-general")
+def oracle_forward(inputs):
+    x, residual, gamma, beta = inputs[:4]
+    shapes = inputs[4:]
+    cols = x.shape[-1]
+    out = hip_oracles.residual_layernorm(x.reshape(-1, cols), residual.reshape(-1, cols),
+                                         gamma, beta, EPS, outputs="hy")
+    h, y = out
+    return (h.view(residual.shape),) + tuple(y.view(tuple(int(d) for d in s))
+                                             for s in shapes[1:4])
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

@@ -23,6 +23,19 @@ REPRO_IDS = [
 ]
 
 
+# Residual add + LayerNorm corpus families on one kernel, by what they
+# return: y2 = y viewed [R, C]; h_y2 = (h, y); h_y2x3 = (h, three views of
+# y); y3_y2x3 = (y, three views of it); y3_y2 = (y, a view of it).
+LN_FAMILY_OUTPUTS = {
+    "var_mean_0ada225c0a04": "y2",
+    "var_mean_96edf0542ecd": "y2",
+    "var_mean_ee167627f636": "y2",
+    "var_mean_f4578c128d74": "h_y2",
+    "var_mean_b19e82f2a47b": "h_y2x3",
+    "var_mean_393456b916a6": "y3_y2x3",
+    "var_mean_45f7dfd4a983": "y3_y2",
+}
+
 # Corpus families the kernels generalise to (the reference's canonical dir
 # names, their shape points and model counts).
 VARIANT_IDS = [
@@ -36,7 +49,7 @@ VARIANT_IDS = [
     "pointwise_021e90d9c17d",
     "mean_b402ee209d0b",
     "amax_sum_fa4cc85fe5ad",
-]
+] + list(LN_FAMILY_OUTPUTS)
 
 
 def pytest_configure(config):

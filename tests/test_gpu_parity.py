@@ -21,7 +21,7 @@ import math
 import pytest
 import torch
 
-from conftest import CANONICAL, REPRO_IDS, VARIANT_IDS
+from conftest import CANONICAL, LN_FAMILY_OUTPUTS, REPRO_IDS, VARIANT_IDS
 
 pytestmark = pytest.mark.gpu
 
@@ -148,6 +148,28 @@ def test_all_points_vs_oracle_and_eager(rid, rocm_device):
         del cpu_in, dev_in, got, want, eager
 
 
+def _ln_family_outputs(rid, i):
+    """The C oracle's (h, y) arranged as the residual LayerNorm family rid
+    returns them (conftest.LN_FAMILY_OUTPUTS)."""
+    import oracle as ref
+    from oracle_harness import load_repro_module
+    eps = load_repro_module(CANONICAL / rid).EPS
+    x, r, g, b = i[:4]
+    shapes = [tuple(int(d) for d in s) for s in i[4:]]
+    cols = x.shape[-1]
+    h, y, _, _ = ref.residual_layernorm(x.reshape(-1, cols), r.reshape(-1, cols), g, b, eps)
+    kind = LN_FAMILY_OUTPUTS[rid]
+    if kind == "y2":
+        return [y.view(shapes[-1])]
+    if kind == "h_y2":
+        return [h.view(r.shape), y.view(shapes[1])]
+    if kind == "h_y2x3":
+        return [h.view(r.shape)] + [y.view(sh) for sh in shapes[1:4]]
+    if kind == "y3_y2x3":
+        return [y.view(shapes[0])] + [y.view(sh) for sh in shapes[1:4]]
+    return [y.view(shapes[0]), y.view(shapes[1])]
+
+
 def _family_oracle(rid, i):
     """The C oracle's outputs for a family point's CPU inputs."""
     import oracle as ref
@@ -169,6 +191,8 @@ def _family_oracle(rid, i):
     if rid == "mean_b402ee209d0b":
         x = i[0]
         return [ref.row_mean_bf16(x.reshape(x.shape[0] * x.shape[1], -1), relu=True)]
+    if rid in LN_FAMILY_OUTPUTS:
+        return _ln_family_outputs(rid, i)
     if rid == "amax_sum_fa4cc85fe5ad":
         x = i[0]
         k = x.shape[-1]
@@ -641,6 +665,42 @@ def test_norm_shapes_off_vector_path(rocm_device):
         want = ref.rmsnorm(x, gm, 1e-5)
         for name, a, w in zip(("y", "rstd"), got, want):
             assert_close(a, w, _tol(w), f"rms {rows}x{cols} {name}")
+
+
+# Row lengths of the segmented LayerNorm kernel's plans (one group per lane
+# on 8 / 16 / 32 / 64 lanes up to 512 values, 64 lanes x 2 or 3 groups up to
+# 1536 for 16384 rows or more), at both ends of each, with idle trailing
+# lanes (144 = 18 of 32), and past it on the multi-wave row kernel (1544,
+# 2048, 2560, 4088).
+LN_SEG_COLS = [8, 56, 64, 72, 120, 128, 136, 144, 192, 240, 256, 264, 384, 512, 520, 768,
+               1024, 1032, 1536, 1544, 2048, 2560, 4088]
+
+
+@pytest.mark.parametrize("cols", LN_SEG_COLS)
+def test_layernorm_segmented_rows(cols, rocm_device):
+    """The segmented kernel against the C oracle: every output, rows that
+    leave the last workgroup partly idle, and the y-only / h-and-y modes
+    (NULL statistics pointers)."""
+    import hip_oracles
+    import oracle as ref
+    bf = torch.bfloat16
+    for rows in (1, 37, 300) + ((16389,) if 512 < cols <= 1536 else ()):
+        g = torch.Generator().manual_seed(rows * 7 + cols)
+        x = (torch.randn(rows, cols, generator=g) * 2 + 0.5).to(bf)
+        r = torch.randn(rows, cols, generator=g).to(bf)
+        gm = (1 + 0.1 * torch.randn(cols, generator=g)).to(bf)
+        bt = (0.1 * torch.randn(cols, generator=g)).to(bf)
+        d = [t.to(rocm_device) for t in (x, r, gm, bt)]
+        want = ref.residual_layernorm(x, r, gm, bt, 1e-6)
+        for name, a, w in zip(("h", "y", "mean", "rstd"),
+                              hip_oracles.residual_layernorm(*d, 1e-6), want):
+            assert_close(a, w, _tol(w), f"ln seg {rows}x{cols} {name}")
+        assert torch.equal(hip_oracles.residual_layernorm(*d, 1e-6)[0].cpu(), want[0]), "h exact"
+        assert_close(hip_oracles.residual_layernorm(*d, 1e-6, outputs="y"), want[1], BF16_TOL,
+                     f"ln seg {rows}x{cols} y-only")
+        h, y = hip_oracles.residual_layernorm(*d, 1e-6, outputs="hy")
+        assert torch.equal(h.cpu(), want[0])
+        assert_close(y, want[1], BF16_TOL, f"ln seg {rows}x{cols} h-and-y")
 
 
 def test_layernorm_k4096_kernel(rocm_device):

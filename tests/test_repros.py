@@ -83,7 +83,7 @@ def test_repro_contract(rid):
 # structure, checked against independent formulations)
 # ---------------------------------------------------------------------------
 
-from conftest import VARIANT_IDS  # noqa: E402
+from conftest import LN_FAMILY_OUTPUTS, VARIANT_IDS  # noqa: E402
 
 bf = torch.bfloat16
 
@@ -125,6 +125,41 @@ def test_plain_softmax_family_repro():
         x, [2, 3, 5, 12], [2, 3, 5, 12], [6, 5, 12])
     assert y.shape == (6, 5, 12) and y.dtype == bf
     assert torch.equal(y, torch.softmax(x.float(), -1).to(bf))
+
+
+@pytest.mark.parametrize("rid", sorted(LN_FAMILY_OUTPUTS))
+def test_residual_layernorm_family_repros(rid):
+    """Each residual-LayerNorm family repro at a small shape of its own
+    signature: outputs (count, shape, aliasing) as LN_FAMILY_OUTPUTS says,
+    values against F.layer_norm of the bf16 sum in fp32."""
+    mod = load_repro_module(CANONICAL / rid)
+    kind = LN_FAMILY_OUTPUTS[rid]
+    g = torch.Generator().manual_seed(sum(map(ord, rid)))
+    b, t, c = 2, 3, 64
+    two_d = rid == "var_mean_ee167627f636"
+    x = torch.randn(b * t, c, generator=g).to(bf)
+    r = (torch.randn(b * t, c, generator=g) if two_d else torch.randn(b, t, c, generator=g)).to(bf)
+    w, beta = torch.randn(c, generator=g).to(bf), torch.randn(c, generator=g).to(bf)
+    nshape = {"y2": 2, "h_y2": 2, "h_y2x3": 4, "y3_y2x3": 4, "y3_y2": 2}[kind]
+    shapes = [[b, t, c]] + [[b * t, c]] * (nshape - 1)
+    out = get_repro_instance(CANONICAL / rid)(x, r, w, beta, *shapes)
+    out = list(out) if isinstance(out, tuple) else [out]
+    h = (x.view(b, t, c) + r.view(b, t, c))
+    y = F.layer_norm(h.float(), [c], w.float(), beta.float(), mod.EPS).to(bf)
+    close = lambda a, e: (a.float() - e.float()).abs().max() <= 1.6e-2 * e.float().abs().max()
+    if kind.startswith("h_"):
+        assert torch.equal(out[0], h.view(r.shape)) and out[0].shape == r.shape
+        ys = out[1:]
+    else:
+        ys = out
+    assert len(ys) == {"y2": 1, "h_y2": 1, "h_y2x3": 3, "y3_y2x3": 4, "y3_y2": 2}[kind]
+    for k, yk in enumerate(ys):
+        assert yk.dtype == bf and close(yk.reshape(b, t, c), y)
+        if kind.startswith("y3") and k == 0:
+            assert yk.shape == (b, t, c)
+        else:
+            assert yk.shape == (b * t, c)
+    assert len({yk.data_ptr() for yk in ys}) == 1, "the y outputs are views of one tensor"
 
 
 def test_longformer_layernorm_family_repro():
