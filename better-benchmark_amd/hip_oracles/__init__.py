@@ -22,7 +22,7 @@ import torch  # imported before the .so so the process has one HIP runtime
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libhip_oracles.so"
 HEADER_PATH = PKG_DIR.parents[1] / "include" / "hip_oracles.h"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c_i64 = ctypes.c_int64
 _c_ptr = ctypes.c_void_p
@@ -44,7 +44,7 @@ _SIGNATURES = {
     "hipo_rmsnorm_bf16": (
         ctypes.c_int, [_c_ptr] * 4 + [_c_i64, _c_i64, _c_f32, _c_ptr]),
     "hipo_rmsnorm_ex_bf16": (
-        ctypes.c_int, [_c_ptr] * 5 + [_c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int, _c_ptr]),
+        ctypes.c_int, [_c_ptr] * 6 + [_c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int, _c_ptr]),
     "hipo_scaled_bias_softmax_bf16": (
         ctypes.c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32,
@@ -346,11 +346,12 @@ def rmsnorm(x, gamma, eps: float):
 
 
 def rmsnorm_ex(x, gamma, eps: float, *, residual=None, scale: float = 1.0, mode: int = 0,
-               want_rstd: bool = False):
+               want_rstd: bool = False, want_h: bool = False):
     """RMSNorm over the last dim with an optional residual (h = bf16(x + r)),
     an output scale and the eager rounding order: mode 0 = torch rms_norm
     (one rounding), mode 1 = HF T5 (bf16(h*rstd), then *gamma, then *scale,
-    each rounded).  Returns y, or (y, rstd) with want_rstd."""
+    each rounded).  Returns y, or (y, rstd) with want_rstd; with want_h
+    (needs a residual) h comes first: (h, y) or (h, y, rstd)."""
     lib = load_library()
     ops = (x, gamma) if residual is None else (x, gamma, residual)
     dev = _require_rocm(*ops)
@@ -362,14 +363,18 @@ def rmsnorm_ex(x, gamma, eps: float, *, residual=None, scale: float = 1.0, mode:
     _require(gamma.shape == (cols,), "rmsnorm_ex: gamma must be [C]")
     _require(residual is None or residual.shape == x.shape, "rmsnorm_ex: residual [R, C]")
     _require(mode in (0, 1), "rmsnorm_ex: mode must be 0 or 1")
+    _require(not want_h or residual is not None, "rmsnorm_ex: h needs a residual")
     y = torch.empty_like(x)
+    h = torch.empty_like(x) if want_h else None
     rstd = torch.empty(rows, dtype=torch.float32, device=dev) if want_rstd else None
     with torch.cuda.device(dev):
         _check(lib.hipo_rmsnorm_ex_bf16(
-            _ptr(x), None if residual is None else _ptr(residual), _ptr(gamma), _ptr(y),
-            None if rstd is None else _ptr(rstd), rows, cols, float(eps), float(scale),
-            int(mode), _stream(dev)), "rmsnorm_ex")
-    return (y, rstd) if want_rstd else y
+            _ptr(x), None if residual is None else _ptr(residual), _ptr(gamma),
+            None if h is None else _ptr(h), _ptr(y), None if rstd is None else _ptr(rstd),
+            rows, cols, float(eps), float(scale), int(mode), _stream(dev)), "rmsnorm_ex")
+    out = (y, rstd) if want_rstd else (y,)
+    out = ((h,) + out) if want_h else out
+    return out if len(out) > 1 else out[0]
 
 
 def scaled_bias_softmax(x, bias, scale: float, heads: int):

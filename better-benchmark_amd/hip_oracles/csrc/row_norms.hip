@@ -126,7 +126,7 @@ __global__ __launch_bounds__(kRowMaxThreads) void residual_layernorm_rows(
 template <int U, int WT, bool RES, int MODE>
 __global__ __launch_bounds__(kRowMaxThreads) void rmsnorm_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
-    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ h, uint16_t* __restrict__ y,
     float* __restrict__ rstd_out, int64_t rows, int64_t cols, float eps,
     float scale, int w_arg, int rpb_arg) {
   const int waves_per_row = WT > 0 ? WT : w_arg;
@@ -148,6 +148,8 @@ __global__ __launch_bounds__(kRowMaxThreads) void rmsnorm_rows(
       for (int d = 0; d < 4; ++d)
         xv[u][d] = pack_bf16x2(bf16lo(xv[u][d]) + bf16lo(rv[d]),
                                bf16hi(xv[u][d]) + bf16hi(rv[d]));
+      const int64_t col = row_group_col(u, waves_per_row, p);
+      if (h != nullptr && p.valid && col < cols) row_store_stream(h + base, col, xv[u]);
     }
   }
   float sq = 0.f;
@@ -252,7 +254,7 @@ __global__ __launch_bounds__(256) void residual_layernorm_rows_scalar(
 
 __global__ __launch_bounds__(256) void rmsnorm_rows_scalar(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
-    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ gamma, uint16_t* __restrict__ h, uint16_t* __restrict__ y,
     float* __restrict__ rstd_out, int64_t rows, int64_t cols, float eps,
     float scale, int mode) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -267,6 +269,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_scalar(
   for (int64_t j = lane; j < cols; j += kWave) {
     const float a = hval(j);
     sq = __builtin_fmaf(a, a, sq);
+    if (h != nullptr) h[base + j] = static_cast<uint16_t>(pack_bf16x2(a, 0.f) & 0xffffu);
   }
   const float rstd =
       1.0f / __builtin_sqrtf(wave_sum(sq) / static_cast<float>(cols) + eps);
@@ -607,47 +610,48 @@ namespace {
 template <bool RES, int MODE>
 void launch_rmsnorm(const RowPlan& plan, dim3 grid, hipStream_t stream,
                     const uint16_t* x, const uint16_t* residual,
-                    const uint16_t* gamma, uint16_t* y, float* rstd,
+                    const uint16_t* gamma, uint16_t* h, uint16_t* y, float* rstd,
                     int64_t rows, int64_t cols, float eps, float scale) {
   const dim3 block(plan.threads());
   const int w = plan.waves_per_row, r = plan.rows_per_block;
 #define HIPO_RMS(U_, W_)                                            \
   rmsnorm_rows<U_, W_, RES, MODE><<<grid, block, 0, stream>>>(      \
-      x, residual, gamma, y, rstd, rows, cols, eps, scale, w, r)
+      x, residual, gamma, h, y, rstd, rows, cols, eps, scale, w, r)
   HIPO_ROW_DISPATCH(plan, HIPO_RMS);
 #undef HIPO_RMS
 }
 
 int rmsnorm_impl(const uint16_t* x, const uint16_t* residual, const uint16_t* gamma,
-                 uint16_t* y, float* rstd, int64_t rows, int64_t cols, float eps,
-                 float scale, int mode, bool require_rstd, hipStream_t stream,
+                 uint16_t* h, uint16_t* y, float* rstd, int64_t rows, int64_t cols,
+                 float eps, float scale, int mode, bool require_rstd, hipStream_t stream,
                  const char* what) {
   clear_error();
   HIPO_REQUIRE(rows >= 0 && cols >= 0, "%s: negative size", what);
   if (rows == 0) return 0;
   HIPO_REQUIRE(cols > 0, "%s: cols must be > 0", what);
   HIPO_REQUIRE(x && gamma && y && (rstd || !require_rstd), "%s: null pointer", what);
+  HIPO_REQUIRE(h == nullptr || residual != nullptr, "%s: h needs a residual", what);
   HIPO_REQUIRE(mode == 0 || mode == 1, "%s: mode must be 0 or 1", what);
   RowPlan plan;
   const bool vec = cols % 8 == 0 && row_plan(cols, plan) && aligned16(x) &&
                    aligned16(gamma) && aligned16(y) &&
-                   (residual == nullptr || aligned16(residual));
+                   (residual == nullptr || aligned16(residual)) && (h == nullptr || aligned16(h));
   if (vec) {
     const int64_t blocks = (rows + plan.rows_per_block - 1) / plan.rows_per_block;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);
     const dim3 grid(static_cast<unsigned>(blocks));
     if (residual != nullptr) {
-      if (mode == 0) launch_rmsnorm<true, 0>(plan, grid, stream, x, residual, gamma, y, rstd, rows, cols, eps, scale);
-      else launch_rmsnorm<true, 1>(plan, grid, stream, x, residual, gamma, y, rstd, rows, cols, eps, scale);
+      if (mode == 0) launch_rmsnorm<true, 0>(plan, grid, stream, x, residual, gamma, h, y, rstd, rows, cols, eps, scale);
+      else launch_rmsnorm<true, 1>(plan, grid, stream, x, residual, gamma, h, y, rstd, rows, cols, eps, scale);
     } else {
-      if (mode == 0) launch_rmsnorm<false, 0>(plan, grid, stream, x, residual, gamma, y, rstd, rows, cols, eps, scale);
-      else launch_rmsnorm<false, 1>(plan, grid, stream, x, residual, gamma, y, rstd, rows, cols, eps, scale);
+      if (mode == 0) launch_rmsnorm<false, 0>(plan, grid, stream, x, residual, gamma, nullptr, y, rstd, rows, cols, eps, scale);
+      else launch_rmsnorm<false, 1>(plan, grid, stream, x, residual, gamma, nullptr, y, rstd, rows, cols, eps, scale);
     }
   } else {
     const int64_t blocks = (rows + 3) / 4;
     HIPO_REQUIRE(blocks <= 0x7fffffff, "%s: too many rows", what);
     rmsnorm_rows_scalar<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
-        x, residual, gamma, y, rstd, rows, cols, eps, scale, mode);
+        x, residual, gamma, h, y, rstd, rows, cols, eps, scale, mode);
   }
   return check_launch(what);
 }
@@ -658,15 +662,15 @@ int rmsnorm_impl(const uint16_t* x, const uint16_t* residual, const uint16_t* ga
 extern "C" int hipo_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma,
                                  uint16_t* y, float* rstd, int64_t rows,
                                  int64_t cols, float eps, hipStream_t stream) {
-  return hipo::rmsnorm_impl(x, nullptr, gamma, y, rstd, rows, cols, eps, 1.0f, 0, true,
-                            stream, "rmsnorm_bf16");
+  return hipo::rmsnorm_impl(x, nullptr, gamma, nullptr, y, rstd, rows, cols, eps, 1.0f, 0,
+                            true, stream, "rmsnorm_bf16");
 }
 
 extern "C" int hipo_rmsnorm_ex_bf16(const uint16_t* x, const uint16_t* residual,
-                                    const uint16_t* gamma, uint16_t* y,
+                                    const uint16_t* gamma, uint16_t* h, uint16_t* y,
                                     float* rstd, int64_t rows, int64_t cols,
                                     float eps, float scale, int mode,
                                     hipStream_t stream) {
-  return hipo::rmsnorm_impl(x, residual, gamma, y, rstd, rows, cols, eps, scale, mode, false,
-                            stream, "rmsnorm_ex_bf16");
+  return hipo::rmsnorm_impl(x, residual, gamma, h, y, rstd, rows, cols, eps, scale, mode,
+                            false, stream, "rmsnorm_ex_bf16");
 }

@@ -1,0 +1,38 @@
+"""
+MI355X oracle for mean_f21cc667fe83: residual add + RMSNorm over the last
+dim (eps 1e-05), returning the bf16 sum h and 1 view of y.
+
+Kernel: hipo_rmsnorm_ex_bf16, mode 0 (bf16(gamma * h * rstd), one rounding) -- h = bf16(x +
+residual) held in registers between its sum of squares and its output, W
+waves per row.  Algorithmic bytes per row of C: 2C (x) + 2C (residual) +
+2C (y) + 2C (h).
+Replaces the Triton body of the reference's
+repros/canonical/mean_f21cc667fe83/oracle.py:56.
+"""
+import sys
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+import hip_oracles  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
+
+EPS = 1e-05
+
+
+@oracle_impl(hardware="MI355X", point="533b2091",
+             description="residual RMSNorm, 1000 x 2880")
+@oracle_impl(hardware="MI355X", description="residual RMSNorm, shape-general")
+def oracle_forward(inputs):
+    x, residual, gamma = inputs[:3]
+    shapes = inputs[3:]
+    cols = x.shape[-1]
+    out = hip_oracles.rmsnorm_ex(x.reshape(-1, cols), gamma, EPS,
+                                 residual=residual.reshape(-1, cols), mode=0,
+                                 want_h=True)
+    h, y = out
+    return (h.view(residual.shape),
+            y.view(tuple(int(d) for d in shapes[1])))
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

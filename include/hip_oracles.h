@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define HIPO_ABI_VERSION 1
+#define HIPO_ABI_VERSION 2
 #define HIPO_EINVAL 1000
 
 /* ABI version of the loaded library (HIPO_ABI_VERSION at build time). */
@@ -130,13 +130,18 @@ int hipo_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma, uint16_t* y,
  *   mode 0: y = bf16(h * rstd * gamma * scale)  (torch rms_norm, one rounding)
  *   mode 1: t = bf16(h * rstd); u = bf16(gamma * t);
  *           y = scale == 1 ? u : bf16(u * scale)   (HF T5 LayerNorm op order)
- * residual and rstd may be NULL.  Shapes as hipo_rmsnorm_bf16.
+ * residual, h and rstd may be NULL (h, the bf16 sum, only with a
+ * residual).  Shapes as hipo_rmsnorm_bf16.
  * Replaces the Triton body of oracle_forward in
  * repros/canonical/mean_4462ce967d63/oracle.py:65 (T5: residual, eps 1e-6,
- * mode 1, scale 0.04419417382415922).
+ * mode 1, scale 0.04419417382415922) and of the residual-RMSNorm families
+ * mean_f08c75b5f21f, mean_db9733790220, mean_8818e35b12aa,
+ * mean_c033ad4c69ca, mean_f21cc667fe83 (mode 0), mean_426e2409482e,
+ * mean_4dace6865eee, mean_bf2ed36e56df, mean_d28c6a07654f and
+ * mean_41e8bba10b8b (oracle.py, oracle_forward).
  */
 int hipo_rmsnorm_ex_bf16(const uint16_t* x, const uint16_t* residual,
-                         const uint16_t* gamma, uint16_t* y, float* rstd,
+                         const uint16_t* gamma, uint16_t* h, uint16_t* y, float* rstd,
                          int64_t rows, int64_t cols, float eps, float scale,
                          int mode, hipStream_t stream);
 

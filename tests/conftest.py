@@ -36,6 +36,23 @@ LN_FAMILY_OUTPUTS = {
     "var_mean_45f7dfd4a983": "y3_y2",
 }
 
+# Residual add + RMSNorm corpus families on one kernel: (mode, first output,
+# views of y after it) -- mode 1 rounds bf16(h * rstd) before the gamma
+# product, mode 0 once at the end; the first output is h (the bf16 sum), y
+# ([b, s, C]) or nothing; the views use the graph's shape parameters 1..n.
+RMS_FAMILY_OUTPUTS = {
+    "mean_f08c75b5f21f": (1, "", 1),
+    "mean_db9733790220": (1, "", 1),
+    "mean_8818e35b12aa": (1, "h", 1),
+    "mean_c033ad4c69ca": (1, "h", 3),
+    "mean_f21cc667fe83": (0, "h", 1),
+    "mean_426e2409482e": (1, "y", 16),
+    "mean_4dace6865eee": (1, "y", 12),
+    "mean_bf2ed36e56df": (1, "h", 3),
+    "mean_d28c6a07654f": (1, "h", 2),
+    "mean_41e8bba10b8b": (1, "h", 2),
+}
+
 # Corpus families the kernels generalise to (the reference's canonical dir
 # names, their shape points and model counts).
 VARIANT_IDS = [
@@ -49,7 +66,7 @@ VARIANT_IDS = [
     "pointwise_021e90d9c17d",
     "mean_b402ee209d0b",
     "amax_sum_fa4cc85fe5ad",
-] + list(LN_FAMILY_OUTPUTS)
+] + list(LN_FAMILY_OUTPUTS) + list(RMS_FAMILY_OUTPUTS)
 
 
 def pytest_configure(config):

@@ -33,7 +33,7 @@ def test_exported_names_match_header():
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.hipo_abi_version() == hip_oracles.ABI_VERSION == 1
+    assert lib.hipo_abi_version() == hip_oracles.ABI_VERSION == 2
     assert lib.hipo_last_error() == b""
 
 
@@ -47,8 +47,9 @@ def test_abi_version_and_error_string(lib):
                                               4, 0, 1e-5, None), b"cols"),
     (lambda l: l.hipo_rmsnorm_bf16(None, None, None, None, -2, 8, 1e-5, None), b"negative"),
     (lambda l: l.hipo_rmsnorm_bf16(1, 1, 1, None, 2, 8, 1e-5, None), b"null"),
-    (lambda l: l.hipo_rmsnorm_ex_bf16(1, None, 1, 1, None, 2, 8, 1e-5, 1.0, 2, None), b"mode"),
-    (lambda l: l.hipo_rmsnorm_ex_bf16(None, None, 1, 1, None, 2, 8, 1e-5, 1.0, 0, None), b"null"),
+    (lambda l: l.hipo_rmsnorm_ex_bf16(1, None, 1, None, 1, None, 2, 8, 1e-5, 1.0, 2, None), b"mode"),
+    (lambda l: l.hipo_rmsnorm_ex_bf16(1, None, 1, 1, 1, None, 2, 8, 1e-5, 1.0, 0, None), b"residual"),
+    (lambda l: l.hipo_rmsnorm_ex_bf16(None, None, 1, None, 1, None, 2, 8, 1e-5, 1.0, 0, None), b"null"),
     (lambda l: l.hipo_scaled_bias_softmax_bf16(1, 1, 1, 6, 4, 8, 8, 0, 4, 1.0, None), b"heads"),
     (lambda l: l.hipo_scaled_bias_softmax_bf16(1, 1, 1, 6, 4, 8, 8, -8, 3, 1.0, None),
      b"mask_batch_stride"),
@@ -89,7 +90,7 @@ def test_empty_inputs_are_no_ops(lib):
     assert lib.hipo_bias_gelu_nchw_to_nhwc_bf16(None, None, None, 0, 8, 8, None) == 0
     assert lib.hipo_scaled_masked_softmax_bf16(None, None, None, 3, 0, 8, 8, 1.0, None) == 0
     assert lib.hipo_scaled_bias_softmax_bf16(None, None, None, 0, 4, 8, 8, 0, 1, 1.0, None) == 0
-    assert lib.hipo_rmsnorm_ex_bf16(None, None, None, None, None, 0, 8, 1e-5, 1.0, 0, None) == 0
+    assert lib.hipo_rmsnorm_ex_bf16(None, None, None, None, None, None, 0, 8, 1e-5, 1.0, 0, None) == 0
     assert lib.hipo_spatial_mean_nhwc_bf16(None, None, 0, 64, 8, None, 0, None) == 0
     assert lib.hipo_batchnorm_nhwc_act_pad_bf16(*[None] * 8, 2, 4, 4, 0, 1, 1, 0.1, 1e-3, 1.0, 2,
                                                 None, 0, None) == 0

@@ -21,7 +21,8 @@ import math
 import pytest
 import torch
 
-from conftest import CANONICAL, LN_FAMILY_OUTPUTS, REPRO_IDS, VARIANT_IDS
+from conftest import (CANONICAL, LN_FAMILY_OUTPUTS, REPRO_IDS, RMS_FAMILY_OUTPUTS,
+                      VARIANT_IDS)
 
 pytestmark = pytest.mark.gpu
 
@@ -170,6 +171,23 @@ def _ln_family_outputs(rid, i):
     return [y.view(shapes[0]), y.view(shapes[1])]
 
 
+def _rms_family_outputs(rid, i):
+    """The C oracle's h and y arranged as the residual RMSNorm family rid
+    returns them (conftest.RMS_FAMILY_OUTPUTS)."""
+    import oracle as ref
+    from oracle_harness import load_repro_module
+    eps = load_repro_module(CANONICAL / rid).EPS
+    mode, first, nviews = RMS_FAMILY_OUTPUTS[rid]
+    x, r, g = i[:3]
+    shapes = [tuple(int(d) for d in s) for s in i[3:]]
+    cols = x.shape[-1]
+    x2, r2 = x.reshape(-1, cols), r.reshape(-1, cols)
+    y = ref.rmsnorm_ex(x2, g, eps, residual=r2, mode=mode)[0]
+    h = (x2.float() + r2.float()).to(torch.bfloat16)  # one bf16 rounding, as the graph's add
+    outs = [h.view(r.shape)] if first == "h" else [y.view(r.shape)] if first == "y" else []
+    return outs + [y.view(shapes[j]) for j in range(1, nviews + 1)]
+
+
 def _family_oracle(rid, i):
     """The C oracle's outputs for a family point's CPU inputs."""
     import oracle as ref
@@ -193,6 +211,8 @@ def _family_oracle(rid, i):
         return [ref.row_mean_bf16(x.reshape(x.shape[0] * x.shape[1], -1), relu=True)]
     if rid in LN_FAMILY_OUTPUTS:
         return _ln_family_outputs(rid, i)
+    if rid in RMS_FAMILY_OUTPUTS:
+        return _rms_family_outputs(rid, i)
     if rid == "amax_sum_fa4cc85fe5ad":
         x = i[0]
         k = x.shape[-1]
@@ -807,6 +827,12 @@ def test_rmsnorm_ex_modes(rocm_device):
                 x.to(rocm_device), gm.to(rocm_device), eps, scale=scale, mode=mode,
                 residual=None if residual is None else residual.to(rocm_device))
             assert torch.equal(y2.cpu(), y.cpu()), what + ": rstd=NULL changes y"
+            if residual is not None:
+                h3, y3 = hip_oracles.rmsnorm_ex(
+                    x.to(rocm_device), gm.to(rocm_device), eps, scale=scale, mode=mode,
+                    residual=residual.to(rocm_device), want_h=True)
+                assert torch.equal(h3.cpu(), x + residual), what + ": h"
+                assert torch.equal(y3.cpu(), y.cpu()), what + ": writing h changes y"
     # closed form: rows of a constant c have rstd = 1/sqrt(c^2 + eps) and, in
     # mode 1 with gamma = 1, y = bf16(c * rstd) * scale rounded
     x = torch.full((4, 512), 3.0, dtype=bf)

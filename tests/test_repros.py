@@ -83,7 +83,7 @@ def test_repro_contract(rid):
 # structure, checked against independent formulations)
 # ---------------------------------------------------------------------------
 
-from conftest import LN_FAMILY_OUTPUTS, VARIANT_IDS  # noqa: E402
+from conftest import LN_FAMILY_OUTPUTS, RMS_FAMILY_OUTPUTS, VARIANT_IDS  # noqa: E402
 
 bf = torch.bfloat16
 
@@ -160,6 +160,39 @@ def test_residual_layernorm_family_repros(rid):
         else:
             assert yk.shape == (b * t, c)
     assert len({yk.data_ptr() for yk in ys}) == 1, "the y outputs are views of one tensor"
+
+
+@pytest.mark.parametrize("rid", sorted(RMS_FAMILY_OUTPUTS))
+def test_residual_rmsnorm_family_repros(rid):
+    """Each residual-RMSNorm family repro at a small shape of its signature:
+    outputs as RMS_FAMILY_OUTPUTS says (h exact, the y views of one tensor),
+    y against the graph's op order written out in fp32 / bf16."""
+    mod = load_repro_module(CANONICAL / rid)
+    mode, first, nviews = RMS_FAMILY_OUTPUTS[rid]
+    g = torch.Generator().manual_seed(sum(map(ord, rid)))
+    b, t, c = 2, 3, 64
+    x = torch.randn(b * t, c, generator=g).to(bf)
+    r = torch.randn(b, t, c, generator=g).to(bf)
+    w = torch.randn(c, generator=g).to(bf)
+    shapes = [[b, t, c]] + [[b * t, c]] * nviews
+    out = get_repro_instance(CANONICAL / rid)(x, r, w, *shapes)
+    out = list(out) if isinstance(out, tuple) else [out]
+    h = x.view(b, t, c) + r
+    rstd = torch.rsqrt(h.float().pow(2).mean(-1, keepdim=True) + mod.EPS)
+    if mode == 1:
+        y = w * (h.float() * rstd).to(bf)
+    else:
+        y = (w.float() * (h.float() * rstd)).to(bf)
+    assert len(out) == (1 if first else 0) + nviews
+    if first == "h":
+        assert torch.equal(out[0], h)
+    elif first == "y":
+        assert torch.equal(out[0], y)
+    views = out[1:] if first else out
+    for v in views:
+        assert v.shape == (b * t, c) and torch.equal(v, y.view(b * t, c))
+    ys = [o for o in out if not (first == "h" and o is out[0])]
+    assert len({o.data_ptr() for o in ys}) == 1, "the y outputs are views of one tensor"
 
 
 def test_longformer_layernorm_family_repro():
