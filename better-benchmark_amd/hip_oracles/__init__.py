@@ -73,6 +73,9 @@ _SIGNATURES = {
     "hipo_transpose_last2": (
         ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_ptr]),
     "hipo_row_mean_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, ctypes.c_int, _c_ptr]),
+    "hipo_gelu_erf_bwd_colsum_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64]),
+    "hipo_gelu_erf_bwd_colsum_bf16": (
+        ctypes.c_int, [_c_ptr] * 4 + [_c_i64, _c_i64, _c_ptr, ctypes.c_size_t, _c_ptr]),
     "hipo_batchnorm_train_fwd_f32_noalloc": (
         ctypes.c_int,
         [_c_ptr] * 8 + [_c_i64, _c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int, _c_ptr]),
@@ -233,6 +236,30 @@ def row_mean_bf16(x: torch.Tensor, *, relu: bool = False) -> torch.Tensor:
         _check(lib.hipo_row_mean_bf16(_ptr(x), _ptr(out), rows, cols, 1 if relu else 0,
                                       _stream(dev)), "row_mean_bf16")
     return out
+
+
+def gelu_erf_bwd_colsum(grad: torch.Tensor, x: torch.Tensor):
+    """GELU(erf) backward and its column sum for contiguous 2-D bf16 grad and
+    x [rows, cols] (cols a multiple of 8): y = bf16(grad * d(x)) with d the
+    correctly rounded fp32 GELU'(x), and colsum = bf16(sum over rows of y)
+    as fp32.  Returns (y [rows, cols] bf16, colsum [cols] fp32)."""
+    lib = load_library()
+    dev = _require_rocm(grad, x)
+    _require(grad.dtype == torch.bfloat16 and x.dtype == torch.bfloat16,
+             "gelu_erf_bwd: bf16 operands required")
+    _require(grad.dim() == 2 and grad.shape == x.shape and grad.is_contiguous()
+             and x.is_contiguous(), "gelu_erf_bwd: grad and x must be contiguous [rows, cols]")
+    rows, cols = x.shape
+    _require(cols % 8 == 0, "gelu_erf_bwd: cols must be a multiple of 8")
+    y = torch.empty((rows, cols), dtype=torch.bfloat16, device=dev)
+    colsum = torch.empty(cols, dtype=torch.float32, device=dev)
+    need = int(lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(rows, cols))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
+    with torch.cuda.device(dev):
+        _check(lib.hipo_gelu_erf_bwd_colsum_bf16(
+            _ptr(grad), _ptr(x), _ptr(y), _ptr(colsum), rows, cols,
+            None if ws is None else _ptr(ws), need, _stream(dev)), "gelu_erf_bwd_colsum")
+    return y, colsum
 
 
 def scaled_masked_softmax(x: torch.Tensor, mask: torch.Tensor, scale: float) -> torch.Tensor:
@@ -650,4 +677,5 @@ __all__ = [
     "batchnorm_workspace_bytes", "batchnorm_train",
     "batchnorm_cached_workspace", "batchnorm_error_flag", "BN_ERROR_WORD_OFFSET",
     "HipOraclesDeviceFault", "device_faults", "raise_on_device_faults", "flat_copy",
+    "gelu_erf_bwd_colsum",
 ]

@@ -39,6 +39,7 @@ SOURCES = [
     "flat_copy.hip",
     "gelu_flat.hip",
     "transpose.hip",
+    "gelu_bwd.hip",
 ]
 
 # Packed-FP32 VALU forms are disabled for all device code (the compiler

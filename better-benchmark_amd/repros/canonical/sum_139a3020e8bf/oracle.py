@@ -1,0 +1,62 @@
+"""
+MI355X oracle for sum_139a3020e8bf: the gradient through an erf GELU, y = bf16(grad *
+GELU'(x)), returned with its transpose view, and its column sum (the bias
+gradient) rounded to bf16 and stored as fp32.
+
+Kernel: hipo_gelu_erf_bwd_colsum_bf16 -- GELU'(x) read from an LDS table of
+its correctly rounded fp32 value at every bf16 x, one fp32 product per
+element, y written once and its column partials accumulated from the bf16 y
+in the same pass (fp32, one row per row block), then a second launch adds
+the partials in a fixed order.  Algorithmic bytes: 2 R C (grad) + 2 R C (x)
++ 2 R C (y) + 4 C (colsum).
+Replaces the Triton body of the reference's
+repros/canonical/sum_139a3020e8bf/oracle.py:101.
+"""
+import sys
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+import hip_oracles  # noqa: E402
+from oracle_harness import oracle_impl, oracle_main  # noqa: E402
+
+
+@oracle_impl(hardware="MI355X", point="8572c66c",
+             description="GELU(erf) bwd + column sum, 25216 x 3072")
+@oracle_impl(hardware="MI355X", point="9448cee8",
+             description="GELU(erf) bwd + column sum, 25216 x 768")
+@oracle_impl(hardware="MI355X", point="5c6c31bb",
+             description="GELU(erf) bwd + column sum, 25344 x 3072")
+@oracle_impl(hardware="MI355X", point="3f451298",
+             description="GELU(erf) bwd + column sum, 175360 x 3072")
+@oracle_impl(hardware="MI355X", point="c064ba70",
+             description="GELU(erf) bwd + column sum, 32768 x 3072")
+@oracle_impl(hardware="MI355X", point="67c7a377",
+             description="GELU(erf) bwd + column sum, 128 x 3072")
+@oracle_impl(hardware="MI355X", point="8951d544",
+             description="GELU(erf) bwd + column sum, 8192 x 4096")
+@oracle_impl(hardware="MI355X", point="a448a1c6",
+             description="GELU(erf) bwd + column sum, 4096 x 10240")
+@oracle_impl(hardware="MI355X", point="5d96adde",
+             description="GELU(erf) bwd + column sum, 2048 x 10240")
+@oracle_impl(hardware="MI355X", point="63ec809a",
+             description="GELU(erf) bwd + column sum, 4096 x 6144")
+@oracle_impl(hardware="MI355X", point="05a5e903",
+             description="GELU(erf) bwd + column sum, 16384 x 3072")
+@oracle_impl(hardware="MI355X", point="7c6aa97f",
+             description="GELU(erf) bwd + column sum, 32768 x 1024")
+@oracle_impl(hardware="MI355X", point="58ff2bc5",
+             description="GELU(erf) bwd + column sum, 8192 x 3072")
+@oracle_impl(hardware="MI355X", point="6a0c3b2c",
+             description="GELU(erf) bwd + column sum, 16384 x 4096")
+@oracle_impl(hardware="MI355X", point="7c4310e0",
+             description="GELU(erf) bwd + column sum, 4096 x 4096")
+@oracle_impl(hardware="MI355X", description="GELU(erf) bwd + column sum, shape-general")
+def oracle_forward(inputs):
+    grad, x, _shape0, _shape1, shape2, shape3 = inputs
+    rows, cols = int(shape2[0]), int(shape2[1])
+    y, colsum = hip_oracles.gelu_erf_bwd_colsum(grad.view(rows, cols), x.view(rows, cols))
+    return (y, y.permute(1, 0), colsum.view(tuple(int(d) for d in shape3)))
+
+
+if __name__ == "__main__":
+    raise SystemExit(oracle_main(__file__, oracle_forward))

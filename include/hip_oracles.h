@@ -364,6 +364,32 @@ int hipo_transpose_last2(const void* x, void* y, int64_t batch, int64_t rows,
 int hipo_row_mean_bf16(const uint16_t* x, uint16_t* out, int64_t rows, int64_t cols,
                        int relu, hipStream_t stream);
 
+/* Workspace bytes of hipo_gelu_erf_bwd_colsum_bf16 (0: empty shape). */
+size_t hipo_gelu_erf_bwd_colsum_workspace_bytes(int64_t rows, int64_t cols);
+
+/*
+ * GELU(erf) backward with the column sum of its output (a bias gradient):
+ *   y[r, c]   = bf16(grad[r, c] * d(x[r, c])),
+ *               d(t) = Phi(t) + t phi(t), the derivative of t Phi(t), taken
+ *               as the correctly rounded fp32 value for each bf16 t (one
+ *               fp32 product, one rounding; inf and NaN t give NaN);
+ *   colsum[c] = bf16(sum_r y[r, c]) stored as fp32 (fp32 sums of the bf16 y,
+ *               in a fixed order for a given shape).
+ * grad, x, y are contiguous [rows, cols] bf16, 16-byte aligned, cols a
+ * multiple of 8; colsum is [cols] fp32.  `workspace` holds fp64 partial sums:
+ * at least hipo_gelu_erf_bwd_colsum_workspace_bytes(rows, cols) bytes,
+ * 16-byte aligned, no initialisation needed; NULL when that is 0 (up to 256
+ * rows, a single launch; rows == 0 sets colsum to zero).
+ * Replaces the Triton body of oracle_forward in
+ * repros/canonical/sum_139a3020e8bf/oracle.py:101-152
+ * (_materialize_partial_kernel :13, _final_sum_kernel :62) for the graph of
+ * repros/canonical/sum_139a3020e8bf/repro.py:24-48.
+ */
+int hipo_gelu_erf_bwd_colsum_bf16(const uint16_t* grad, const uint16_t* x, uint16_t* y,
+                                  float* colsum, int64_t rows, int64_t cols,
+                                  void* workspace, size_t workspace_bytes,
+                                  hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -49,6 +49,8 @@ _SIGS = {
     "ref_gelu_tanh_f32": (None, [_p, _p, _i64, _i]),
     "ref_transpose_last2": (None, [_p, _p, _i64, _i64, _i64, _i, _i]),
     "ref_row_mean_bf16": (None, [_p, _p, _i64, _i64, _i, _i]),
+    "ref_gelu_erf_grad_f32": (None, [_p, _p, _i64, _i]),
+    "ref_gelu_erf_bwd_colsum_bf16": (None, [_p] * 4 + [_i64, _i64, _i]),
 }
 
 _ACTS = {None: 0, "none": 0, "relu": 1, "silu": 2}
@@ -274,3 +276,27 @@ def row_mean_bf16(x, *, relu: bool = False, threads=None):
     load().ref_row_mean_bf16(x.data_ptr(), out.data_ptr(), rows, cols, 1 if relu else 0,
                              _th(threads))
     return out
+
+
+def gelu_erf_grad(x, threads=None):
+    """The fp32 derivative of GELU(erf), Phi(t) + t phi(t), of every element
+    of a bf16 tensor: fp64, one rounding; same shape."""
+    x = _cpu(x, torch.bfloat16)
+    d = torch.empty(x.shape, dtype=torch.float32)
+    load().ref_gelu_erf_grad_f32(x.data_ptr(), d.data_ptr(), x.numel(), _th(threads))
+    return d
+
+
+def gelu_erf_bwd_colsum(grad, x, threads=None):
+    """(y, colsum) of the GELU(erf) backward + column sum graph for 2-D bf16
+    grad and x: y = bf16(grad * d(x)) with the fp32 d above, colsum =
+    bf16(fp64 sum over rows of y) as fp32."""
+    grad = _cpu(grad, torch.bfloat16)
+    x = _cpu(x, torch.bfloat16)
+    assert grad.shape == x.shape and x.dim() == 2, (grad.shape, x.shape)
+    rows, cols = x.shape
+    y = torch.empty((rows, cols), dtype=torch.bfloat16)
+    colsum = torch.empty(cols, dtype=torch.float32)
+    load().ref_gelu_erf_bwd_colsum_bf16(grad.data_ptr(), x.data_ptr(), y.data_ptr(),
+                                        colsum.data_ptr(), rows, cols, _th(threads))
+    return y, colsum

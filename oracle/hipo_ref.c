@@ -24,6 +24,7 @@
  *   T5 residual RMSNorm           repros/canonical/mean_4462ce967d63/repro.py:23-38
  *   bf16 BN + SiLU + pad (NHWC)   repros/canonical/var_mean_ceb5c315290a/repro.py:27-58
  *   bf16 BN + ReLU + mean (NCHW)  repros/canonical/var_mean_mean_19ffdb35cc67/repro.py:23-54
+ *   GELU(erf) bwd + column sum    repros/canonical/sum_139a3020e8bf/repro.py:24-48
  * (paths relative to the reference tree).  Every rounding that the eager
  * graph performs on a bf16 tensor is reproduced (float arithmetic, then
  * round-to-nearest-even to bf16); reductions and transcendental functions
@@ -507,4 +508,53 @@ void ref_row_mean_bf16(const uint16_t* x, uint16_t* out, int64_t rows, int64_t c
     }
     out[r] = f64_to_bf16(s / (double)cols);
   }
+}
+
+/* d(t) = Phi(t) + t phi(t), the derivative of GELU(erf) t Phi(t), in fp64
+ * (Phi through erfc, so the negative tail does not cancel) and rounded once
+ * to fp32; inf and NaN give NaN (as eager's t * exp(-t^2 / 2) = inf * 0). */
+static inline float gelu_erf_grad_f32(float t) {
+  const double td = (double)t;
+  const double cdf = 0.5 * erfc(-td * 0.70710678118654752440);
+  const double pdf = exp(-0.5 * td * td) * 0.39894228040143267794; /* 1 / sqrt(2 pi) */
+  return (float)(cdf + td * pdf);
+}
+
+/* d[i] = the fp32 d(t) above for n bf16 inputs t. */
+void ref_gelu_erf_grad_f32(const uint16_t* x, float* d, int64_t n, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t i = 0; i < n; ++i) d[i] = gelu_erf_grad_f32(bf16_to_f32(x[i]));
+}
+
+/* GELU(erf) backward and the column sum of its output (the graph of
+ * repros/canonical/sum_139a3020e8bf/repro.py:24-48):
+ *   y[r, c]   = bf16(g[r, c] * d(x[r, c]))   (one fp32 product)
+ *   colsum[c] = bf16(sum_r y[r, c]), fp64 sum, one rounding, stored as fp32.
+ * The fp64 sums run over fixed blocks of 1024 rows (in parallel) and then
+ * over the blocks in order: the result does not depend on the thread count. */
+void ref_gelu_erf_bwd_colsum_bf16(const uint16_t* g, const uint16_t* x, uint16_t* y,
+                                  float* colsum, int64_t rows, int64_t cols, int threads) {
+  const int64_t kBlock = 1024;
+  const int64_t nblk = (rows + kBlock - 1) / kBlock;
+  double* part = (double*)calloc((size_t)(nblk > 0 ? nblk : 1) * (size_t)(cols > 0 ? cols : 1),
+                                 sizeof(double));
+  if (part == NULL) abort();
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+  for (int64_t b = 0; b < nblk; ++b) {
+    double* acc = part + b * cols;
+    const int64_t r1 = (b + 1) * kBlock < rows ? (b + 1) * kBlock : rows;
+    for (int64_t r = b * kBlock; r < r1; ++r) {
+      for (int64_t c = 0; c < cols; ++c) {
+        const int64_t i = r * cols + c;
+        y[i] = f32_to_bf16(bf16_to_f32(g[i]) * gelu_erf_grad_f32(bf16_to_f32(x[i])));
+        acc[c] += bf16_to_f32(y[i]);
+      }
+    }
+  }
+  for (int64_t c = 0; c < cols; ++c) {
+    double s = 0.0;
+    for (int64_t b = 0; b < nblk; ++b) s += part[b * cols + c];
+    colsum[c] = bf16_to_f32(f64_to_bf16(s));
+  }
+  free(part);
 }

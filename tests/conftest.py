@@ -66,7 +66,9 @@ VARIANT_IDS = [
     "pointwise_021e90d9c17d",
     "mean_b402ee209d0b",
     "amax_sum_fa4cc85fe5ad",
-] + list(LN_FAMILY_OUTPUTS) + list(RMS_FAMILY_OUTPUTS)
+] + list(LN_FAMILY_OUTPUTS) + list(RMS_FAMILY_OUTPUTS) + [
+    "sum_139a3020e8bf",
+]
 
 
 def pytest_configure(config):

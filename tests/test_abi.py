@@ -79,6 +79,18 @@ def test_abi_version_and_error_string(lib):
                                                    16, 1 << 20, None), b"null"),
     (lambda l: l.hipo_batchnorm_nchw_act_mean_bf16(*[1] * 8, 5, 8, 0, 0.1, 1e-5, 1.0, 1,
                                                    16, 1 << 20, None), b"empty reduction"),
+    (lambda l: l.hipo_gelu_erf_bwd_colsum_bf16(16, 16, 16, 16, 4, 12, 16, 1 << 20, None),
+     b"multiple of 8"),
+    (lambda l: l.hipo_gelu_erf_bwd_colsum_bf16(16, 16, 16, 16, -1, 16, 16, 1 << 20, None),
+     b"negative"),
+    (lambda l: l.hipo_gelu_erf_bwd_colsum_bf16(16, 16, 16, None, 4, 16, 16, 1 << 20, None),
+     b"colsum"),
+    (lambda l: l.hipo_gelu_erf_bwd_colsum_bf16(None, 16, 16, 16, 4, 16, 16, 1 << 20, None),
+     b"null"),
+    (lambda l: l.hipo_gelu_erf_bwd_colsum_bf16(8, 16, 16, 16, 4, 16, 16, 1 << 20, None),
+     b"aligned"),
+    (lambda l: l.hipo_gelu_erf_bwd_colsum_bf16(16, 16, 16, 16, 4096, 3072, 16, 8, None),
+     b"workspace"),
 ])
 def test_argument_errors_before_launch(lib, call, msg):
     assert call(lib) == HIPO_EINVAL
@@ -96,6 +108,7 @@ def test_empty_inputs_are_no_ops(lib):
                                                 None, 0, None) == 0
     assert lib.hipo_batchnorm_nchw_act_mean_bf16(*[None] * 8, 2, 0, 49, 0.1, 1e-5, 1.0, 1,
                                                  None, 0, None) == 0
+    assert lib.hipo_gelu_erf_bwd_colsum_bf16(None, None, None, None, 0, 0, None, 0, None) == 0
     assert lib.hipo_last_error() == b""
 
 
@@ -120,6 +133,27 @@ def test_bf16_batchnorm_workspace_bytes(lib):
     assert lib.hipo_batchnorm_nchw_mean_workspace_bytes(128, 1024, 49) == 32 * 1024 * 8
     assert lib.hipo_batchnorm_nchw_mean_workspace_bytes(5, 8, 9) == 2 * 8 * 8
     assert lib.hipo_batchnorm_nchw_mean_workspace_bytes(5, 8, 0) == 0
+
+
+def test_gelu_bwd_workspace_bytes(lib):
+    """fp64 column partials, one row per row block: none up to 256 rows (one
+    launch); 8-row blocks up to 1024 rows; 256-row blocks for one or two
+    512-column blocks; rows * blocks / 2048 rows held to [64, 128] (up to 8
+    column blocks) or [32, 128]."""
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(25216, 3072) == 346 * 3072 * 8
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(175360, 3072) == 1370 * 3072 * 8
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(32768, 1024) == 128 * 1024 * 8
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(2048, 10240) == 64 * 10240 * 8
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(128, 3072) == 0
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(256, 16) == 0
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(257, 3072) == 33 * 3072 * 8
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(1000, 16) == 125 * 16 * 8
+    # grid.y holds at most 65535 row blocks: longer tensors get longer blocks
+    rows = 10 ** 8
+    rpb = -(-rows // 65535)
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(rows, 8) == -(-rows // rpb) * 8 * 8
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(0, 16) == 0
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(16, 0) == 0
 
 
 def test_batchnorm_workspace_bytes(lib):

@@ -383,6 +383,36 @@ def check_row_mean_bf16(fn):
     assert fn(mixed, relu=True).item() == 1.25 and fn(mixed).item() == -1.0, "mean(relu(x))"
 
 
+def check_gelu_erf_bwd(fn):
+    g = torch.Generator().manual_seed(13)
+    grad = torch.randn(64, 256, generator=g).to(BF)
+    x = (2 * torch.randn(64, 256, generator=g)).to(BF)
+    y, colsum = fn(grad, x)
+    assert y.shape == (64, 256) and y.dtype == BF and colsum.shape == (256,)
+    # d against central differences of GELU(t) = t Phi(t) (math.erfc, fp64):
+    # y is within one bf16 rounding of grad * d
+    def gelu(t):
+        return t * math.erfc(-t / math.sqrt(2.0)) / 2
+    h = 2.0 ** -12
+    for gv, xv, yv in list(zip(grad.flatten().tolist(), x.flatten().tolist(),
+                               y.float().flatten().tolist()))[::37]:
+        want = gv * (gelu(xv + h) - gelu(xv - h)) / (2 * h)
+        assert abs(yv - want) <= 2 ** -8 * abs(want) + 1e-6, (gv, xv, yv, want)
+    # colsum: bf16 of the exact (fsum) sum of the returned bf16 y
+    cols = y.double().t().tolist()
+    assert colsum.tolist() == [bf16_round(math.fsum(c)) for c in cols], "brute-force column sum"
+    # closed forms: d(0) = 1/2, d -> 1 and 0 in the tails, inf / NaN -> NaN
+    gg = torch.tensor([[1.5, -3.0, 2.0, 7.0, -1.0, 5.0, 2.0, 1.0]]).to(BF)
+    xx = torch.tensor([[0.0, -0.0, 20.0, 1e4, -20.0, -1e4, float("inf"), float("nan")]]).to(BF)
+    yy, cs = fn(gg, xx)
+    assert yy.float()[0, :6].tolist() == [0.75, -1.5, 2.0, 7.0, 0.0, 0.0]
+    assert torch.isnan(yy.float()[0, 6:]).all() and torch.isnan(cs[6:]).all()
+    # zero rows: zero column sums
+    empty = torch.zeros(0, 16, dtype=BF)
+    ye, ce = fn(empty, empty)
+    assert ye.shape == (0, 16) and torch.equal(ce, torch.zeros(16))
+
+
 CHECKS = {
     "row_mean": (check_row_mean, ref.row_mean),
     "bias_gelu": (check_bias_gelu, ref.bias_gelu_nchw_to_nhwc),
@@ -398,6 +428,7 @@ CHECKS = {
     "gelu_flat": (check_gelu_flat, ref.gelu_tanh),
     "transpose": (check_transpose, ref.transpose_last2),
     "row_mean_bf16": (check_row_mean_bf16, ref.row_mean_bf16),
+    "gelu_erf_bwd": (check_gelu_erf_bwd, ref.gelu_erf_bwd_colsum),
 }
 
 
@@ -515,7 +546,32 @@ def _row_mean_wrong_divisor(x, *, relu=False):
     return (ref.row_mean_bf16(x, relu=relu).double() * x.shape[1] / (x.shape[1] - 1)).to(BF)
 
 
+def _gelu_bwd_cdf_only(grad, x):
+    """d = Phi(t): the t phi(t) term dropped."""
+    d = torch.special.ndtr(x.double())
+    y = (grad.double() * d).to(BF)
+    return y, y.double().sum(0).to(BF).float()
+
+
+def _gelu_bwd_sum_unrounded(grad, x):
+    """The column sum of grad * d before y's bf16 rounding."""
+    y, _ = ref.gelu_erf_bwd_colsum(grad, x)
+    exact = grad.float() * ref.gelu_erf_grad(x)
+    return y, exact.double().sum(0).to(BF).float()
+
+
+def _gelu_bwd_unscaled_erf(grad, x):
+    """Phi(t) taken as (1 + erf(t)) / 2, without the 1 / sqrt 2."""
+    t = x.double()
+    d = 0.5 * (1 + torch.erf(t)) + t * torch.exp(-0.5 * t * t) / math.sqrt(2 * math.pi)
+    y = (grad.double() * d).to(BF)
+    return y, y.double().sum(0).to(BF).float()
+
+
 MUTANTS = [
+    ("gelu_erf_bwd", _gelu_bwd_cdf_only),
+    ("gelu_erf_bwd", _gelu_bwd_sum_unrounded),
+    ("gelu_erf_bwd", _gelu_bwd_unscaled_erf),
     ("gelu_flat", _gelu_erf_form),
     ("gelu_flat", _gelu_no_cubic),
     ("transpose", _transpose_leading_dims),
@@ -612,6 +668,12 @@ def test_oracle_matches_family_repros():
     zero = torch.zeros(1, 12, dtype=BF)
     assert close(ref.scaled_masked_softmax(x.reshape(30, 1, 12), zero, 1.0).view(6, 5, 12),
                  want, 1.6e-2)
+    grad, x = torch.randn(12, 16, generator=g).to(BF), torch.randn(12, 16, generator=g).to(BF)
+    want = get_repro_instance(CANONICAL / "sum_139a3020e8bf")(
+        grad, x, [3, 4, 16], [3, 4, 16], [12, 16], [16])
+    y, colsum = ref.gelu_erf_bwd_colsum(grad, x)
+    assert close(y, want[0], 1.6e-2) and close(y.t(), want[1], 1.6e-2)
+    assert close(colsum, want[2], 1e-2)
     x = torch.randn(2, 5, 3, 3, generator=g).to(BF)
     want = get_repro_instance(CANONICAL / "mean_b402ee209d0b")(x, [2, 5])
     assert close(ref.row_mean_bf16(x.reshape(10, 9), relu=True).view(2, 5), want, 1.6e-2)

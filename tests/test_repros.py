@@ -127,6 +127,23 @@ def test_plain_softmax_family_repro():
     assert torch.equal(y, torch.softmax(x.float(), -1).to(bf))
 
 
+def test_gelu_bwd_family_repro():
+    """GELU(erf) backward + column sum: y against ATen's own gelu_backward
+    (fp32, within a bf16 rounding), its transpose a view of y, the column sum
+    the bf16 rounding of y's fp32 column sum."""
+    g = torch.Generator().manual_seed(21)
+    grad = torch.randn(12, 16, generator=g).to(bf)
+    x = (2 * torch.randn(12, 16, generator=g)).to(bf)
+    y, yt, colsum = get_repro_instance(CANONICAL / "sum_139a3020e8bf")(
+        grad, x, [3, 4, 16], [3, 4, 16], [12, 16], [16])
+    want = torch.ops.aten.gelu_backward(grad.float(), x.float())
+    assert y.shape == (12, 16) and y.dtype == bf
+    assert (y.float() - want).abs().max() <= 2 ** -8 * want.abs().max()
+    assert yt.shape == (16, 12) and yt.data_ptr() == y.data_ptr() and torch.equal(yt, y.t())
+    assert colsum.dtype == torch.float32 and colsum.shape == (16,)
+    assert torch.equal(colsum, y.float().sum(0).to(bf).float())
+
+
 @pytest.mark.parametrize("rid", sorted(LN_FAMILY_OUTPUTS))
 def test_residual_layernorm_family_repros(rid):
     """Each residual-LayerNorm family repro at a small shape of its own
