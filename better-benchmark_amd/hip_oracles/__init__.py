@@ -73,6 +73,8 @@ _SIGNATURES = {
     "hipo_transpose_last2": (
         ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_ptr]),
     "hipo_row_mean_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, ctypes.c_int, _c_ptr]),
+    "hipo_cast_bf16_to_f32": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
+    "hipo_cast_f32_to_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "hipo_gelu_erf_bwd_colsum_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64]),
     "hipo_gelu_erf_bwd_colsum_bf16": (
         ctypes.c_int, [_c_ptr] * 4 + [_c_i64, _c_i64, _c_ptr, ctypes.c_size_t, _c_ptr]),
@@ -236,6 +238,37 @@ def row_mean_bf16(x: torch.Tensor, *, relu: bool = False) -> torch.Tensor:
         _check(lib.hipo_row_mean_bf16(_ptr(x), _ptr(out), rows, cols, 1 if relu else 0,
                                       _stream(dev)), "row_mean_bf16")
     return out
+
+
+def _dense_layout(t: torch.Tensor) -> bool:
+    """True if t's strides lay its elements out densely and without overlap
+    (contiguous, channels-last, or any permutation of dims): its storage
+    span is exactly numel elements."""
+    dims = sorted((st, sz) for st, sz in zip(t.stride(), t.shape) if sz != 1)
+    expect = 1
+    for st, sz in dims:
+        if st != expect:
+            return False
+        expect *= sz
+    return True
+
+
+def cast_storage(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """x cast between bf16 and fp32 in storage order: the result has x's
+    shape and strides (eager's preserve-format convert_element_type) and
+    element i of x's storage becomes element i of the result's.  bf16 ->
+    fp32 is exact; fp32 -> bf16 rounds to nearest, ties to even."""
+    lib = load_library()
+    dev = _require_rocm(x)
+    pairs = {(torch.bfloat16, torch.float32): lib.hipo_cast_bf16_to_f32,
+             (torch.float32, torch.bfloat16): lib.hipo_cast_f32_to_bf16}
+    _require((x.dtype, dtype) in pairs, "cast_storage: bf16 <-> fp32 only")
+    _require(_dense_layout(x), "cast_storage: x must be dense (no gaps or overlap)")
+    y = torch.empty_strided(tuple(x.shape), tuple(x.stride()), dtype=dtype, device=dev)
+    with torch.cuda.device(dev):
+        _check(pairs[(x.dtype, dtype)](_ptr(x), _ptr(y), x.numel(), _stream(dev)),
+               "cast_storage")
+    return y
 
 
 def gelu_erf_bwd_colsum(grad: torch.Tensor, x: torch.Tensor):
@@ -677,5 +710,5 @@ __all__ = [
     "batchnorm_workspace_bytes", "batchnorm_train",
     "batchnorm_cached_workspace", "batchnorm_error_flag", "BN_ERROR_WORD_OFFSET",
     "HipOraclesDeviceFault", "device_faults", "raise_on_device_faults", "flat_copy",
-    "gelu_erf_bwd_colsum",
+    "gelu_erf_bwd_colsum", "cast_storage",
 ]

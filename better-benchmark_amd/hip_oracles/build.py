@@ -40,6 +40,7 @@ SOURCES = [
     "gelu_flat.hip",
     "transpose.hip",
     "gelu_bwd.hip",
+    "cast.hip",
 ]
 
 # Packed-FP32 VALU forms are disabled for all device code (the compiler

@@ -390,6 +390,23 @@ int hipo_gelu_erf_bwd_colsum_bf16(const uint16_t* grad, const uint16_t* x, uint1
                                   void* workspace, size_t workspace_bytes,
                                   hipStream_t stream);
 
+/*
+ * Storage-order casts between bf16 and fp32 over n elements:
+ *   bf16 -> fp32 exact;  fp32 -> bf16 rounded to nearest, ties to even
+ *   (NaN stays NaN).
+ * Element i of x's storage becomes element i of y's, so a dense tensor of
+ * any layout (contiguous, channels-last, ...) is cast by passing its data
+ * pointer and numel, with y allocated with the same strides.  Any
+ * alignment (16-byte aligned pointers take the vector path).
+ * Replaces the Triton bodies of oracle_forward in
+ * repros/canonical/pointwise_04d85912d998/oracle.py:18-34 (bf16 -> fp32),
+ * repros/canonical/pointwise_ccd411f2a45d/oracle.py:23-39 (fp32 -> bf16) and
+ * repros/canonical/pointwise_8bb40810003c/oracle.py:102-119 (fp32 -> bf16,
+ * the two returned views taken in Python).
+ */
+int hipo_cast_bf16_to_f32(const uint16_t* x, float* y, int64_t n, hipStream_t stream);
+int hipo_cast_f32_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -51,6 +51,8 @@ _SIGS = {
     "ref_row_mean_bf16": (None, [_p, _p, _i64, _i64, _i, _i]),
     "ref_gelu_erf_grad_f32": (None, [_p, _p, _i64, _i]),
     "ref_gelu_erf_bwd_colsum_bf16": (None, [_p] * 4 + [_i64, _i64, _i]),
+    "ref_cast_bf16_to_f32": (None, [_p, _p, _i64, _i]),
+    "ref_cast_f32_to_bf16": (None, [_p, _p, _i64, _i]),
 }
 
 _ACTS = {None: 0, "none": 0, "relu": 1, "silu": 2}
@@ -300,3 +302,17 @@ def gelu_erf_bwd_colsum(grad, x, threads=None):
     load().ref_gelu_erf_bwd_colsum_bf16(grad.data_ptr(), x.data_ptr(), y.data_ptr(),
                                         colsum.data_ptr(), rows, cols, _th(threads))
     return y, colsum
+
+
+def cast_storage(x, dtype, threads=None):
+    """x cast bf16 <-> fp32 element by element in storage order, keeping
+    x's shape and strides: bf16 -> fp32 exact, fp32 -> bf16 to nearest
+    even."""
+    pairs = {(torch.bfloat16, torch.float32): "ref_cast_bf16_to_f32",
+             (torch.float32, torch.bfloat16): "ref_cast_f32_to_bf16"}
+    assert (x.dtype, dtype) in pairs, (x.dtype, dtype)
+    x = x.detach().to("cpu")
+    y = torch.empty_strided(tuple(x.shape), tuple(x.stride()), dtype=dtype)
+    getattr(load(), pairs[(x.dtype, dtype)])(x.data_ptr(), y.data_ptr(), x.numel(),
+                                             _th(threads))
+    return y

@@ -25,6 +25,8 @@
  *   bf16 BN + SiLU + pad (NHWC)   repros/canonical/var_mean_ceb5c315290a/repro.py:27-58
  *   bf16 BN + ReLU + mean (NCHW)  repros/canonical/var_mean_mean_19ffdb35cc67/repro.py:23-54
  *   GELU(erf) bwd + column sum    repros/canonical/sum_139a3020e8bf/repro.py:24-48
+ *   bf16 <-> fp32 casts           repros/canonical/pointwise_04d85912d998/repro.py:24-27 (and
+ *                                 pointwise_ccd411f2a45d, pointwise_8bb40810003c)
  * (paths relative to the reference tree).  Every rounding that the eager
  * graph performs on a bf16 tensor is reproduced (float arithmetic, then
  * round-to-nearest-even to bf16); reductions and transcendental functions
@@ -557,4 +559,17 @@ void ref_gelu_erf_bwd_colsum_bf16(const uint16_t* g, const uint16_t* x, uint16_t
     colsum[c] = bf16_to_f32(f64_to_bf16(s));
   }
   free(part);
+}
+
+/* Storage-order casts (repros/canonical/pointwise_04d85912d998/repro.py:24-27,
+ * pointwise_ccd411f2a45d/repro.py:24-27, pointwise_8bb40810003c/repro.py:24-29):
+ * bf16 -> fp32 exact; fp32 -> bf16 to nearest even (NaN stays NaN). */
+void ref_cast_bf16_to_f32(const uint16_t* x, float* y, int64_t n, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t i = 0; i < n; ++i) y[i] = bf16_to_f32(x[i]);
+}
+
+void ref_cast_f32_to_bf16(const float* x, uint16_t* y, int64_t n, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t i = 0; i < n; ++i) y[i] = f32_to_bf16(x[i]);
 }

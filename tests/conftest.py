@@ -68,6 +68,9 @@ VARIANT_IDS = [
     "amax_sum_fa4cc85fe5ad",
 ] + list(LN_FAMILY_OUTPUTS) + list(RMS_FAMILY_OUTPUTS) + [
     "sum_139a3020e8bf",
+    "pointwise_04d85912d998",
+    "pointwise_ccd411f2a45d",
+    "pointwise_8bb40810003c",
 ]
 
 

@@ -91,6 +91,8 @@ def test_abi_version_and_error_string(lib):
      b"aligned"),
     (lambda l: l.hipo_gelu_erf_bwd_colsum_bf16(16, 16, 16, 16, 4096, 3072, 16, 8, None),
      b"workspace"),
+    (lambda l: l.hipo_cast_bf16_to_f32(16, 16, -1, None), b"negative"),
+    (lambda l: l.hipo_cast_f32_to_bf16(None, 16, 8, None), b"null"),
 ])
 def test_argument_errors_before_launch(lib, call, msg):
     assert call(lib) == HIPO_EINVAL
@@ -109,6 +111,8 @@ def test_empty_inputs_are_no_ops(lib):
     assert lib.hipo_batchnorm_nchw_act_mean_bf16(*[None] * 8, 2, 0, 49, 0.1, 1e-5, 1.0, 1,
                                                  None, 0, None) == 0
     assert lib.hipo_gelu_erf_bwd_colsum_bf16(None, None, None, None, 0, 0, None, 0, None) == 0
+    assert lib.hipo_cast_bf16_to_f32(None, None, 0, None) == 0
+    assert lib.hipo_cast_f32_to_bf16(None, None, 0, None) == 0
     assert lib.hipo_last_error() == b""
 
 

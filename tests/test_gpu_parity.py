@@ -218,6 +218,13 @@ def _family_oracle(rid, i):
         k = x.shape[-1]
         zero = torch.zeros(1, k, dtype=torch.bfloat16)
         return [ref.scaled_masked_softmax(x.reshape(-1, 1, k), zero, 1.0).reshape(x.shape)]
+    if rid == "pointwise_04d85912d998":
+        return [ref.cast_storage(i[0], torch.float32)]
+    if rid == "pointwise_ccd411f2a45d":
+        return [ref.cast_storage(i[0], torch.bfloat16)]
+    if rid == "pointwise_8bb40810003c":
+        w = ref.cast_storage(i[0].contiguous(), torch.bfloat16)
+        return [w.t(), w]
     if rid == "sum_139a3020e8bf":
         y, colsum = ref.gelu_erf_bwd_colsum(i[0], i[1])
         return [y, y.t(), colsum.view(tuple(int(d) for d in i[5]))]
@@ -260,18 +267,25 @@ COLSUM_TOL = (2 ** -7, 1e-4)
 COLSUM_EAGER_TOL = (2 ** -7, 1e-2)
 FAMILY_ORACLE_TOLS = {"pointwise_021e90d9c17d": {torch.bfloat16: EXACT},
                       "pointwise_2d969ac9ad59": {torch.bfloat16: PROB_TOL},
-                      "sum_139a3020e8bf": {torch.bfloat16: EXACT, torch.float32: EXACT}}
+                      "sum_139a3020e8bf": {torch.bfloat16: EXACT, torch.float32: EXACT},
+                      "pointwise_04d85912d998": {torch.float32: EXACT},
+                      "pointwise_ccd411f2a45d": {torch.bfloat16: EXACT},
+                      "pointwise_8bb40810003c": {torch.bfloat16: EXACT}}
 FAMILY_EAGER_TOLS = {"pointwise_2d969ac9ad59": {torch.bfloat16: (1e-2, 1e-2)},
                      "amax_sum_20ccc18dda60": {torch.bfloat16: (1e-2, 1e-2)},
                      "pointwise_021e90d9c17d": {torch.bfloat16: EXACT},
-                     "sum_139a3020e8bf": {torch.float32: COLSUM_EAGER_TOL}}
+                     "sum_139a3020e8bf": {torch.float32: COLSUM_EAGER_TOL},
+                     "pointwise_04d85912d998": {torch.float32: EXACT},
+                     "pointwise_ccd411f2a45d": {torch.bfloat16: EXACT},
+                     "pointwise_8bb40810003c": {torch.bfloat16: EXACT}}
 FAMILY_ULP_FLOOR = {"pointwise_2d969ac9ad59": 0.0, "pointwise_021e90d9c17d": 0.0,
                     "mean_b402ee209d0b": 0.0}
 # Points above this many input elements are checked against the C oracle
 # only (the eager and fp64 CPU evaluations of a 10-op elementwise graph over
 # hundreds of millions of elements take minutes); the smaller points of the
 # same family carry the eager and fp64 checks.
-FAMILY_EAGER_MAX_ELEMS = {"sum_139a3020e8bf": 1 << 26}
+FAMILY_EAGER_MAX_ELEMS = {"sum_139a3020e8bf": 1 << 26, "pointwise_04d85912d998": 1 << 25,
+                          "pointwise_ccd411f2a45d": 1 << 25, "pointwise_8bb40810003c": 1 << 25}
 
 
 @pytest.mark.parametrize("rid", VARIANT_IDS)
@@ -642,6 +656,74 @@ def test_gelu_erf_bwd_closed_forms_and_empty(rocm_device):
     assert y.shape == (0, cols) and colsum.shape == (cols,) and (colsum == 0).all()
     with pytest.raises(ValueError):
         hip_oracles.gelu_erf_bwd_colsum(grad[:, :1036].contiguous(), grad[:, :1036].contiguous())
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16 if t.element_size() == 2 else torch.int32).cpu()
+
+
+def test_cast_bf16_to_f32_every_input(rocm_device):
+    """All 65536 bf16 patterns (NaN payloads included) -> fp32: the bf16 bits
+    in the high half, bit for bit."""
+    import hip_oracles
+    x = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    y = hip_oracles.cast_storage(x.to(rocm_device), torch.float32)
+    want = ((x.view(torch.int16).to(torch.int64) & 0xFFFF) << 16).to(torch.int32)
+    assert torch.equal(_bits(y), want)
+
+
+def test_cast_f32_to_bf16_rounding(rocm_device):
+    """fp32 -> bf16 against ATen's CPU cast (round to nearest even): random
+    magnitudes over the whole range, exact ties both ways, subnormals, the
+    largest values (rounding to inf), infinities and NaN."""
+    import hip_oracles
+    g = torch.Generator().manual_seed(6)
+    mant = torch.randint(0, 1 << 23, (100000,), generator=g)
+    expo = torch.randint(0, 255, (100000,), generator=g)
+    sign = torch.randint(0, 2, (100000,), generator=g)
+    bits = (sign << 31) | (expo << 23) | mant
+    ties = torch.tensor([0x3F808000, 0x3F818000, 0xBF808000, 0x7F7F8000, 0x7F7FFFFF,
+                         0x00008000, 0x00018000, 0x00000001, 0x807FFFFF, 0x7F800000,
+                         0xFF800000, 0x7FC00000, 0x7F800001, 0x00000000, 0x80000000],
+                        dtype=torch.int64)
+    x = torch.cat([bits, ties]).to(torch.int32).view(torch.float32)
+    y = hip_oracles.cast_storage(x.to(rocm_device), torch.bfloat16).cpu()
+    want = x.to(torch.bfloat16)
+    nan = torch.isnan(want.float())
+    assert torch.equal(torch.isnan(y.float()), nan), "NaN positions"
+    assert torch.equal(_bits(y)[~nan], _bits(want)[~nan]), "nearest-even rounding"
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 4095, 4096, 4097, (1 << 20) + 3])
+def test_cast_sizes_and_alignment(n, rocm_device):
+    """Vector path and scalar tail, then a view one element into the tensor
+    (not 16-byte aligned: the element-by-element path), both directions."""
+    import hip_oracles
+    import oracle as ref
+    g = torch.Generator().manual_seed(n)
+    base = torch.randn(n + 1, generator=g) * 100
+    for src, dst in ((torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32)):
+        full = base.to(src).to(rocm_device)
+        for x in (full[:n], full[1:]):
+            y = hip_oracles.cast_storage(x, dst)
+            assert y.shape == (n,) and y.dtype == dst
+            assert torch.equal(_bits(y), _bits(ref.cast_storage(x.cpu(), dst))), (n, src, dst)
+
+
+def test_cast_keeps_layouts(rocm_device):
+    """Channels-last and permuted dense inputs: the result keeps the strides
+    and equals eager's preserve-format cast; a tensor with gaps is refused."""
+    import hip_oracles
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(8, 24, 7, 5, generator=g).to(memory_format=torch.channels_last)
+    for src, dst in ((torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32)):
+        xs = x.to(src)
+        for t in (xs, xs.permute(3, 1, 0, 2)):
+            y = hip_oracles.cast_storage(t.to(rocm_device), dst)
+            want = t.to(dst)
+            assert y.stride() == want.stride() and torch.equal(y.cpu(), want)
+    with pytest.raises(ValueError):
+        hip_oracles.cast_storage(x.to(rocm_device)[:, :, ::2], torch.bfloat16)
 
 
 def test_softmax_closed_forms(rocm_device):

@@ -413,6 +413,48 @@ def check_gelu_erf_bwd(fn):
     assert ye.shape == (0, 16) and torch.equal(ce, torch.zeros(16))
 
 
+def _rne_bf16_bits(v: float) -> int:
+    """fp32 value -> bf16 bits by hand: round to nearest, ties to even."""
+    import struct
+    u = struct.unpack("<I", struct.pack("<f", v))[0]
+    if (u & 0x7FFFFFFF) > 0x7F800000:
+        return None  # NaN: any NaN
+    lower = u & 0xFFFF
+    hi = u >> 16
+    if lower > 0x8000 or (lower == 0x8000 and hi & 1):
+        hi += 1
+    return hi & 0xFFFF
+
+
+def check_cast(fn):
+    # bf16 -> fp32: every bf16 pattern, its bits in the high half
+    x = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(BF)
+    y = fn(x, torch.float32)
+    assert y.dtype == torch.float32
+    want = ((x.view(torch.int16).to(torch.int64) & 0xFFFF) << 16).to(torch.int32)
+    assert torch.equal(y.view(torch.int32), want), "bf16 -> fp32 is exact"
+    # fp32 -> bf16: by hand (nearest even) on ties, near-ties, subnormals,
+    # overflow to inf, and ATen's own cast on random patterns
+    vals = [1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8), 1.0 + 2 ** -8 + 2 ** -20,
+            3.3895313892515355e38, 3.4028234663852886e38, 1e-40, -1e-42, 2 ** -133,
+            2 ** -134, 0.0, -0.0, float("inf"), -float("inf"), 65504.0, 0.1, -7.3e-5]
+    got = fn(torch.tensor(vals), BF).view(torch.int16).tolist()
+    for v, gb in zip(vals, got):
+        assert (gb & 0xFFFF) == _rne_bf16_bits(v), (v, hex(gb & 0xFFFF))
+    g = torch.Generator().manual_seed(9)
+    bits = torch.randint(-(2 ** 31), 2 ** 31 - 1, (20000,), generator=g, dtype=torch.int64)
+    xf = bits.to(torch.int32).view(torch.float32)
+    yb = fn(xf, BF)
+    want = xf.to(BF)
+    nan = torch.isnan(want.float())
+    assert torch.equal(torch.isnan(yb.float()), nan)
+    assert torch.equal(yb.view(torch.int16)[~nan], want.view(torch.int16)[~nan]), "vs ATen"
+    # strides kept (channels-last in, channels-last out)
+    xc = torch.randn(2, 5, 3, 4).to(memory_format=torch.channels_last)
+    yc = fn(xc, BF)
+    assert yc.stride() == xc.stride() and torch.equal(yc, xc.to(BF))
+
+
 CHECKS = {
     "row_mean": (check_row_mean, ref.row_mean),
     "bias_gelu": (check_bias_gelu, ref.bias_gelu_nchw_to_nhwc),
@@ -429,6 +471,7 @@ CHECKS = {
     "transpose": (check_transpose, ref.transpose_last2),
     "row_mean_bf16": (check_row_mean_bf16, ref.row_mean_bf16),
     "gelu_erf_bwd": (check_gelu_erf_bwd, ref.gelu_erf_bwd_colsum),
+    "cast": (check_cast, ref.cast_storage),
 }
 
 
@@ -568,7 +611,27 @@ def _gelu_bwd_unscaled_erf(grad, x):
     return y, y.double().sum(0).to(BF).float()
 
 
+def _cast_truncates(x, dtype):
+    """fp32 -> bf16 by dropping the low half (round toward zero)."""
+    if x.dtype == torch.float32 and dtype == BF:
+        return (x.contiguous().view(torch.int32) >> 16).to(torch.int16).view(BF).reshape(x.shape)
+    return ref.cast_storage(x, dtype)
+
+
+def _cast_ties_away(x, dtype):
+    """fp32 -> bf16 with ties rounded away from zero."""
+    if x.dtype == torch.float32 and dtype == BF:
+        u = x.contiguous().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+        r = ((u + 0x8000) >> 16) & 0xFFFF
+        nan = torch.isnan(x.contiguous())
+        r = torch.where(nan, torch.full_like(r, 0x7FC0), r)
+        return r.to(torch.int32).to(torch.int16).view(BF).reshape(x.shape)
+    return ref.cast_storage(x, dtype)
+
+
 MUTANTS = [
+    ("cast", _cast_truncates),
+    ("cast", _cast_ties_away),
     ("gelu_erf_bwd", _gelu_bwd_cdf_only),
     ("gelu_erf_bwd", _gelu_bwd_sum_unrounded),
     ("gelu_erf_bwd", _gelu_bwd_unscaled_erf),

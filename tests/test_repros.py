@@ -127,6 +127,22 @@ def test_plain_softmax_family_repro():
     assert torch.equal(y, torch.softmax(x.float(), -1).to(bf))
 
 
+def test_cast_family_repros():
+    """The three cast families: eager's preserve-format convert_element_type
+    (strides kept), and the fp32 -> bf16 weight returned as its transpose and
+    itself, both views of one tensor."""
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(4, 6, 3, 3, generator=g).to(memory_format=torch.channels_last)
+    y = get_repro_instance(CANONICAL / "pointwise_04d85912d998")(x.to(bf))
+    assert y.dtype == torch.float32 and y.stride() == x.stride() and torch.equal(y, x.to(bf).float())
+    y = get_repro_instance(CANONICAL / "pointwise_ccd411f2a45d")(x)
+    assert y.dtype == bf and y.stride() == x.stride() and torch.equal(y, x.to(bf))
+    w = torch.randn(5, 7, generator=g)
+    wt, w2 = get_repro_instance(CANONICAL / "pointwise_8bb40810003c")(w)
+    assert wt.shape == (7, 5) and w2.shape == (5, 7) and wt.data_ptr() == w2.data_ptr()
+    assert torch.equal(w2, w.to(bf)) and w2.is_contiguous()
+
+
 def test_gelu_bwd_family_repro():
     """GELU(erf) backward + column sum: y against ATen's own gelu_backward
     (fp32, within a bf16 rounding), its transpose a view of y, the column sum
@@ -245,13 +261,21 @@ def test_family_repro_contract(rid):
     import json
     meta = json.loads((CANONICAL / rid / "meta.json").read_text())
     assert rid.endswith(meta["pattern_hash"])
-    # every shapes.json point has its MI355X registration, plus one
-    # shape-general entry for shapes outside the corpus
+    # every shapes.json point has an MI355X registration -- its own, or, where
+    # points differ only in strides (the registry keys by input shapes), that
+    # of a point with the same input shapes -- plus one shape-general entry
+    # for shapes outside the corpus
     import oracle_harness as oh
     _, fn, _ = oh._load_oracle_module(CANONICAL / rid)
     entries = oh.get_module_registry(fn.__module__)._entries
-    hashes = {p["shape_hash"] for p in json.loads((CANONICAL / rid / "shapes.json").read_text())["points"]}
-    assert {e["point"] for e in entries if e["point"]} == hashes
+    points = json.loads((CANONICAL / rid / "shapes.json").read_text())["points"]
+
+    def shapes(p):
+        return tuple(tuple(i[0]) for i in p["inputs"] if i[0] != "S")
+    registered = {e["point"] for e in entries if e["point"]}
+    assert registered <= {p["shape_hash"] for p in points}
+    covered = {shapes(p) for p in points if p["shape_hash"] in registered}
+    assert all(shapes(p) in covered for p in points)
     assert any(e["shape"] is None and e["hardware"] == "MI355X" for e in entries)
 
 
