@@ -75,6 +75,8 @@ _SIGNATURES = {
     "hipo_row_mean_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, ctypes.c_int, _c_ptr]),
     "hipo_cast_bf16_to_f32": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "hipo_cast_f32_to_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
+    "hipo_bn_infer_act_bf16": (ctypes.c_int, [_c_ptr] * 12 + [_c_i64, _c_i64, _c_i64, ctypes.c_int,
+                                                          ctypes.c_float, ctypes.c_int, _c_ptr]),
     "hipo_gelu_erf_bwd_colsum_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64]),
     "hipo_gelu_erf_bwd_colsum_bf16": (
         ctypes.c_int, [_c_ptr] * 4 + [_c_i64, _c_i64, _c_ptr, ctypes.c_size_t, _c_ptr]),
@@ -268,6 +270,62 @@ def cast_storage(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     with torch.cuda.device(dev):
         _check(pairs[(x.dtype, dtype)](_ptr(x), _ptr(y), x.numel(), _stream(dev)),
                "cast_storage")
+    return y
+
+
+BN_ACTS = {"none": 0, "relu": 1, "relu6": 2}
+
+
+def _nchw_layout(t: torch.Tensor):
+    """0 for contiguous NCHW, 1 for channels-last, None otherwise."""
+    if t.is_contiguous():
+        return 0
+    if t.is_contiguous(memory_format=torch.channels_last):
+        return 1
+    return None
+
+
+def bn_infer_act(x: torch.Tensor, mean: torch.Tensor, var: torch.Tensor, weight: torch.Tensor,
+                 bias: torch.Tensor, *, eps: float, act: str = "none",
+                 residual: torch.Tensor = None, second=None) -> torch.Tensor:
+    """BatchNorm inference affine of a bf16 [N, C, H, W] tensor (contiguous or
+    channels-last), its epilogue and the graph's bf16 rounding points:
+    t = bf16(((x - mean) * inv) * weight + bias), inv = 1 / sqrt(var + eps)
+    per channel in fp32 and the four element ops in fp64 (as the graph's
+    fp64 evaluation makes them); second = (x2, mean2, var2, weight2, bias2) adds the same
+    affine of x2, rounded to bf16; residual adds a bf16 tensor, rounded to
+    bf16; then act "none", "relu" or "relu6".  The parameters are bf16 [C];
+    x2, residual and the result share x's strides."""
+    lib = load_library()
+    extra = [t for t in ((residual,) if residual is not None else ()) + tuple(second or ())]
+    dev = _require_rocm(x, mean, var, weight, bias, *extra)
+    _require(act in BN_ACTS, f"bn_infer_act: act must be one of {sorted(BN_ACTS)}")
+    _require(x.dim() == 4, "bn_infer_act: x must be [N, C, H, W]")
+    n, c, h, w = x.shape
+    layout = _nchw_layout(x)
+    _require(layout is not None, "bn_infer_act: x must be contiguous or channels-last")
+    params = [mean, var, weight, bias]
+    x2 = None
+    if second is not None:
+        _require(len(second) == 5, "bn_infer_act: second = (x2, mean2, var2, weight2, bias2)")
+        x2 = second[0]
+        params += list(second[1:])
+    for t in params:
+        _require(t.dtype == torch.bfloat16 and t.shape == (c,) and t.is_contiguous(),
+                 "bn_infer_act: parameters must be contiguous bf16 [C]")
+    for t in [x] + [u for u in (x2, residual) if u is not None]:
+        _require(t.dtype == torch.bfloat16 and t.shape == x.shape and t.stride() == x.stride(),
+                 "bn_infer_act: x, x2 and residual must be bf16 of one shape and strides")
+    y = torch.empty_strided(tuple(x.shape), tuple(x.stride()), dtype=torch.bfloat16, device=dev)
+    if y.numel() == 0:
+        return y
+    p2 = [_ptr(t) for t in second[1:]] if second is not None else [0, 0, 0, 0]
+    with torch.cuda.device(dev):
+        _check(lib.hipo_bn_infer_act_bf16(
+            _ptr(x), _ptr(mean), _ptr(var), _ptr(weight), _ptr(bias),
+            _ptr(x2) if x2 is not None else 0, *p2,
+            _ptr(residual) if residual is not None else 0, _ptr(y),
+            n, c, h * w, layout, float(eps), BN_ACTS[act], _stream(dev)), "bn_infer_act")
     return y
 
 
@@ -710,5 +768,5 @@ __all__ = [
     "batchnorm_workspace_bytes", "batchnorm_train",
     "batchnorm_cached_workspace", "batchnorm_error_flag", "BN_ERROR_WORD_OFFSET",
     "HipOraclesDeviceFault", "device_faults", "raise_on_device_faults", "flat_copy",
-    "gelu_erf_bwd_colsum", "cast_storage",
+    "gelu_erf_bwd_colsum", "cast_storage", "bn_infer_act",
 ]

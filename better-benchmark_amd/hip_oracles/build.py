@@ -41,6 +41,7 @@ SOURCES = [
     "transpose.hip",
     "gelu_bwd.hip",
     "cast.hip",
+    "bn_infer.hip",
 ]
 
 # Packed-FP32 VALU forms are disabled for all device code (the compiler

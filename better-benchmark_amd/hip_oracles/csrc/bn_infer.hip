@@ -1,0 +1,389 @@
+// BatchNorm inference affine with the epilogues of the reference's
+// BN-inference families, bf16 in and out, in the graph's op order (no
+// contraction):
+//   t  = bf16(f32(((x - mean[c]) * inv[c]) * w[c] + b[c])), the four ops in
+//        fp64, inv[c] = 1 / sqrt(f32(var[c]) + eps) in fp32  (one affine)
+//   second affine (x2 with its own parameters): t = bf16(f32(t) + f32(t2))
+//   residual: t = bf16(f32(t) + f32(res))
+//   act: none, ReLU (max(t, 0), NaN kept), ReLU6 (clamp to [0, 6], NaN kept)
+// -- pointwise_7899d74e0838 (ReLU), pointwise_818c3aa59952 (none),
+// pointwise_e6ddc8e897ec (residual), pointwise_9595e73ff43b (ReLU6),
+// pointwise_81485f33f5b9 (residual + ReLU), pointwise_2c331ef4f17f (two
+// affines + ReLU).
+//
+// The tensors are dense and share one layout (contiguous NCHW or
+// channels-last), and the kernels walk storage order in 8-element groups
+// (16-byte non-temporal loads and stores, loads issued before the math):
+//  * channels-last, C % 8 == 0 and C <= 2048 (1024 with two affines): the
+//    workgroup computes the C channels' parameters into LDS; a thread owns
+//    one group of 8 channels, holds their parameters in registers and
+//    walks 8 positions (4 with two affines); consecutive threads take
+//    consecutive groups of one position, so each load instruction is one
+//    contiguous run;
+//  * otherwise (NCHW, or an odd C): every workgroup first computes the
+//    parameters of the channels its elements touch into LDS (about
+//    4096 / D + 2 of them, at most C and 64 KB); the channel of storage
+//    element i is (i / D) % C with D = H*W (NCHW) or 1, found once per group
+//    by division; when D % 8 == 0 a group lies in one channel plane and
+//    reads its parameters once, when D >= 8 it spans at most two planes and
+//    reads two sets, otherwise the channel is stepped element by element.
+// A channel's parameters are (mean, inv * w, b) in fp64 with inv = 1 /
+// sqrt(var + eps) in fp32 (IEEE sqrt and division).
+// Unaligned tensors, tables past 64 KB and the n % 8 tail go one element
+// per thread (parameters computed per element).
+// Bytes: 4 per element (+2 per residual / second input).
+#include "hipo_common.h"
+
+namespace hipo {
+namespace {
+
+constexpr int kBnThreads = 256;
+constexpr int kGroupsPerThread = 2;  // groups per thread, LDS-table kernel
+constexpr int kMaxChannels = 4096;
+// dynamic LDS of the table kernels: at most 2048 parameter sets (1024 with
+// two affines); beyond, the one-element-per-thread kernel runs
+constexpr size_t kMaxLdsBytes = 65536;
+
+struct Affine {
+  const uint16_t* mean;
+  const uint16_t* var;
+  const uint16_t* w;
+  const uint16_t* b;
+};
+
+struct BnGeom {
+  uint32_t n;    // elements
+  int channels;  // C
+  uint32_t d;    // elements per channel run: H*W (NCHW) or 1 (channels-last)
+  DivMagic by_d;
+  DivMagic by_c;
+  float eps;
+};
+
+typedef double f64x4_t __attribute__((ext_vector_type(4)));
+
+// (mean, inv * w, b, 0) of channel c in fp64, inv = 1 / sqrt(var + eps) in
+// fp32 (IEEE sqrt and division).  inv * w is exact in fp64 (24 x 8 bits).
+__device__ __forceinline__ f64x4_t channel_params(const Affine& a, int c, float eps) {
+#pragma clang fp contract(off)
+  const float inv = 1.0f / sqrtf(bf16_to_f32(a.var[c]) + eps);
+  return f64x4_t{static_cast<double>(bf16_to_f32(a.mean[c])),
+                 static_cast<double>(inv) * static_cast<double>(bf16_to_f32(a.w[c])),
+                 static_cast<double>(bf16_to_f32(a.b[c])), 0.0};
+}
+
+// The parameters of the channels that elements [first, last] of the storage
+// order touch, into LDS: entry j holds channel (c_first + j) % C for j <
+// min(planes spanned, C), the second affine's at offset `entries`.
+// Returns c_first.
+template <bool kDual>
+__device__ __forceinline__ uint32_t stage_params(f64x4_t* lds, uint32_t entries, const Affine& a1,
+                                                 const Affine& a2, const BnGeom& g, uint32_t first,
+                                                 uint32_t last) {
+  const uint32_t channels = static_cast<uint32_t>(g.channels);
+  const uint32_t q0 = div_by(first, g.by_d);
+  const uint32_t c_first = q0 - div_by(q0, g.by_c) * channels;
+  const uint32_t span = div_by(last, g.by_d) - q0 + 1;
+  const uint32_t count = span < channels ? span : channels;
+  for (uint32_t j = threadIdx.x; j < count; j += kBnThreads) {
+    const uint32_t c = c_first + j >= channels ? c_first + j - channels : c_first + j;
+    lds[j] = channel_params(a1, static_cast<int>(c), g.eps);
+    if (kDual) lds[entries + j] = channel_params(a2, static_cast<int>(c), g.eps);
+  }
+  __syncthreads();
+  return c_first;
+}
+
+// The affine of one element in fp64 from fp32 operands, as the graph's fp64
+// evaluation (the reference harness's numerics anchor) makes it: x - mean,
+// * inv and * w are exact in fp64 (8 x 24 x 8 significant bits), + b rounds
+// at most once; the result goes to bf16 through fp32, as a bf16 cast of an
+// fp64 tensor does.  The fp32 graph (eager, Inductor) rounds each of the
+// four ops to fp32 instead, and so lands one bf16 ulp away wherever its
+// fp32 value straddles a bf16 rounding midpoint; computed this way the
+// kernel matches the anchor there.
+// The fp64 product ((x - mean) * inv) * w rounds at most at the last
+// multiply (x - mean and inv carry 24 significant bits at most, w 8), as
+// does (x - mean) * (inv * w): both are the one rounding of the same exact
+// product, so the folded form is bit for bit the graph's order.
+__device__ __forceinline__ float affine_bf16(float xf, const f64x4_t& p) {
+#pragma clang fp contract(off)
+  const double t = (static_cast<double>(xf) - p[0]) * p[1] + p[2];
+  return round_bf16(static_cast<float>(t));
+}
+
+// One element: affine (+ second affine) (+ residual), rounded to bf16 after
+// each op as eager stores bf16, then the activation.  maximum / minimum are
+// IEEE-2019 (NaN in, NaN out; -0 < +0), as eager's relu and clamp.
+template <bool kDual, bool kRes, int kAct>
+__device__ __forceinline__ float epilogue(float xf, float x2f, float rf, const f64x4_t& p1,
+                                          const f64x4_t& p2) {
+#pragma clang fp contract(off)
+  float t = affine_bf16(xf, p1);
+  if (kDual) t = round_bf16(t + affine_bf16(x2f, p2));
+  if (kRes) t = round_bf16(t + rf);
+  if (kAct == 1) t = __builtin_elementwise_maximum(t, 0.0f);
+  if (kAct == 2) t = __builtin_elementwise_minimum(__builtin_elementwise_maximum(t, 0.0f), 6.0f);
+  return t;
+}
+
+__device__ __forceinline__ float elem(const u32x4_t& v, int e) {
+  return (e & 1) ? bf16hi(v[e >> 1]) : bf16lo(v[e >> 1]);
+}
+
+template <bool kDual, bool kRes, int kAct, typename ParamOf>
+__device__ __forceinline__ u32x4_t group_out(const u32x4_t& xv, const u32x4_t& x2v,
+                                             const u32x4_t& rv, ParamOf param_of) {
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    f64x4_t p1, p2;
+    param_of(e, p1, p2);
+    o[e] = epilogue<kDual, kRes, kAct>(elem(xv, e), kDual ? elem(x2v, e) : 0.0f,
+                                       kRes ? elem(rv, e) : 0.0f, p1, p2);
+  }
+  return u32x4_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
+                 pack_bf16x2(o[6], o[7])};
+}
+
+// LDS-table kernel: groups [0, groups); dynamic LDS of `entries` (x2 for
+// two affines) parameter sets.  kPlanes: 1 when D % 8 == 0 (the 8 elements
+// of a group share one channel: one LDS read), 2 when D >= 8 (a group spans
+// at most two channel planes: two reads, selected per element), 0 otherwise
+// (a read per element, the channel stepped along).
+template <bool kDual, bool kRes, int kAct, int kPlanes>
+__global__ __launch_bounds__(kBnThreads) void bn_infer_vec(
+    const u32x4_t* __restrict__ x, const u32x4_t* __restrict__ x2, const u32x4_t* __restrict__ res,
+    u32x4_t* __restrict__ y, Affine a1, Affine a2, BnGeom g, uint32_t groups, uint32_t entries) {
+  extern __shared__ f64x4_t lds[];
+  const uint32_t g0 = blockIdx.x * kGroupsPerThread * kBnThreads;
+  u32x4_t xv[kGroupsPerThread], x2v[kGroupsPerThread], rv[kGroupsPerThread];
+#pragma unroll
+  for (int k = 0; k < kGroupsPerThread; ++k) {
+    const uint32_t gi = g0 + k * kBnThreads + threadIdx.x;
+    const uint32_t gl = gi < groups ? gi : groups - 1;
+    xv[k] = __builtin_nontemporal_load(x + gl);
+    x2v[k] = kDual ? __builtin_nontemporal_load(x2 + gl) : u32x4_t{0u, 0u, 0u, 0u};
+    rv[k] = kRes ? __builtin_nontemporal_load(res + gl) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  const uint32_t g_end = g0 + kGroupsPerThread * kBnThreads < groups
+                             ? g0 + kGroupsPerThread * kBnThreads
+                             : groups;
+  const uint32_t c_first = stage_params<kDual>(lds, entries, a1, a2, g, g0 * 8, g_end * 8 - 1);
+  const uint32_t channels = static_cast<uint32_t>(g.channels);
+#pragma unroll
+  for (int k = 0; k < kGroupsPerThread; ++k) {
+    const uint32_t gi = g0 + k * kBnThreads + threadIdx.x;
+    if (gi >= groups) break;
+    const uint32_t q = div_by(gi * 8, g.by_d);
+    const uint32_t c = q - div_by(q, g.by_c) * channels;
+    uint32_t j = c >= c_first ? c - c_first : c + channels - c_first;
+    u32x4_t out;
+    if (kPlanes == 1) {
+      const f64x4_t p1 = lds[j];
+      const f64x4_t p2 = kDual ? lds[entries + j] : p1;
+      out = group_out<kDual, kRes, kAct>(xv[k], x2v[k], rv[k],
+                                         [&](int, f64x4_t& a, f64x4_t& b) { a = p1; b = p2; });
+    } else if (kPlanes == 2) {
+      // elements [0, split) lie in plane j, the rest (if any) in the next
+      const uint32_t r = gi * 8 - q * g.d;
+      const uint32_t split = g.d - r;
+      const uint32_t jn = j + 1 == channels ? 0u : j + 1;
+      const f64x4_t p1a = lds[j];
+      const f64x4_t p2a = kDual ? lds[entries + j] : p1a;
+      f64x4_t p1b = p1a, p2b = p2a;
+      if (split < 8) {
+        p1b = lds[jn];
+        p2b = kDual ? lds[entries + jn] : p1b;
+      }
+      out = group_out<kDual, kRes, kAct>(xv[k], x2v[k], rv[k], [&](int e, f64x4_t& a, f64x4_t& b) {
+        const bool first = static_cast<uint32_t>(e) < split;
+        a = first ? p1a : p1b;
+        b = first ? p2a : p2b;
+      });
+    } else {
+      uint32_t r = gi * 8 - q * g.d;
+      out = group_out<kDual, kRes, kAct>(xv[k], x2v[k], rv[k], [&](int, f64x4_t& a, f64x4_t& b) {
+        a = lds[j];
+        b = kDual ? lds[entries + j] : a;
+        if (++r == g.d) {
+          r = 0;
+          j = j + 1 == channels ? 0u : j + 1;
+        }
+      });
+    }
+    __builtin_nontemporal_store(out, y + gi);
+  }
+}
+
+// Channels-last kernel: C % 8 == 0, cgroups = C / 8 <= kBnThreads.  The
+// workgroup stages all C channels' parameters in LDS (dynamic, C entries, x2
+// for two affines); thread t owns channel group t % cgroups, reads its 8
+// channels' parameters into registers once and walks positions
+// (blockIdx.x * kIters + k) * per_pass + t / cgroups, per_pass =
+// kBnThreads / cgroups; threads past per_pass * cgroups have no work.
+template <bool kDual, bool kRes, int kAct>
+__global__ __launch_bounds__(kBnThreads) void bn_infer_nhwc(
+    const u32x4_t* __restrict__ x, const u32x4_t* __restrict__ x2, const u32x4_t* __restrict__ res,
+    u32x4_t* __restrict__ y, Affine a1, Affine a2, BnGeom g, uint32_t positions,
+    uint32_t cgroups) {
+  constexpr int kIters = kDual ? 4 : 8;
+  extern __shared__ f64x4_t lds[];
+  const uint32_t channels = static_cast<uint32_t>(g.channels);
+  const uint32_t per_pass = kBnThreads / cgroups;
+  const uint32_t t = threadIdx.x;
+  const bool active = t < per_pass * cgroups;
+  const uint32_t cg = active ? t % cgroups : 0;
+  const uint32_t pl = active ? t / cgroups : 0;
+  u32x4_t xv[kIters], x2v[kIters], rv[kIters];
+#pragma unroll
+  for (int k = 0; k < kIters; ++k) {
+    const uint32_t p = (blockIdx.x * kIters + k) * per_pass + pl;
+    const uint32_t gl = (p < positions ? p : positions - 1) * cgroups + cg;
+    xv[k] = __builtin_nontemporal_load(x + gl);
+    x2v[k] = kDual ? __builtin_nontemporal_load(x2 + gl) : u32x4_t{0u, 0u, 0u, 0u};
+    rv[k] = kRes ? __builtin_nontemporal_load(res + gl) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  for (uint32_t c = t; c < channels; c += kBnThreads) {
+    lds[c] = channel_params(a1, static_cast<int>(c), g.eps);
+    if (kDual) lds[channels + c] = channel_params(a2, static_cast<int>(c), g.eps);
+  }
+  __syncthreads();
+  if (!active) return;
+  f64x4_t p1[8], p2[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    p1[e] = lds[cg * 8 + e];
+    p2[e] = kDual ? lds[channels + cg * 8 + e] : p1[e];
+  }
+#pragma unroll
+  for (int k = 0; k < kIters; ++k) {
+    const uint32_t p = (blockIdx.x * kIters + k) * per_pass + pl;
+    if (p >= positions) break;
+    const u32x4_t out = group_out<kDual, kRes, kAct>(
+        xv[k], x2v[k], rv[k], [&](int e, f64x4_t& a, f64x4_t& b) { a = p1[e]; b = p2[e]; });
+    __builtin_nontemporal_store(out, y + p * cgroups + cg);
+  }
+}
+
+// Elements [first, n), one per thread.
+template <bool kDual, bool kRes, int kAct>
+__global__ __launch_bounds__(kBnThreads) void bn_infer_scalar(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ x2,
+    const uint16_t* __restrict__ res, uint16_t* __restrict__ y, Affine a1, Affine a2, BnGeom g,
+    uint32_t first) {
+  const uint32_t i = first + blockIdx.x * kBnThreads + threadIdx.x;
+  if (i >= g.n) return;
+  const uint32_t q = div_by(i, g.by_d);
+  const int c = static_cast<int>(q - div_by(q, g.by_c) * static_cast<uint32_t>(g.channels));
+  const f64x4_t p1 = channel_params(a1, c, g.eps);
+  const f64x4_t p2 = kDual ? channel_params(a2, c, g.eps) : p1;
+  const float o = epilogue<kDual, kRes, kAct>(
+      bf16_to_f32(x[i]), kDual ? bf16_to_f32(x2[i]) : 0.0f, kRes ? bf16_to_f32(res[i]) : 0.0f,
+      p1, p2);
+  y[i] = static_cast<uint16_t>(pack_bf16x2(o, 0.0f) & 0xffffu);
+}
+
+unsigned blocks_for(uint32_t items, uint32_t per_block) {
+  return (items + per_block - 1) / per_block;
+}
+
+template <bool kDual, bool kRes, int kAct>
+void launch_bn(const uint16_t* x, const uint16_t* x2, const uint16_t* res, uint16_t* y,
+               const Affine& a1, const Affine& a2, const BnGeom& g, bool aligned,
+               hipStream_t stream) {
+  const auto* xq = reinterpret_cast<const u32x4_t*>(x);
+  const auto* x2q = reinterpret_cast<const u32x4_t*>(x2);
+  const auto* rq = reinterpret_cast<const u32x4_t*>(res);
+  auto* yq = reinterpret_cast<u32x4_t*>(y);
+  const uint32_t cgroups = static_cast<uint32_t>(g.channels) / 8;
+  const size_t set_bytes = (kDual ? 2 : 1) * sizeof(f64x4_t);
+  if (aligned && g.d == 1 && g.channels % 8 == 0 && cgroups <= kBnThreads &&
+      set_bytes * static_cast<size_t>(g.channels) <= kMaxLdsBytes) {
+    const uint32_t positions = g.n / static_cast<uint32_t>(g.channels);
+    const uint32_t per_block = (kBnThreads / cgroups) * (kDual ? 4 : 8);
+    const size_t lds_bytes = set_bytes * static_cast<size_t>(g.channels);
+    bn_infer_nhwc<kDual, kRes, kAct><<<blocks_for(positions, per_block), kBnThreads, lds_bytes,
+                                       stream>>>(xq, x2q, rq, yq, a1, a2, g, positions, cgroups);
+    return;
+  }
+  uint32_t done = 0;
+  const uint32_t per_block = kBnThreads * kGroupsPerThread;
+  // planes one workgroup's 8 * per_block elements can touch, at most C
+  const uint32_t span = (8 * per_block - 1) / g.d + 2;
+  const uint32_t entries = span < static_cast<uint32_t>(g.channels) ? span : g.channels;
+  const size_t lds_bytes = set_bytes * entries;
+  if (aligned && g.n >= 8 && lds_bytes <= kMaxLdsBytes) {
+    const uint32_t groups = g.n / 8;
+    const unsigned blocks = blocks_for(groups, per_block);
+    if (g.d % 8 == 0)
+      bn_infer_vec<kDual, kRes, kAct, 1>
+          <<<blocks, kBnThreads, lds_bytes, stream>>>(xq, x2q, rq, yq, a1, a2, g, groups, entries);
+    else if (g.d >= 8)
+      bn_infer_vec<kDual, kRes, kAct, 2>
+          <<<blocks, kBnThreads, lds_bytes, stream>>>(xq, x2q, rq, yq, a1, a2, g, groups, entries);
+    else
+      bn_infer_vec<kDual, kRes, kAct, 0>
+          <<<blocks, kBnThreads, lds_bytes, stream>>>(xq, x2q, rq, yq, a1, a2, g, groups, entries);
+    done = groups * 8;
+  }
+  if (done < g.n)
+    bn_infer_scalar<kDual, kRes, kAct><<<blocks_for(g.n - done, kBnThreads), kBnThreads, 0,
+                                         stream>>>(x, x2, res, y, a1, a2, g, done);
+}
+
+template <bool kDual, bool kRes>
+void launch_act(int act, const uint16_t* x, const uint16_t* x2, const uint16_t* res, uint16_t* y,
+                const Affine& a1, const Affine& a2, const BnGeom& g, bool aligned,
+                hipStream_t stream) {
+  switch (act) {
+    case 0: launch_bn<kDual, kRes, 0>(x, x2, res, y, a1, a2, g, aligned, stream); break;
+    case 1: launch_bn<kDual, kRes, 1>(x, x2, res, y, a1, a2, g, aligned, stream); break;
+    default: launch_bn<kDual, kRes, 2>(x, x2, res, y, a1, a2, g, aligned, stream); break;
+  }
+}
+
+}  // namespace
+}  // namespace hipo
+
+extern "C" int hipo_bn_infer_act_bf16(const uint16_t* x, const uint16_t* mean,
+                                      const uint16_t* var, const uint16_t* weight,
+                                      const uint16_t* bias, const uint16_t* x2,
+                                      const uint16_t* mean2, const uint16_t* var2,
+                                      const uint16_t* weight2, const uint16_t* bias2,
+                                      const uint16_t* residual, uint16_t* y, int64_t n,
+                                      int64_t c, int64_t hw, int channels_last, float eps,
+                                      int act, hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  HIPO_REQUIRE(n >= 0 && c >= 0 && hw >= 0, "bn_infer: negative size");
+  HIPO_REQUIRE(c <= kMaxChannels, "bn_infer: at most %d channels (got %lld)", kMaxChannels,
+               (long long)c);
+  HIPO_REQUIRE(act >= 0 && act <= 2, "bn_infer: act must be 0 (none), 1 (relu) or 2 (relu6)");
+  if (n == 0 || c == 0 || hw == 0) return 0;
+  HIPO_REQUIRE(n <= (int64_t{1} << 31) / (c * hw) && n * c * hw <= (int64_t{1} << 31) - 16,
+               "bn_infer: at most 2^31 - 16 elements");
+  HIPO_REQUIRE(x && mean && var && weight && bias && y, "bn_infer: null pointer");
+  const bool dual = x2 != nullptr;
+  HIPO_REQUIRE(!dual || (mean2 && var2 && weight2 && bias2),
+               "bn_infer: the second affine needs all four parameters");
+  BnGeom g;
+  g.n = static_cast<uint32_t>(n * c * hw);
+  g.channels = static_cast<int>(c);
+  g.d = channels_last ? 1u : static_cast<uint32_t>(hw);
+  g.by_d = div_magic(g.d);
+  g.by_c = div_magic(static_cast<uint32_t>(c));
+  g.eps = eps;
+  const Affine a1{mean, var, weight, bias};
+  const Affine a2{mean2, var2, weight2, bias2};
+  const bool aligned = aligned16(x) && aligned16(y) && (!dual || aligned16(x2)) &&
+                       (residual == nullptr || aligned16(residual));
+  if (dual) {
+    if (residual) launch_act<true, true>(act, x, x2, residual, y, a1, a2, g, aligned, stream);
+    else launch_act<true, false>(act, x, x2, residual, y, a1, a2, g, aligned, stream);
+  } else {
+    if (residual) launch_act<false, true>(act, x, x2, residual, y, a1, a2, g, aligned, stream);
+    else launch_act<false, false>(act, x, x2, residual, y, a1, a2, g, aligned, stream);
+  }
+  return check_launch("bn_infer_act_bf16");
+}

@@ -93,6 +93,18 @@ def test_abi_version_and_error_string(lib):
      b"workspace"),
     (lambda l: l.hipo_cast_bf16_to_f32(16, 16, -1, None), b"negative"),
     (lambda l: l.hipo_cast_f32_to_bf16(None, 16, 8, None), b"null"),
+    (lambda l: l.hipo_bn_infer_act_bf16(*([16] * 5), *([None] * 6), 16, -1, 8, 4, 0, 1e-5, 1,
+                                        None), b"negative"),
+    (lambda l: l.hipo_bn_infer_act_bf16(*([16] * 5), *([None] * 6), 16, 2, 4097, 4, 0, 1e-5, 1,
+                                        None), b"channels"),
+    (lambda l: l.hipo_bn_infer_act_bf16(*([16] * 5), *([None] * 6), 16, 2, 8, 4, 0, 1e-5, 3,
+                                        None), b"act"),
+    (lambda l: l.hipo_bn_infer_act_bf16(*([16] * 5), *([None] * 6), 16, 1 << 20, 4096, 1024, 1,
+                                        1e-5, 0, None), b"2^31"),
+    (lambda l: l.hipo_bn_infer_act_bf16(16, None, 16, 16, 16, *([None] * 6), 16, 2, 8, 4, 0,
+                                        1e-5, 0, None), b"null"),
+    (lambda l: l.hipo_bn_infer_act_bf16(*([16] * 5), 16, 16, None, 16, 16, None, 16, 2, 8, 4, 1,
+                                        1e-5, 1, None), b"second affine"),
 ])
 def test_argument_errors_before_launch(lib, call, msg):
     assert call(lib) == HIPO_EINVAL
@@ -113,6 +125,8 @@ def test_empty_inputs_are_no_ops(lib):
     assert lib.hipo_gelu_erf_bwd_colsum_bf16(None, None, None, None, 0, 0, None, 0, None) == 0
     assert lib.hipo_cast_bf16_to_f32(None, None, 0, None) == 0
     assert lib.hipo_cast_f32_to_bf16(None, None, 0, None) == 0
+    for dims in ((0, 8, 4), (2, 0, 4), (2, 8, 0)):
+        assert lib.hipo_bn_infer_act_bf16(*([None] * 12), *dims, 0, 1e-5, 1, None) == 0
     assert lib.hipo_last_error() == b""
 
 
