@@ -6,8 +6,8 @@
 // GELU_tanh(t) = 0.5 t (1 + tanh(u)), u = sqrt(2/pi) (t + 0.044715 t^3).
 // t is a bf16 value, so the output is a function of its 65536 bit patterns,
 // and the kernel returns the correctly rounded bf16 of the exact function
-// (gelu_bf16.h: a 7 KiB table staged once per workgroup in LDS, bit
-// arithmetic outside its range).
+// (gelu_bf16.h: an fp32 evaluation for t > -4 that rounds correctly for
+// every such bf16 t, the exact table in global memory below that).
 //
 // Layout: one wave64 per tile of 64 channels x 64 spatial positions of one
 // image.  Lane l owns an 8x8 (channel x position) block: cb = l / 8 picks 8
@@ -20,9 +20,11 @@
 // thread workgroup takes four consecutive tiles (with C = 256: all channel
 // groups of one position tile, i.e. 64 whole NHWC rows).  The grid is one-
 // shot (no persistent loop): on MI355X many short workgroups dispatched in
-// order keep the chip's in-flight address window compact, which measured
-// 67.5 us for config 2 against 71 us for a persistent one-workgroup-per-CU
-// version of this kernel with the GELU read from a 128 KiB LDS table.
+// order keep the chip's in-flight address window compact (a persistent
+// one-workgroup-per-CU version of this kernel ran 71 us at config 2).  The
+// kernel uses no LDS and has no barrier: a 7 KiB table staged into LDS by
+// every workgroup cost 3-5 us at config 2 (25,088 waves, each waiting at the
+// barrier for the table before its first lookup).
 // Loads and stores are non-temporal.  Launches of at most 2^19 elements
 // (and shapes off the 16-byte vector path) take a one-element-per-thread
 // kernel instead.
@@ -35,7 +37,9 @@ namespace {
 
 constexpr int kTileHw = 64;  // positions per wave tile
 constexpr int kTileC = 64;   // channels per wave tile
-constexpr int kWavesPerBlock = 4;
+constexpr int kWavesC = 4;  // waves of a workgroup along channels (consecutive channel tiles)
+constexpr int kWavesP = 1;  // and along positions (consecutive position tiles)
+constexpr int kWavesPerBlock = kWavesC * kWavesP;
 constexpr int kBlockThreads = kWavesPerBlock * kWave;
 constexpr int kTilesPerWave = 1;  // consecutive position tiles per wave (3-D grid)
 constexpr int64_t kTileMinElems = int64_t{1} << 19;  // smaller launches: scalar kernel
@@ -45,8 +49,8 @@ struct TileGeom {
   int c_tiles, hw_tiles, ntiles;  // ntiles < 2^31 (checked on the host)
 };
 
-// GRID3: the grid carries the tile coordinates (x = group of kWavesPerBlock
-// channel tiles, y = position tile, z = image), so a workgroup starts its
+// GRID3: the grid carries the tile coordinates (x = group of kWavesC channel
+// tiles, y = group of kWavesP x TPW position tiles, z = image), so a workgroup starts its
 // loads without integer divisions (66.1 against 66.6 us at config 2); the
 // dispatch order is the 1-D numbering's.  Otherwise (grids past the y / z
 // limits) the block index is split by division.
@@ -54,17 +58,16 @@ template <bool GRID3, int TPW>
 __global__ __launch_bounds__(kBlockThreads) void bias_gelu_nchw_to_nhwc_tiles(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ out, TileGeom g) {
-  __shared__ __align__(16) uint16_t lut[kGeluTableSize];
   const int lane = threadIdx.x & (kWave - 1);
   int ct, ht0;
   int64_t img;
   bool tile_ok;  // wave-uniform
   if constexpr (GRID3) {
-    ct = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * kWavesPerBlock +
-                                        static_cast<int>(threadIdx.x >> 6));
-    tile_ok = ct < g.c_tiles;
-    if (!tile_ok) ct = 0;
-    ht0 = static_cast<int>(blockIdx.y) * TPW;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    ct = static_cast<int>(blockIdx.x) * kWavesC + wave % kWavesC;
+    ht0 = (static_cast<int>(blockIdx.y) * kWavesP + wave / kWavesC) * TPW;
+    tile_ok = ct < g.c_tiles && ht0 < g.hw_tiles;
+    if (!tile_ok) ct = 0, ht0 = 0;
     img = blockIdx.z;
   } else {
     static_assert(GRID3 || TPW == 1, "the 1-D numbering takes one tile per wave");
@@ -93,24 +96,9 @@ __global__ __launch_bounds__(kBlockThreads) void bias_gelu_nchw_to_nhwc_tiles(
           reinterpret_cast<const u32x4_t*>(x + in_off + j * g.HW));
   };
 
-  // Stage the GELU table (7 KiB, L2-resident) first: loads return in issue
-  // order, so its LDS writes and the barrier complete while the tile's HBM
-  // loads, issued after it, are still in flight.
-  u32x4_t tab[(kGeluTableChunks + kBlockThreads - 1) / kBlockThreads];
-#pragma unroll
-  for (int k = 0; k < (kGeluTableChunks + kBlockThreads - 1) / kBlockThreads; ++k) {
-    const int i = static_cast<int>(threadIdx.x) + k * kBlockThreads;
-    if (i < kGeluTableChunks) tab[k] = reinterpret_cast<const u32x4_t*>(kGeluTable)[i];
-  }
   u32x4_t va[8], vb[8];
   load_tile(ht0, va);
   const u32x4_t bw = *reinterpret_cast<const u32x4_t*>(bias + cl);
-#pragma unroll
-  for (int k = 0; k < (kGeluTableChunks + kBlockThreads - 1) / kBlockThreads; ++k) {
-    const int i = static_cast<int>(threadIdx.x) + k * kBlockThreads;
-    if (i < kGeluTableChunks) reinterpret_cast<u32x4_t*>(lut)[i] = tab[k];
-  }
-  __syncthreads();
   float b[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) b[j] = (j & 1) ? bf16hi(bw[j >> 1]) : bf16lo(bw[j >> 1]);
@@ -132,13 +120,10 @@ __global__ __launch_bounds__(kBlockThreads) void bias_gelu_nchw_to_nhwc_tiles(
         const float x0 = (i & 1) ? bf16hi(w0) : bf16lo(w0);
         const float x1 = (i & 1) ? bf16hi(w1) : bf16lo(w1);
         tt[k] = pack_bf16x2(x0 + b[2 * k], x1 + b[2 * k + 1]);
-        o[k] = gelu_pair_common(tt[k], lut);
-        rare |= gelu_pair_rare(tt[k]);
+        o[k] = gelu_pair_fast(tt[k], rare);
       }
       if (rare) {  // one branch per 8 values, rarely taken for ordinary data
-#pragma unroll
-        for (int k = 0; k < 4; ++k) o[k] = gelu_bits(tt[k] & 0xffffu, lut) |
-                                           (gelu_bits(tt[k] >> 16, lut) << 16);
+        gelu_exact_x8(tt, o);
       }
       __builtin_nontemporal_store(
           o, reinterpret_cast<u32x4_t*>(out + out_off + static_cast<int64_t>(i) * g.C));
@@ -215,8 +200,9 @@ extern "C" int hipo_bias_gelu_nchw_to_nhwc_bf16(const uint16_t* x,
     g.c_tiles = static_cast<int>(c_tiles);
     g.hw_tiles = static_cast<int>(hw_tiles);
     g.ntiles = static_cast<int>(ntiles);
-    const int64_t c_groups = (c_tiles + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int64_t hw_groups = (hw_tiles + kTilesPerWave - 1) / kTilesPerWave;
+    const int64_t c_groups = (c_tiles + kWavesC - 1) / kWavesC;
+    const int64_t hw_groups =
+        (hw_tiles + kWavesP * kTilesPerWave - 1) / (kWavesP * kTilesPerWave);
     if (hw_groups <= 65535 && n <= 65535) {
       const dim3 grid(static_cast<unsigned>(c_groups), static_cast<unsigned>(hw_groups),
                       static_cast<unsigned>(n));

@@ -1,8 +1,8 @@
 // GELU(tanh) of a contiguous tensor, element by element (no layout change).
 //
 // bf16: y = the correctly rounded bf16 GELU_tanh(x) for every bf16 x, by bit
-//   pattern (gelu_bf16.h): a 7 KiB table of correctly rounded results staged
-//   once per workgroup in LDS, bit arithmetic outside its range.  The
+//   pattern (gelu_bf16.h): an fp32 evaluation that rounds correctly for
+//   x > -4, the exact table in global memory below that.  The
 //   repro's eager graph rounds every intermediate to bf16 (its 1 + tanh(u)
 //   cancels in the negative tail); Inductor and the reference's Triton
 //   oracle evaluate the chain in fp32 and round once -- the exact result is
@@ -35,26 +35,16 @@ namespace {
 
 constexpr int kGeluWaves = 4;
 constexpr int kGeluThreads = kGeluWaves * kWave;
-constexpr int kTabPerThread = (kGeluTableChunks + kGeluThreads - 1) / kGeluThreads;
 
 template <int U>
 __global__ __launch_bounds__(kGeluThreads) void gelu_bf16_flat(
     const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int64_t nvec) {
-  __shared__ __align__(16) uint16_t lut[kGeluTableSize];
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t v0 =
       (static_cast<int64_t>(blockIdx.x) * kGeluWaves + (threadIdx.x >> 6)) * (U * kWave) + lane;
   const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x);
   u32x4_t* yv = reinterpret_cast<u32x4_t*>(y);
 
-  // The table's loads first (L2-resident), then the data's, so the table's
-  // LDS writes and the barrier overlap the HBM loads in flight.
-  u32x4_t tab[kTabPerThread];
-#pragma unroll
-  for (int k = 0; k < kTabPerThread; ++k) {
-    const int i = static_cast<int>(threadIdx.x) + k * kGeluThreads;
-    if (i < kGeluTableChunks) tab[k] = reinterpret_cast<const u32x4_t*>(kGeluTable)[i];
-  }
   u32x4_t v[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -63,25 +53,14 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_bf16_flat(
     v[u] = __builtin_nontemporal_load(xv + (i < nvec ? i : nvec - 1));
   }
 #pragma unroll
-  for (int k = 0; k < kTabPerThread; ++k) {
-    const int i = static_cast<int>(threadIdx.x) + k * kGeluThreads;
-    if (i < kGeluTableChunks) reinterpret_cast<u32x4_t*>(lut)[i] = tab[k];
-  }
-  __syncthreads();
-
-#pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t i = v0 + u * kWave;
     u32x4_t o;
     bool rare = false;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      o[k] = gelu_pair_common(v[u][k], lut);
-      rare |= gelu_pair_rare(v[u][k]);
-    }
+    for (int k = 0; k < 4; ++k) o[k] = gelu_pair_fast(v[u][k], rare);
     if (rare) {  // one branch per 8 values, rarely taken for ordinary data
-#pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = gelu_pair(v[u][k], lut);
+      gelu_exact_x8(v[u], o);
     }
     if (i < nvec) __builtin_nontemporal_store(o, yv + i);
   }
