@@ -170,26 +170,65 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// Full-wave maximum with NaN propagation (IEEE 754-2019 maximum: NaN if
+// any lane holds NaN; v_maximum3_f32 on gfx950, so no operand
+// canonicalisation as fmaxf needs); every lane receives it.
+__device__ __forceinline__ float wave_maximum(float v) {
+  v = __builtin_elementwise_maximum(v, dpp<kDppQuadXor1>(v));
+  v = __builtin_elementwise_maximum(v, dpp<kDppQuadXor2>(v));
+  v = __builtin_elementwise_maximum(v, dpp<kDppRowRor4>(v));
+  v = __builtin_elementwise_maximum(v, dpp<kDppRowRor8>(v));
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b),
+                                       __builtin_elementwise_maximum(c, d));
+}
+
 // e^x in fp32 to about one ulp, for x in [-104, 89] (NaN propagates), by
-// the extended-precision reduction of the device library's expf: x*log2(e)
-// is the rounded product ph plus a residual pl carried to first order (the
-// product's exact rounding error from an FMA, plus x times the rounding
-// error of the constant), so e^x = 2^ph * 2^pl = r * (1 + pl * ln2) with
-// r = 2^ph from the hardware exp2 (|pl| <= 2^-17 here, so the dropped
-// second-order term is below 2^-35 relative; the product form keeps
-// r = inf and r = 0 exact).  Unlike the library routine
-// the result is not rescaled by ldexp: results below 2^-126 (x < -87.3) are
-// whatever the hardware exp2 gives there (denormal or zero) -- below any
-// bf16 rounding these kernels apply.  Callers clamp x first (exp_domain):
+// a Cody-Waite reduction: ph = x * log2(e) rounded (any rounding of it is
+// absorbed below), r = x - ph * ln2 with ln2 split into hi + lo (two FMAs;
+// the first is exact to within 2^-24 of its tiny result, so r carries
+// x's full precision: |r| <= ~6e-6 here, accurate to ~1e-13), and
+// e^x = 2^ph * e^r with 2^ph from the hardware exp2 and e^r = 1 + r
+// (r^2 / 2 <= 2e-11 is below fp32's 2^-24).  exp_f32 forms 2^ph * (1 + r):
+// the product keeps 2^ph = inf (x up to 89: e^89 overflows) and 2^ph = 0
+// exact; exp_f32_nonpos, for x <= 0 only (2^ph <= 1, never inf), forms
+// fma(2^ph, r, 2^ph), one instruction and one rounding fewer (the fma
+// would give inf * r + inf = NaN for an overflowed 2^ph and r <= 0).
+// Results below 2^-126 (x < -87.3) are whatever the hardware exp2 gives
+// there (denormal or zero) -- below any bf16 rounding these kernels apply.
+// Callers clamp x first (exp_domain, or at -104 for exp_f32_nonpos):
 // e^-104 rounds to 0, e^89 overflows to inf.
 constexpr float kLog2eHi = 1.4426950216293335f;   // log2(e) rounded to fp32
-constexpr float kLog2eLo = 1.9259629891e-8f;      // log2(e) - kLog2eHi
-constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLn2Hi = 0.6931471824645996f;     // ln 2 rounded to fp32
+constexpr float kLn2Lo = -1.9046542121259336e-09f;  // ln 2 - kLn2Hi, rounded
+__device__ __forceinline__ float exp_reduce(float x, float& ph) {
+  ph = x * kLog2eHi;
+  return __builtin_fmaf(-ph, kLn2Lo, __builtin_fmaf(-ph, kLn2Hi, x));
+}
 __device__ __forceinline__ float exp_f32(float x) {
-  const float ph = x * kLog2eHi;
-  const float pl = __builtin_fmaf(x, kLog2eLo, __builtin_fmaf(x, kLog2eHi, -ph));
-  const float r = __builtin_amdgcn_exp2f(ph);
-  return r * __builtin_fmaf(pl, kLn2, 1.0f);
+  float ph;
+  const float r = exp_reduce(x, ph);
+  return __builtin_amdgcn_exp2f(ph) * (1.0f + r);
+}
+__device__ __forceinline__ float exp_f32_nonpos(float x) {
+  float ph;
+  const float r = exp_reduce(x, ph);
+  const float e = __builtin_amdgcn_exp2f(ph);
+  return __builtin_fmaf(e, r, e);
+}
+
+// e / sum correctly rounded (the IEEE quotient), given inv = 1 / sum
+// correctly rounded: q = e * inv is within 1.5 ulp of e / sum, and one FMA
+// step with the exact remainder e - q * sum gives the rounded quotient
+// (Markstein's correction; pinned against exact rational arithmetic over
+// the softmax domain, e in (0, 1], sum in [1, 2048], by a CPU test).  2
+// FMAs per element where a full division takes ~10 instructions.
+__device__ __forceinline__ float div_rn(float e, float sum, float inv) {
+  const float q = e * inv;
+  return __builtin_fmaf(__builtin_fmaf(-q, sum, e), inv, q);
 }
 
 // Clamp to the domain of exp_f32; NaN stays NaN (IEEE 754-2019 maximum /

@@ -3,10 +3,12 @@
 // Semantics (softmax(x * scale + mask, -1) on bf16, scores formed in fp32
 // as the reference's Triton oracles and Inductor form them):
 //   s = fma(x, scale, mask[q, :])                  (fp32, one rounding)
-//   out = bf16(exp(s - max(s)) / sum(exp(s - max(s))))   (fp32 max and sum)
+//   out = bf16(exp(s - max(s)) / sum(exp(s - max(s))))   (fp32 max and sum;
+//         the quotient is the IEEE fp32 division's, div_rn)
 // exp is natural exp of the fp32 difference s - max(s) (as aten.exp and
-// Inductor's libdevice.exp), evaluated to about one ulp by exp_f32, the
-// device library's extended-precision reduction (no exp2 rewrite).  Eager
+// Inductor's libdevice.exp), evaluated to about one ulp by exp_f32_nonpos,
+// an extended-precision (Cody-Waite) reduction as the device library's
+// (no exp2 rewrite).  Eager
 // rounds x * scale and the sum to bf16 first; with a power-of-two scale and
 // a 0 / -inf mask (the causal softmax) both roundings are exact, so the
 // scores are eager's; with a general bias (TrOCR) the fp32 scores are the
@@ -16,14 +18,15 @@
 // Layout: rows held in registers, non-temporal 16-byte streaming accesses
 // for x and out; the mask row (mask[q, :], q = row % Q) is re-read by every
 // batch entry and stays cache-resident.  Row max and row sum: DPP within a
-// wave, then a fixed-order combine of the wave results through LDS.  Three
+// wave, then (where a row spans several waves) a fixed-order combine of the
+// wave results through LDS.  Three
 // kernels by row length:
 //   K <= 512: L lanes per row, 64 / L rows per access instruction, 2 KiB of
 //     x per wave, reductions within lane segments, no LDS;
-//   K = 1024 or 2048 (config [384, 1024, 1024]): 1 KiB of x per wave and
-//     row, each wave taking RPW = 4 rows with their loads issued together,
-//     the rows of one q for 4 RPW / W batch entries in a 256-thread
-//     workgroup, their shared mask row loaded once and staged through LDS;
+//   K = 1024 or 2048 (config [384, 1024, 1024]): one wave per row (2 or 4
+//     KiB of x), the rows of one q for 4 consecutive batch entries in a
+//     256-thread workgroup, their shared mask row loaded once and staged
+//     through LDS, row reductions within the wave;
 //   otherwise (or a per-batch mask the grouping cannot share): the
 //     row_layout.h plan, W waves per row, 2 KiB per wave.
 // HBM-bound: algorithmic bytes per element = 2 (read) + 2 (write), plus the
@@ -36,9 +39,9 @@ namespace {
 // exp(s - m): masked entries (s = -inf) give exactly 0; (-inf) - (-inf)
 // gives NaN for an all-masked row, exactly as the eager formula.
 __device__ __forceinline__ float exp_shifted(float s, float m) {
-  // s - m <= 0 (m is the row max) or NaN, so only exp_f32's lower bound
-  // needs the clamp (IEEE maximum: NaN stays NaN).
-  return exp_f32(__builtin_elementwise_maximum(s - m, -104.0f));
+  // s - m <= 0 (m is the row max) or NaN, so only the lower bound needs
+  // the clamp (IEEE maximum: NaN stays NaN).
+  return exp_f32_nonpos(__builtin_elementwise_maximum(s - m, -104.0f));
 }
 
 template <int U, int WT>
@@ -112,10 +115,9 @@ __global__ __launch_bounds__(kRowMaxThreads) void masked_softmax_rows(
   for (int u = 0; u < U; ++u) {
     const int64_t col = row_group_col(u, waves_per_row, p);
     u32x4_t o;
-    o[0] = pack_bf16x2(s[u][0] * inv, s[u][1] * inv);
-    o[1] = pack_bf16x2(s[u][2] * inv, s[u][3] * inv);
-    o[2] = pack_bf16x2(s[u][4] * inv, s[u][5] * inv);
-    o[3] = pack_bf16x2(s[u][6] * inv, s[u][7] * inv);
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      o[d] = pack_bf16x2(div_rn(s[u][2 * d], sum, inv), div_rn(s[u][2 * d + 1], sum, inv));
     if (p.valid && col < K) row_store_stream(orow, col, o);
   }
 }
@@ -185,10 +187,12 @@ __global__ __launch_bounds__(kShortThreads) void masked_softmax_short_rows(
       s[e] = exp_shifted(s[e], m);
       sum += s[e];
     }
-    const float inv = 1.0f / seg_sum<L>(sum);
+    const float tot = seg_sum<L>(sum);
+    const float inv = 1.0f / tot;
     u32x4_t o;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) o[d] = pack_bf16x2(s[2 * d] * inv, s[2 * d + 1] * inv);
+    for (int d = 0; d < 4; ++d)
+      o[d] = pack_bf16x2(div_rn(s[2 * d], tot, inv), div_rn(s[2 * d + 1], tot, inv));
     if (row[v] < rows && col_in)
       __builtin_nontemporal_store(
           o, reinterpret_cast<u32x4_t*>(out + static_cast<int64_t>(row[v]) * K + col));
@@ -206,144 +210,140 @@ void launch_short(dim3 grid, hipStream_t stream, const uint16_t* x, const uint16
       x, mask, out, r, q, qd, static_cast<int>(K), ms, mbs, hd, scale);
 }
 
-// Rows of exactly K = 1024 or 2048 (KC, a compile-time constant):
-// 256-thread workgroups, W = KC / 512 waves per row (one 16-byte group per
-// lane: 1 KiB of x per wave and row, no idle lanes), NR = 4 / W row slots
-// per workgroup, RPW rows per slot.  Workgroup (q, y, z) of the 3-D grid
-// takes the rows (b0 + i) * Q + q, i < NR * RPW, b0 = (z * gy + y) * NR *
-// RPW: the same q of NR * RPW consecutive batch entries, which share one
-// mask row; slot rr holds entries b0 + rr + NR * j, j < RPW, whose loads a
-// wave issues together before working through them.  z is the mask's batch
-// group (offset z * mask_batch_stride; a single z when the mask is
-// broadcast over batch) and gy its workgroups along y, so the kernel does
-// no integer division; x is fastest, so dispatch order walks q in memory
-// order.  The mask row (2 KC bytes, 2 KC / 256 per thread) is loaded once
-// per workgroup, issued before the x loads, and staged through LDS; row max
-// and sum combine the W wave results through LDS in a fixed order.  Rows
-// past the batch end (NR * RPW not dividing a broadcast batch) re-read the
-// last batch entry and store nothing.
-// With the accurate exp (exp_f32: about 9 issue slots per element against
-// 5 for a bare exp2) one row per wave ran at 288-291 us at [384, 1024,
-// 1024]; issuing 2 / 4 / 8 / 16 rows' loads per wave 280 / 271-276 /
-// 275-280 / 303-306 us (the bare exp2 form, one row per wave, 269-273 us on
-// the same boxes).
-// Measured on MI355X (graph loop, rotating buffers, 2 B read + 2 B written
-// per element, % of 8 TB/s), [384, 1024, 1024]: one wave per row with every
-// wave reading its own mask row (the row-plan kernel) 261.6-263.5 us
-// (76.6-77.0 %); this layout with the block index split by division 272.2
-// us, with a 3-D grid and a runtime K 252.7-255.0 us, with K fixed 245.4
-// us = a flat copy of the same bytes; 512-thread workgroups (NR = 4 or 8)
-// 260-267 us.  [192, 1024, 2048]: 258.7-260.1 us against 253.3 us.  With a
-// runtime K and idle lanes (K = 776, 1032) the layout lost 8-15 % to the
-// row-plan kernel, so other row lengths stay there.
-template <int KC, int RPW>
-__global__ __launch_bounds__(256) void masked_softmax_shared_mask(
+// Rows of exactly K = 1024 or 2048 (KC, a compile-time constant): whole
+// rows per wave, the shared mask row staged once per workgroup.  Workgroup
+// (q, y, z) of the 3-D grid takes the NW * RPW rows (b0 + wave + NW i) * Q +
+// q, b0 = (z * gy + y) * NW * RPW: the same q of consecutive batch entries,
+// which share mask[q, :]; z is the mask's batch group (offset z *
+// mask_batch_stride; a single z when the mask is broadcast over batch) and
+// gy its workgroups along y, so the kernel does no integer division; x is
+// fastest, so dispatch order walks q in memory order.  Each wave owns its
+// RPW rows entirely -- G = KC / 512 16-byte groups per lane per row, group g
+// covering columns [512 g, 512 g + 512) across the wave -- so a row's max
+// and sum are wave reductions with no LDS exchange, and the only barrier is
+// the mask staging (the row's 2 KC bytes, loaded before the x rows).  A
+// column group whose 512 scores are all -inf in a row (the causal upper
+// triangle: group 1 of every row q < 512 at K = 1024) skips its exp.  Rows
+// past the batch end re-read the last batch entry and store nothing.
+// Measured at [384, 1024, 1024] (steady loop, same process; a flat copy of
+// the same bytes 246.9-247.5 us): 4 waves x 1 row (shipped) 252.9-254.6 us;
+// 4 x 2 rows 258.3-259.9; 4 x 4 rows 270.7; 2 / 8 waves x 1 row 257.3-258.2
+// / 258.5-258.8; the previous layout (2 waves per row, 1 KiB each, 4 rows
+// per wave, maxima and sums exchanged through LDS) 258.0-261.8; 8
+// consecutive rows of one batch entry per workgroup, each wave reading its
+// mask rows through the cache, 274.2-275.7.  Timing probes of the 4 x 2
+// layout with the exp replaced by a bare exp2, or removed, or without the
+// division correction, all ran 258-260 us: these rows are bound by their
+// memory pattern, not by arithmetic.
+template <int KC, int NW, int RPW>
+__global__ __launch_bounds__(NW * 64) void masked_softmax_wave_rows(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ mask,
     uint16_t* __restrict__ out, uint32_t batch, uint32_t Q, uint32_t gy,
     int64_t mask_stride, int64_t mask_batch_stride, float scale) {
-  constexpr int W = KC / 512;
-  constexpr int NR = 4 / W;
-  static_assert(W * NR * kWave == 256 && W * kWave * kRowGroup == KC, "full rows");
-  constexpr int kStageWords = KC / 512;  // 32-bit words of the mask row per thread
+  constexpr int G = KC / 512;
+  constexpr int kThreads = NW * kWave;
+  constexpr int kStageWords = KC / 2 / kThreads;  // 32-bit mask words per thread
+  static_assert(kStageWords * kThreads * 2 == KC, "the mask row splits evenly");
   __shared__ __align__(16) uint32_t mrow[KC / 2];  // read back as 16-byte groups
-  __shared__ float pmax[RPW][W * NR], psum[RPW][W * NR];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
-  const int w = wave % W;
-  const int rr = wave / W;
   const uint32_t q = blockIdx.x;
-  // The workgroup's NR * RPW rows: batch entries b0 + rr + NR * i of query q;
-  // wave (rr, w) takes the RPW rows of slot rr, all loads issued up front.
-  const uint32_t b0 = (blockIdx.z * gy + blockIdx.y) * (NR * RPW) + rr;
+  const uint32_t b0 = (blockIdx.z * gy + blockIdx.y) * (NW * RPW) + wave;
 
-  const uint16_t* mr = mask + blockIdx.z * mask_batch_stride +
-                       static_cast<int64_t>(q) * mask_stride;
-  const int st = static_cast<int>(threadIdx.x) * kStageWords;  // first word staged
+  const uint32_t* mr = reinterpret_cast<const uint32_t*>(
+      mask + blockIdx.z * mask_batch_stride + static_cast<int64_t>(q) * mask_stride);
   uint32_t mval[kStageWords];
-  if constexpr (kStageWords == 2) {
-    const u32x2_t v = *reinterpret_cast<const u32x2_t*>(mr + 2 * st);
-    mval[0] = v[0];
-    mval[1] = v[1];
-  } else {
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(mr + 2 * st);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mval[i] = v[i];
-  }
-  const int col = (w * kWave + lane) * kRowGroup;
-  u32x4_t xv[RPW];
+  for (int k = 0; k < kStageWords; ++k) mval[k] = mr[threadIdx.x + k * kThreads];
+  u32x4_t xv[RPW][G];
   int64_t row[RPW];
   bool row_ok[RPW];
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
-    const uint32_t b = b0 + NR * i;
+    const uint32_t b = b0 + NW * i;
     row_ok[i] = b < batch;
     // Rows past the batch end re-read the last batch entry and store nothing.
     row[i] = static_cast<int64_t>(row_ok[i] ? b : batch - 1) * Q + q;
-    xv[i] = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4_t*>(x + row[i] * KC + col));
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      xv[i][g] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(x + row[i] * KC + g * 512 + lane * kRowGroup));
   }
 #pragma unroll
-  for (int i = 0; i < kStageWords; ++i) mrow[st + i] = mval[i];
+  for (int k = 0; k < kStageWords; ++k) mrow[threadIdx.x + k * kThreads] = mval[k];
   __syncthreads();
-  const u32x4_t mv = *reinterpret_cast<const u32x4_t*>(&mrow[col / 2]);
+  u32x4_t mv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    mv[g] = *reinterpret_cast<const u32x4_t*>(&mrow[(g * 512 + lane * kRowGroup) / 2]);
 
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
-    float s[8];
-    float lmax = -__builtin_inff();  // NaN-propagating: NaN if any score is
+    float sc[G][8];
+    float gmax[G];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      s[2 * d] = __builtin_fmaf(bf16lo(xv[i][d]), scale, bf16lo(mv[d]));
-      s[2 * d + 1] = __builtin_fmaf(bf16hi(xv[i][d]), scale, bf16hi(mv[d]));
-      lmax = __builtin_elementwise_maximum(
-          lmax, __builtin_elementwise_maximum(s[2 * d], s[2 * d + 1]));
-    }
-    float m = wave_max(lmax);  // fmaxf: the row max of the non-NaN scores
-    if (lane == 0) pmax[i][wave] = m;
-    __syncthreads();
-    m = pmax[i][rr * W];
+    for (int g = 0; g < G; ++g) {
+      gmax[g] = -__builtin_inff();  // NaN-propagating: NaN if any score is
 #pragma unroll
-    for (int k = 1; k < W; ++k) m = fmaxf(m, pmax[i][rr * W + k]);
-
-    // A lane whose 8 scores are all -inf (a fully masked group: the causal
-    // mask's upper triangle makes whole waves of them) has exp = 0 for each;
-    // a NaN score makes lmax NaN, so it still goes through exp and poisons
-    // the row as in eager.
-    float sum = 0.f;
-    if (lmax == -__builtin_inff()) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s[e] = 0.f;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        s[e] = exp_shifted(s[e], m);
-        sum += s[e];
+      for (int d = 0; d < 4; ++d) {
+        sc[g][2 * d] = __builtin_fmaf(bf16lo(xv[i][g][d]), scale, bf16lo(mv[g][d]));
+        sc[g][2 * d + 1] = __builtin_fmaf(bf16hi(xv[i][g][d]), scale, bf16hi(mv[g][d]));
+        gmax[g] = __builtin_elementwise_maximum(
+            gmax[g], __builtin_elementwise_maximum(sc[g][2 * d], sc[g][2 * d + 1]));
       }
     }
-    sum = wave_sum(sum);
-    if (lane == 0) psum[i][wave] = sum;
-    __syncthreads();
-    sum = psum[i][rr * W];
+    float lmax = gmax[0];
 #pragma unroll
-    for (int k = 1; k < W; ++k) sum += psum[i][rr * W + k];
-    const float inv = 1.0f / sum;
-
-    u32x4_t o;
+    for (int g = 1; g < G; ++g) lmax = __builtin_elementwise_maximum(lmax, gmax[g]);
+    const float m = wave_maximum(lmax);
+    // A column group that is -inf in every lane skips its exp (wave-
+    // uniform); a lane of -inf scores in a live group gets exp = 0 from the
+    // clamped argument; a NaN score keeps its group live, so the NaN reaches
+    // the row sum, as in eager.
+    bool live[G];
+    float sum = 0.f;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) o[d] = pack_bf16x2(s[2 * d] * inv, s[2 * d + 1] * inv);
-    if (row_ok[i])
-      __builtin_nontemporal_store(o, reinterpret_cast<u32x4_t*>(out + row[i] * KC + col));
+    for (int g = 0; g < G; ++g) {
+      live[g] = __builtin_amdgcn_ballot_w64(!(gmax[g] == -__builtin_inff())) != 0;
+      if (live[g]) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sc[g][e] = exp_shifted(sc[g][e], m);
+        sum += ((sc[g][0] + sc[g][1]) + (sc[g][2] + sc[g][3])) +
+               ((sc[g][4] + sc[g][5]) + (sc[g][6] + sc[g][7]));
+      }
+    }
+    const float tot = wave_sum(sum);
+    const float inv = 1.0f / tot;
+    // p = e / sum, the IEEE quotient (div_rn), rounded to bf16.  A skipped
+    // group's outputs are 0 * (1 / sum): 0, or NaN for a row whose every
+    // score is -inf (sum 0), as in eager.
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      u32x4_t o;
+      if (live[g]) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          o[d] = pack_bf16x2(div_rn(sc[g][2 * d], tot, inv), div_rn(sc[g][2 * d + 1], tot, inv));
+      } else {
+        const uint32_t z = pack_bf16x2(0.f * inv, 0.f * inv);
+        o = u32x4_t{z, z, z, z};
+      }
+      if (row_ok[i])
+        __builtin_nontemporal_store(
+            o, reinterpret_cast<u32x4_t*>(out + row[i] * KC + g * 512 + lane * kRowGroup));
+    }
   }
 }
 
-// Rows per wave of the shared-mask kernel (consecutive rows of one query in
-// steps of NR batch entries; their loads are issued together).
-constexpr int kSharedMaskRowsPerWave = 4;
+// Waves per workgroup and rows per wave of the whole-row kernel (a
+// workgroup's rows: one query q of NW * RPW consecutive batch entries).
+constexpr int kSharedMaskWaves = 4;
+constexpr int kSharedMaskRowsPerWave = 1;
 
-// Launch shape of the shared-mask kernel: its row length (1024 or 2048; 0
+// Launch shape of the whole-row kernel: its row length (1024 or 2048; 0
 // when the kernel does not apply) and the 3-D grid.  It does not apply to
-// other K, to a per-batch mask whose heads groups the NR * RPW rows of a workgroup do not
-// divide, or to grids beyond the y / z limits.
+// other K, to a per-batch mask whose heads groups the NW * RPW rows of a
+// workgroup do not divide, or to grids beyond the y / z limits.
 struct SharedMaskPlan {
   int k = 0;
   uint32_t gy = 0;  // workgroups along y per mask batch group
@@ -354,7 +354,7 @@ SharedMaskPlan shared_mask_plan(int64_t batch, int64_t Q, int64_t K, int64_t mbs
                                 int64_t heads) {
   SharedMaskPlan plan;
   if ((K != 1024 && K != 2048) || Q > 0x7fffffff) return plan;
-  const int nr = (K == 1024 ? 2 : 1) * kSharedMaskRowsPerWave;  // rows per workgroup
+  const int nr = kSharedMaskWaves * kSharedMaskRowsPerWave;  // rows per workgroup
   int64_t gy, gz;
   if (mbs == 0) {
     gy = (batch + nr - 1) / nr;
@@ -376,7 +376,8 @@ template <int KC>
 void launch_shared_mask(const SharedMaskPlan& plan, hipStream_t stream, const uint16_t* x,
                         const uint16_t* mask, uint16_t* out, int64_t batch, int64_t Q,
                         int64_t ms, int64_t mbs, float scale) {
-  masked_softmax_shared_mask<KC, kSharedMaskRowsPerWave><<<plan.grid, dim3(256), 0, stream>>>(
+  masked_softmax_wave_rows<KC, kSharedMaskWaves, kSharedMaskRowsPerWave>
+      <<<plan.grid, dim3(kSharedMaskWaves * kWave), 0, stream>>>(
       x, mask, out, static_cast<uint32_t>(batch), static_cast<uint32_t>(Q), plan.gy, ms, mbs,
       scale);
 }
@@ -409,7 +410,7 @@ __global__ __launch_bounds__(256) void masked_softmax_rows_scalar(
   const float inv = 1.0f / sum;
   for (int64_t j = lane; j < K; j += kWave) {
     const float e = exp_shifted(score(j), m);
-    orow[j] = static_cast<uint16_t>(pack_bf16x2(e * inv, 0.f) & 0xffffu);
+    orow[j] = static_cast<uint16_t>(pack_bf16x2(div_rn(e, sum, inv), 0.f) & 0xffffu);
   }
 }
 
