@@ -26,11 +26,18 @@ roofline.flat_copy_us = a non-temporal flat copy (hipo_flat_copy) of the
                     config's read and write bytes in the same loop: the
                     ceiling of the access style; vs_flat_copy = flat_copy_us
                     / kernel_us
+configs[].pattern_copy_us = where a flat copy does not share the kernel's
+                    access pattern, the copy that does (config 4a: two
+                    streams in, two out), same loop; vs_pattern_copy =
+                    pattern_copy_us / steady_us
 cpu_baseline      = the eager repro (ATen) on the host CPU, os.cpu_count()
                     threads, warmup 1 + min of 5 (BASELINE.md's method); the
                     CPU oracle (oracle/hipo_ref.c) time rides along.
 configs           = every BASELINE config: the same steady-state loop and
-                    flat copy, plus oracle_harness.bench_oracle (graph-replay
+                    flat copy; the compiled repro (torch.compile, Inductor)
+                    in that same loop (compile_steady_us, steady_ratio =
+                    compile_steady_us / steady_us: the status ratio under
+                    sustained streaming); plus oracle_harness.bench_oracle (graph-replay
                     timing after a cache flush, the Inductor comparator, the
                     fp64 numerics gate) with the eager repro timed on the host
                     CPU beside it.
@@ -154,10 +161,12 @@ def cpu_baseline(rid, cpu_inputs, nbytes) -> dict:
 STEPS_PER_GRAPH = 64
 
 
-def steady_state(rid, steps, warmup, point=None):
+def steady_state(rid, steps, warmup, point=None, compiled=False):
     """Back-to-back steps over rotating input sets (see module docstring);
     `point` picks another shapes.json point of the dir (by shape hash) than
-    the BASELINE one."""
+    the BASELINE one.  compiled=True times torch.compile(Repro()) (Inductor,
+    coordinate-descent tuning as in bench_oracle's comparator) in the same
+    loop instead of the oracle."""
     import torch
     import oracle_harness as oh
     from repro_harness import load_shape_configs, make_inputs_from_config
@@ -180,9 +189,21 @@ def steady_state(rid, steps, warmup, point=None):
     tail_steps = steps % per_graph
     input_sets = [[t.to(dev) if isinstance(t, torch.Tensor) else t for t in cpu_inputs]
                   for _ in range(sets)]
-    impl, info = oh.resolve_oracle(fn, input_sets[0])
+    if compiled:
+        import importlib
+        icfg = importlib.import_module("torch._inductor.config")
+        icfg.coordinate_descent_tuning = True
+        importlib.import_module("torch._dynamo").reset()
+        module = torch.compile(instance)
+
+        def impl(inp):
+            with torch.no_grad():
+                return module(*inp)
+        info = None
+    else:
+        impl, info = oh.resolve_oracle(fn, input_sets[0])
     log(f"{rid}: {label}, {nbytes} algorithmic bytes/step, {sets} input sets, "
-        f"{per_graph} steps per graph")
+        f"{per_graph} steps per graph{' (torch.compile)' if compiled else ''}")
     in_ptrs = {t.data_ptr() for inp in input_sets for t in inp if isinstance(t, torch.Tensor)}
     out_bytes = 0
     for s in range(sets):
@@ -247,6 +268,7 @@ def steady_state(rid, steps, warmup, point=None):
     out = {
         "label": label, "nbytes": nbytes, "sets": sets, "steps_per_graph": per_graph,
         "dispatch": info and {"matched": info["matched"], "tuned_on": info["tuned_hardware"]},
+        "timed": "torch.compile(Repro())" if compiled else "oracle_forward",
         "ms_per_step": round(wall_s * 1e3, 4),
         "device_us_per_step": round(device_s * 1e6, 2),
         "value": round(nbytes / wall_s / 1e9, 1),
@@ -335,6 +357,54 @@ def flat_copy_steady(read_bytes: int, write_bytes: int, steps: int = 128) -> flo
     return round(us, 2)
 
 
+def _steady_callable(fn, sets, steps, label):
+    """Device us per call of fn(k) (k = the rotating buffer set), captured
+    in one hipGraph of back-to-back calls, events on the launch stream."""
+    import torch
+    import oracle_harness as oh
+    per_graph = sets * max(1, min(STEPS_PER_GRAPH, steps) // sets)
+    for k in range(sets):
+        fn(k)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for k in range(per_graph):
+            fn(k % sets)
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // per_graph)
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with oh._gpu_exclusive_lock(f"bench:{label}"):
+        ev0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / (reps * per_graph)
+    del g
+    return round(us, 2)
+
+
+def pattern_copy_steady(rid, cpu_inputs, steps: int = 128):
+    """The copy that shares a config's access pattern, where a flat copy does
+    not, in the steady-state loop: config 4a, a 2-in / 2-out copy of x and
+    residual's bytes (hipo_flat_copy2).  (name, us) or None."""
+    import torch
+    import hip_oracles
+    if rid == "var_mean_residual_layernorm":
+        n = cpu_inputs[0].numel()
+        sets = max(2, math.ceil((1 << 30) / (4 * 2 * n)))
+        bufs = [[torch.ones(n, dtype=torch.bfloat16, device="cuda") for _ in range(4)]
+                for _ in range(sets)]
+        us = _steady_callable(lambda k: hip_oracles.flat_copy2(*bufs[k]), sets, steps,
+                              "flat_copy2")
+        del bufs
+        torch.cuda.empty_cache()
+        return "2-in/2-out copy (hipo_flat_copy2)", us
+    return None
+
+
 def read_write_bytes(cpu_inputs, nbytes):
     """(read, write) split of the algorithmic bytes: every tensor input is
     read once, the rest is written."""
@@ -364,7 +434,15 @@ def per_config(want_cpu, steady_steps=64, compare_compile=True, coordinate_desce
         log(f"config {tag}: {rid}")
         ss, cpu_inputs = steady_state(rid, steady_steps, 8)
         rd, wr = read_write_bytes(cpu_inputs, ss["nbytes"])
+        pattern = pattern_copy_steady(rid, cpu_inputs)
         del cpu_inputs
+        compile_steady = None
+        if compare_compile:
+            try:
+                cs, _ = steady_state(rid, steady_steps, 8, compiled=True)
+                compile_steady = cs["device_us_per_step"]
+            except Exception as e:  # Inductor unavailable: the oracle is still timed
+                log(f"config {tag}: compiled steady loop failed: {type(e).__name__}: {e}")
         flat_us = flat_copy_steady(rd, wr)
         memcopy_us = memcopy_sol_steady(ss["nbytes"])
         _, fn, d = oh._load_oracle_module(CANONICAL / rid)
@@ -385,9 +463,15 @@ def per_config(want_cpu, steady_steps=64, compare_compile=True, coordinate_desce
                  "bytes": r.get("bytes"), "read_bytes": rd, "write_bytes": wr,
                  "steady_us": ss["device_us_per_step"], "steady_gbps": ss["achieved"],
                  "steady_sol_frac": round(ss["achieved"] / PEAK_GBPS, 4),
+                 "compile_steady_us": compile_steady,
+                 "steady_ratio": (round(compile_steady / ss["device_us_per_step"], 4)
+                                  if compile_steady else None),
                  "flat_copy_us": flat_us,
                  "vs_flat_copy": round(flat_us / ss["device_us_per_step"], 4),
                  "memcopy_sol_us": memcopy_us,
+                 **({"pattern_copy": pattern[0], "pattern_copy_us": pattern[1],
+                     "vs_pattern_copy": round(pattern[1] / ss["device_us_per_step"], 4)}
+                    if pattern else {}),
                  "steady_vs_memcopy_sol": round(memcopy_us / ss["device_us_per_step"], 4),
                  "traffic": pmc_traffic(rid),
                  "oracle_us": r.get("oracle_us"), "compile_us": r.get("compile_us"),

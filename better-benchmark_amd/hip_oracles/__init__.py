@@ -22,7 +22,7 @@ import torch  # imported before the .so so the process has one HIP runtime
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libhip_oracles.so"
 HEADER_PATH = PKG_DIR.parents[1] / "include" / "hip_oracles.h"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _c_i64 = ctypes.c_int64
 _c_ptr = ctypes.c_void_p
@@ -68,6 +68,7 @@ _SIGNATURES = {
         [_c_ptr] * 8 + [_c_i64, _c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int,
                         _c_ptr, ctypes.c_size_t, _c_ptr]),
     "hipo_flat_copy": (ctypes.c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
+    "hipo_flat_copy2": (ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "hipo_gelu_tanh_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "hipo_gelu_tanh_f32": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "hipo_transpose_last2": (
@@ -639,6 +640,22 @@ def flat_copy(src: torch.Tensor, dst: torch.Tensor, read_bytes: int | None = Non
         _check(lib.hipo_flat_copy(_ptr(src), rb, _ptr(dst), wb, _stream(dev)), "flat_copy")
 
 
+def flat_copy2(src0: torch.Tensor, src1: torch.Tensor, dst0: torch.Tensor,
+               dst1: torch.Tensor) -> None:
+    """Measurement yardstick: copy src0 -> dst0 and src1 -> dst1 in one
+    launch, four streams in lockstep (the residual LayerNorm's pattern).  All
+    four buffers contiguous, the same size, a multiple of 1024 bytes."""
+    lib = load_library()
+    dev = _require_rocm(src0, src1, dst0, dst1)
+    nb = src0.numel() * src0.element_size()
+    for t in (src0, src1, dst0, dst1):
+        _require(t.is_contiguous() and t.numel() * t.element_size() == nb,
+                 "flat_copy2: four contiguous buffers of one size")
+    with torch.cuda.device(dev):
+        _check(lib.hipo_flat_copy2(_ptr(src0), _ptr(src1), _ptr(dst0), _ptr(dst1), nb,
+                                   _stream(dev)), "flat_copy2")
+
+
 _BN_ACTS = {None: 0, "none": 0, "relu": 1, "silu": 2}
 
 
@@ -768,5 +785,6 @@ __all__ = [
     "batchnorm_workspace_bytes", "batchnorm_train",
     "batchnorm_cached_workspace", "batchnorm_error_flag", "BN_ERROR_WORD_OFFSET",
     "HipOraclesDeviceFault", "device_faults", "raise_on_device_faults", "flat_copy",
+    "flat_copy2",
     "gelu_erf_bwd_colsum", "cast_storage", "bn_infer_act",
 ]

@@ -12,6 +12,10 @@
 // exists a constant is written.
 //
 // HBM-bound: algorithmic bytes = read_bytes + write_bytes.
+//
+// hipo_flat_copy2: the same for two input and two output streams moved
+// chunk by chunk in lockstep (the residual LayerNorm's x, residual -> h, y),
+// a pattern a one-stream copy does not share.
 #include "hipo_common.h"
 
 namespace hipo {
@@ -36,6 +40,20 @@ __global__ __launch_bounds__(kCopyWaves * kWave) void flat_copy_chunks(
   }
 }
 
+// Two streams in, two out: wave chunk i moves 1 KiB of src0 to dst0 and 1
+// KiB of src1 to dst1, all four accesses of a lane issued together.
+__global__ __launch_bounds__(kCopyWaves * kWave) void flat_copy2_chunks(
+    const u32x4_t* __restrict__ src0, const u32x4_t* __restrict__ src1,
+    u32x4_t* __restrict__ dst0, u32x4_t* __restrict__ dst1, uint64_t chunks) {
+  const uint64_t chunk = static_cast<uint64_t>(blockIdx.x) * kCopyWaves + (threadIdx.x >> 6);
+  if (chunk >= chunks) return;
+  const uint64_t idx = chunk * kWave + (threadIdx.x & (kWave - 1));
+  const u32x4_t a = __builtin_nontemporal_load(src0 + idx);
+  const u32x4_t b = __builtin_nontemporal_load(src1 + idx);
+  __builtin_nontemporal_store(a, dst0 + idx);
+  __builtin_nontemporal_store(b, dst1 + idx);
+}
+
 }  // namespace
 }  // namespace hipo
 
@@ -58,4 +76,23 @@ extern "C" int hipo_flat_copy(const void* src, int64_t read_bytes, void* dst,
                      stream>>>(static_cast<const u32x4_t*>(src), static_cast<u32x4_t*>(dst),
                                rc, wc);
   return check_launch("flat_copy");
+}
+
+extern "C" int hipo_flat_copy2(const void* src0, const void* src1, void* dst0, void* dst1,
+                               int64_t bytes, hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  HIPO_REQUIRE(bytes >= kChunk && bytes % kChunk == 0,
+               "flat_copy2: bytes must be a positive multiple of %d", kChunk);
+  HIPO_REQUIRE(src0 && src1 && dst0 && dst1, "flat_copy2: null pointer");
+  HIPO_REQUIRE(aligned16(src0) && aligned16(src1) && aligned16(dst0) && aligned16(dst1),
+               "flat_copy2: pointers must be 16-byte aligned");
+  const uint64_t chunks = static_cast<uint64_t>(bytes) / kChunk;
+  const uint64_t blocks = (chunks + kCopyWaves - 1) / kCopyWaves;
+  HIPO_REQUIRE(blocks < (uint64_t{1} << 31), "flat_copy2: too large");
+  flat_copy2_chunks<<<dim3(static_cast<unsigned>(blocks)), dim3(kCopyWaves * kWave), 0,
+                      stream>>>(static_cast<const u32x4_t*>(src0),
+                                static_cast<const u32x4_t*>(src1), static_cast<u32x4_t*>(dst0),
+                                static_cast<u32x4_t*>(dst1), chunks);
+  return check_launch("flat_copy2");
 }

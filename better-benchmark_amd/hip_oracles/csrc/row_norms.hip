@@ -287,24 +287,27 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_scalar(
   if (rstd_out != nullptr && lane == 0) rstd_out[row] = rstd;
 }
 
-// Rows of exactly KC columns (4096, the config): 256-thread workgroups of
-// NR = 2 row slots, W = 2 waves per row (4 groups of 16 bytes per lane and
+// Rows of exactly KC columns (4096, the config): NR row slots per
+// workgroup, W waves per row (KC / (8 W 64) groups of 16 bytes per lane and
 // stream), RPW rows per slot (rows b * NR * RPW + rr + NR * j, j < RPW),
-// their loads issued together; gamma and beta staged once per workgroup in
-// LDS, row index from the block index without division.  Same arithmetic as
-// residual_layernorm_rows (per-wave two-pass statistics of the bf16 h,
-// closed-form merge of the W triples in wave order).
-template <int KC, int RPW>
-__global__ __launch_bounds__(256) void residual_layernorm_k(
+// their loads issued together; row index from the block index without
+// division.  gamma and beta: STAGE = staged once per workgroup in LDS (the
+// barrier publishes them), else each lane loads its own groups from the
+// cache with the row.  Same arithmetic as residual_layernorm_rows
+// (per-wave two-pass statistics of the bf16 h, closed-form merge of the W
+// triples in wave order).
+template <int KC, int W, int NR, int RPW, bool STAGE>
+__global__ __launch_bounds__(W * NR * 64) void residual_layernorm_k(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
     const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
     uint16_t* __restrict__ h, uint16_t* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out, int64_t rows, float eps) {
-  constexpr int W = 2, NR = 2, G = KC / kRowGroup;
+  constexpr int kThreads = W * NR * kWave;
+  constexpr int G = KC / kRowGroup;
   constexpr int U = G / (W * kWave);
-  static_assert(U * W * kWave == G && W * NR * kWave == 256, "row shape");
-  __shared__ __align__(16) u32x4_t gs[G];
-  __shared__ __align__(16) u32x4_t bs[G];
+  static_assert(U * W * kWave == G, "row shape");
+  __shared__ __align__(16) u32x4_t gs[STAGE ? G : 1];
+  __shared__ __align__(16) u32x4_t bs[STAGE ? G : 1];
   __shared__ Welford part[RPW][W * NR];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
@@ -327,9 +330,19 @@ __global__ __launch_bounds__(256) void residual_layernorm_k(
           __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(res + base[j] + col));
     }
   }
-  for (int i = threadIdx.x; i < G; i += 256) {
-    gs[i] = *reinterpret_cast<const u32x4_t*>(gamma + i * kRowGroup);
-    bs[i] = *reinterpret_cast<const u32x4_t*>(beta + i * kRowGroup);
+  u32x4_t gl[STAGE ? 1 : U], bl[STAGE ? 1 : U];
+  if constexpr (STAGE) {
+    for (int i = threadIdx.x; i < G; i += kThreads) {
+      gs[i] = *reinterpret_cast<const u32x4_t*>(gamma + i * kRowGroup);
+      bs[i] = *reinterpret_cast<const u32x4_t*>(beta + i * kRowGroup);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int g = (u * W + w) * kWave + lane;
+      gl[u] = *reinterpret_cast<const u32x4_t*>(gamma + g * kRowGroup);
+      bl[u] = *reinterpret_cast<const u32x4_t*>(beta + g * kRowGroup);
+    }
   }
 
 #pragma unroll
@@ -383,8 +396,8 @@ __global__ __launch_bounds__(256) void residual_layernorm_k(
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int g = (u * W + w) * kWave + lane;
-      const u32x4_t gv = gs[g];
-      const u32x4_t bv = bs[g];
+      const u32x4_t gv = STAGE ? gs[g] : gl[STAGE ? 0 : u];
+      const u32x4_t bv = STAGE ? bs[g] : bl[STAGE ? 0 : u];
       u32x4_t o;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
@@ -550,11 +563,14 @@ void launch_seg_plan(const SegPlan& sp, int64_t rows, hipStream_t stream, const 
 #undef HIPO_SEG
 }
 
-// Rows per slot of residual_layernorm_k.  Measured at [16384, 4096], one
-// process: 1 row 90.2-90.8 us, 2 rows 93.4 us, 4 rows 100.6-102.8 us (each
-// wave already keeps 8 KiB in flight per row; the masked softmax, at 1 KiB
-// per row, gains from more).
+// Shape of residual_layernorm_k at 4096 columns: waves per row, row slots
+// per workgroup, rows per slot, gamma / beta staged in LDS.  Rows per slot,
+// measured at [16384, 4096], one process: 1 row 90.2-90.8 us, 2 rows 93.4
+// us, 4 rows 100.6-102.8 us.
+constexpr int kLnWaves = 2;
+constexpr int kLnSlots = 2;
 constexpr int kLayerNormRowsPerWave = 1;
+constexpr bool kLnStage = true;
 
 }  // namespace
 }  // namespace hipo
@@ -575,11 +591,12 @@ extern "C" int hipo_residual_layernorm_bf16(
   const bool vec = cols % 8 == 0 && row_plan(cols, plan) && aligned16(x) &&
                    aligned16(residual) && aligned16(gamma) && aligned16(beta) &&
                    (h == nullptr || aligned16(h)) && aligned16(y);
-  constexpr int kRowsPerBlock = 2 * kLayerNormRowsPerWave;
+  constexpr int kRowsPerBlock = kLnSlots * kLayerNormRowsPerWave;
   if (vec && cols == 4096 && (rows + kRowsPerBlock - 1) / kRowsPerBlock <= 0x7fffffff) {
-    residual_layernorm_k<4096, kLayerNormRowsPerWave>
-        <<<dim3(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock)), dim3(256), 0,
-           stream>>>(x, residual, gamma, beta, h, y, mean, rstd, rows, eps);
+    residual_layernorm_k<4096, kLnWaves, kLnSlots, kLayerNormRowsPerWave, kLnStage>
+        <<<dim3(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
+           dim3(kLnWaves * kLnSlots * kWave), 0, stream>>>(x, residual, gamma, beta, h, y, mean,
+                                                           rstd, rows, eps);
   } else if (const SegPlan sp = vec ? seg_plan(rows, cols) : SegPlan{};
              sp.lanes > 0 && (rows + 256 / sp.lanes - 1) / (256 / sp.lanes) <= 0x7fffffff) {
     launch_seg_plan(sp, rows, stream, x, residual, gamma, beta, h, y, mean, rstd,

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define HIPO_ABI_VERSION 2
+#define HIPO_ABI_VERSION 3
 #define HIPO_EINVAL 1000
 
 /* ABI version of the loaded library (HIPO_ABI_VERSION at build time). */
@@ -324,6 +324,19 @@ int hipo_batchnorm_train_fwd_f32_noalloc(const float* x, const float* gamma,
  */
 int hipo_flat_copy(const void* src, int64_t read_bytes, void* dst,
                    int64_t write_bytes, hipStream_t stream);
+
+/*
+ * Yardstick for two-input, two-output streaming kernels (the residual
+ * LayerNorm: x, residual -> h, y): copies bytes of src0 to dst0 and of src1
+ * to dst1 in one launch, each wave moving one 1 KiB chunk of all four
+ * buffers with 16-byte non-temporal accesses.  bytes: a positive multiple
+ * of 1024; pointers 16-byte aligned.  No counterpart in the reference (its
+ * memcopy SOL is one stream each way, repro_harness.py:952-958); used only
+ * to price a kernel's access pattern.
+ */
+int hipo_flat_copy2(const void* src0, const void* src1, void* dst0, void* dst1,
+                    int64_t bytes, hipStream_t stream);
+
 
 /*
  * GELU(tanh) of a contiguous tensor of n elements, element by element:

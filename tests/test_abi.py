@@ -33,7 +33,7 @@ def test_exported_names_match_header():
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.hipo_abi_version() == hip_oracles.ABI_VERSION == 2
+    assert lib.hipo_abi_version() == hip_oracles.ABI_VERSION == 3
     assert lib.hipo_last_error() == b""
 
 
@@ -151,6 +151,23 @@ def test_bf16_batchnorm_workspace_bytes(lib):
     assert lib.hipo_batchnorm_nchw_mean_workspace_bytes(128, 1024, 49) == 32 * 1024 * 8
     assert lib.hipo_batchnorm_nchw_mean_workspace_bytes(5, 8, 9) == 2 * 8 * 8
     assert lib.hipo_batchnorm_nchw_mean_workspace_bytes(5, 8, 0) == 0
+
+
+def test_yardstick_argument_checks(lib):
+    """The two-stream yardstick rejects bad arguments on the host, before
+    any device call: sizes that are not positive multiples of 1 KiB, null or
+    misaligned pointers."""
+    import ctypes
+    buf = ctypes.create_string_buffer(4096 + 16)
+    base = (ctypes.addressof(buf) + 15) // 16 * 16
+    p = ctypes.c_void_p(base)
+    assert lib.hipo_flat_copy2(p, p, p, p, 1000, None) != 0
+    assert "multiple of 1024" in lib.hipo_last_error().decode()
+    assert lib.hipo_flat_copy2(p, None, p, p, 1024, None) != 0
+    assert "null" in lib.hipo_last_error().decode()
+    q = ctypes.c_void_p(base + 4)
+    assert lib.hipo_flat_copy2(p, q, p, p, 1024, None) != 0
+    assert "aligned" in lib.hipo_last_error().decode()
 
 
 def test_gelu_bwd_workspace_bytes(lib):

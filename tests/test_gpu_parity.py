@@ -1826,3 +1826,22 @@ def test_bn_infer_largest_points(rid, rocm_device):
     del dev_in
     (want,) = _family_oracle(rid, cpu_in)
     _same_bits(got[0], want, f"{rid}/{label}")
+
+
+def test_yardstick_copies_are_copies(rocm_device):
+    """The measurement yardsticks move the data they claim to: hipo_flat_copy
+    (equal sizes) and hipo_flat_copy2 (two streams each way) are bit-exact
+    copies."""
+    import hip_oracles
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(1 << 18, generator=g).to(rocm_device)
+    b = torch.empty_like(a)
+    hip_oracles.flat_copy(a, b)
+    assert torch.equal(a, b)
+    srcs = [torch.randint(-32768, 32767, (1 << 19,), generator=g, dtype=torch.int16).view(
+        torch.bfloat16).to(rocm_device) for _ in range(2)]
+    dsts = [torch.empty_like(t) for t in srcs]
+    hip_oracles.flat_copy2(srcs[0], srcs[1], dsts[0], dsts[1])
+    torch.cuda.synchronize()
+    for s_, d_ in zip(srcs, dsts):
+        assert torch.equal(s_.view(torch.int16), d_.view(torch.int16))
