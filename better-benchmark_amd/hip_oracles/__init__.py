@@ -67,6 +67,8 @@ _SIGNATURES = {
         ctypes.c_int,
         [_c_ptr] * 8 + [_c_i64, _c_i64, _c_i64, _c_f32, _c_f32, ctypes.c_int,
                         _c_ptr, ctypes.c_size_t, _c_ptr]),
+    "hipo_batchnorm_noalloc_error": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_uint32),
+                                                    ctypes.c_int]),
     "hipo_flat_copy": (ctypes.c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
     "hipo_flat_copy2": (ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "hipo_gelu_tanh_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
@@ -74,10 +76,6 @@ _SIGNATURES = {
     "hipo_transpose_last2": (
         ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_ptr]),
     "hipo_row_mean_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, ctypes.c_int, _c_ptr]),
-    "hipo_cast_bf16_to_f32": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
-    "hipo_cast_f32_to_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
-    "hipo_bn_infer_act_bf16": (ctypes.c_int, [_c_ptr] * 12 + [_c_i64, _c_i64, _c_i64, ctypes.c_int,
-                                                          ctypes.c_float, ctypes.c_int, _c_ptr]),
     "hipo_gelu_erf_bwd_colsum_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64]),
     "hipo_gelu_erf_bwd_colsum_bf16": (
         ctypes.c_int, [_c_ptr] * 4 + [_c_i64, _c_i64, _c_ptr, ctypes.c_size_t, _c_ptr]),
@@ -241,93 +239,6 @@ def row_mean_bf16(x: torch.Tensor, *, relu: bool = False) -> torch.Tensor:
         _check(lib.hipo_row_mean_bf16(_ptr(x), _ptr(out), rows, cols, 1 if relu else 0,
                                       _stream(dev)), "row_mean_bf16")
     return out
-
-
-def _dense_layout(t: torch.Tensor) -> bool:
-    """True if t's strides lay its elements out densely and without overlap
-    (contiguous, channels-last, or any permutation of dims): its storage
-    span is exactly numel elements."""
-    dims = sorted((st, sz) for st, sz in zip(t.stride(), t.shape) if sz != 1)
-    expect = 1
-    for st, sz in dims:
-        if st != expect:
-            return False
-        expect *= sz
-    return True
-
-
-def cast_storage(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    """x cast between bf16 and fp32 in storage order: the result has x's
-    shape and strides (eager's preserve-format convert_element_type) and
-    element i of x's storage becomes element i of the result's.  bf16 ->
-    fp32 is exact; fp32 -> bf16 rounds to nearest, ties to even."""
-    lib = load_library()
-    dev = _require_rocm(x)
-    pairs = {(torch.bfloat16, torch.float32): lib.hipo_cast_bf16_to_f32,
-             (torch.float32, torch.bfloat16): lib.hipo_cast_f32_to_bf16}
-    _require((x.dtype, dtype) in pairs, "cast_storage: bf16 <-> fp32 only")
-    _require(_dense_layout(x), "cast_storage: x must be dense (no gaps or overlap)")
-    y = torch.empty_strided(tuple(x.shape), tuple(x.stride()), dtype=dtype, device=dev)
-    with torch.cuda.device(dev):
-        _check(pairs[(x.dtype, dtype)](_ptr(x), _ptr(y), x.numel(), _stream(dev)),
-               "cast_storage")
-    return y
-
-
-BN_ACTS = {"none": 0, "relu": 1, "relu6": 2}
-
-
-def _nchw_layout(t: torch.Tensor):
-    """0 for contiguous NCHW, 1 for channels-last, None otherwise."""
-    if t.is_contiguous():
-        return 0
-    if t.is_contiguous(memory_format=torch.channels_last):
-        return 1
-    return None
-
-
-def bn_infer_act(x: torch.Tensor, mean: torch.Tensor, var: torch.Tensor, weight: torch.Tensor,
-                 bias: torch.Tensor, *, eps: float, act: str = "none",
-                 residual: torch.Tensor = None, second=None) -> torch.Tensor:
-    """BatchNorm inference affine of a bf16 [N, C, H, W] tensor (contiguous or
-    channels-last), its epilogue and the graph's bf16 rounding points:
-    t = bf16(((x - mean) * inv) * weight + bias), inv = 1 / sqrt(var + eps)
-    per channel in fp32 and the four element ops in fp64 (as the graph's
-    fp64 evaluation makes them); second = (x2, mean2, var2, weight2, bias2) adds the same
-    affine of x2, rounded to bf16; residual adds a bf16 tensor, rounded to
-    bf16; then act "none", "relu" or "relu6".  The parameters are bf16 [C];
-    x2, residual and the result share x's strides."""
-    lib = load_library()
-    extra = [t for t in ((residual,) if residual is not None else ()) + tuple(second or ())]
-    dev = _require_rocm(x, mean, var, weight, bias, *extra)
-    _require(act in BN_ACTS, f"bn_infer_act: act must be one of {sorted(BN_ACTS)}")
-    _require(x.dim() == 4, "bn_infer_act: x must be [N, C, H, W]")
-    n, c, h, w = x.shape
-    layout = _nchw_layout(x)
-    _require(layout is not None, "bn_infer_act: x must be contiguous or channels-last")
-    params = [mean, var, weight, bias]
-    x2 = None
-    if second is not None:
-        _require(len(second) == 5, "bn_infer_act: second = (x2, mean2, var2, weight2, bias2)")
-        x2 = second[0]
-        params += list(second[1:])
-    for t in params:
-        _require(t.dtype == torch.bfloat16 and t.shape == (c,) and t.is_contiguous(),
-                 "bn_infer_act: parameters must be contiguous bf16 [C]")
-    for t in [x] + [u for u in (x2, residual) if u is not None]:
-        _require(t.dtype == torch.bfloat16 and t.shape == x.shape and t.stride() == x.stride(),
-                 "bn_infer_act: x, x2 and residual must be bf16 of one shape and strides")
-    y = torch.empty_strided(tuple(x.shape), tuple(x.stride()), dtype=torch.bfloat16, device=dev)
-    if y.numel() == 0:
-        return y
-    p2 = [_ptr(t) for t in second[1:]] if second is not None else [0, 0, 0, 0]
-    with torch.cuda.device(dev):
-        _check(lib.hipo_bn_infer_act_bf16(
-            _ptr(x), _ptr(mean), _ptr(var), _ptr(weight), _ptr(bias),
-            _ptr(x2) if x2 is not None else 0, *p2,
-            _ptr(residual) if residual is not None else 0, _ptr(y),
-            n, c, h * w, layout, float(eps), BN_ACTS[act], _stream(dev)), "bn_infer_act")
-    return y
 
 
 def gelu_erf_bwd_colsum(grad: torch.Tensor, x: torch.Tensor):
@@ -754,8 +665,9 @@ def batchnorm_error_flag(dev: torch.device | None = None, *,
 def device_faults(dev: torch.device | None = None, *, clear: bool = True) -> list[str]:
     """Faults recorded by kernels in every BatchNorm workspace this process has
     used on `dev` (all devices if None): the shared, retired and caller-provided
-    ones.  With `clear`, each reported word is reset to zero on the current
-    stream, so the next check sees only new faults.  Synchronises."""
+    ones, and the allocation-free entry point's static scratch array.  With
+    `clear`, each reported word is reset to zero, so the next check sees only
+    new faults.  Synchronises."""
     out = []
     for ws in _known_workspaces(dev):
         word = _error_word(ws)
@@ -766,6 +678,17 @@ def device_faults(dev: torch.device | None = None, *, clear: bool = True) -> lis
                        f"its outputs and running statistics are NaN")
             if clear:
                 word.zero_()
+    # The allocation-free entry point's static scratch array, per device.
+    lib = load_library()
+    devices = [dev.index] if dev is not None else range(torch.cuda.device_count())
+    for d in devices:
+        w = ctypes.c_uint32(0)
+        _check(lib.hipo_batchnorm_noalloc_error(int(d), ctypes.byref(w), 1 if clear else 0),
+               "batchnorm_noalloc_error")
+        if w.value:
+            out.append(f"batchnorm_train_fwd_f32_noalloc: exchange wait timed out "
+                       f"(error word {w.value:#x} in the static scratch array of cuda:{d}); "
+                       f"its outputs and running statistics are NaN")
     return out
 
 
@@ -786,5 +709,5 @@ __all__ = [
     "batchnorm_cached_workspace", "batchnorm_error_flag", "BN_ERROR_WORD_OFFSET",
     "HipOraclesDeviceFault", "device_faults", "raise_on_device_faults", "flat_copy",
     "flat_copy2",
-    "gelu_erf_bwd_colsum", "cast_storage", "bn_infer_act",
+    "gelu_erf_bwd_colsum",
 ]

@@ -40,8 +40,6 @@ SOURCES = [
     "gelu_flat.hip",
     "transpose.hip",
     "gelu_bwd.hip",
-    "cast.hip",
-    "bn_infer.hip",
 ]
 
 # Packed-FP32 VALU forms are disabled for all device code (the compiler

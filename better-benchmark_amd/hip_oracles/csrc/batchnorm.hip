@@ -473,10 +473,12 @@ extern "C" int hipo_batchnorm_train_fwd_f32(
 // that memory: its device address is looked up once per device
 // (hipGetSymbolAddress, with that device current) and only that address is
 // passed to kernels.  The first call on a device also clears the array with
-// a fill kernel on the caller's stream, ordered before the call's own
-// kernels: the single-pass kernel's control words (completion count, epoch)
-// must start at zero and its exchange slots must carry no tag of a future
-// epoch.  After that, the epoch protocol keeps the array consistent from one
+// a fill kernel on the caller's stream and waits for it (that first call
+// synchronises; later ones do not): the single-pass kernel's control words
+// (completion count, epoch) must start at zero and its exchange slots must
+// carry no tag of a future epoch.  hipo_batchnorm_noalloc_error reads (and
+// clears) the array's sticky error word, the one fault signal of this path
+// besides the NaN outputs.  After that, the epoch protocol keeps the array consistent from one
 // call to the next, for any shape that fits; calls that overlap on one
 // device (two streams) race on it.
 // ---------------------------------------------------------------------------
@@ -523,6 +525,15 @@ void* scratch_for_current_device(hipStream_t stream) {
   const uint32_t n16 = static_cast<uint32_t>(kBnScratchBytes / 16);
   bn_scratch_clear<<<dim3(256), dim3(256), 0, stream>>>(static_cast<u32x4_t*>(ptr), n16);
   if (check_launch("batchnorm (no-alloc) scratch clear") != 0) return nullptr;
+  // The clear completes before the address is published: a first call on
+  // another stream that finds the pointer cannot start while the control
+  // words are still being zeroed.
+  const hipError_t se = hipStreamSynchronize(stream);
+  if (se != hipSuccess) {
+    (void)hipGetLastError();
+    set_error("batchnorm (no-alloc): scratch clear failed: %s", hipGetErrorString(se));
+    return nullptr;
+  }
   g_scratch_ptr[dev] = ptr;
   return ptr;
 }
@@ -548,4 +559,37 @@ extern "C" int hipo_batchnorm_train_fwd_f32_noalloc(
   return hipo_batchnorm_train_fwd_f32(x, gamma, beta, running_mean, running_var, y,
                                       save_mean, save_invstd, n, c, hw, momentum, eps,
                                       relu, ws, kBnScratchBytes, stream);
+}
+
+extern "C" int hipo_batchnorm_noalloc_error(int device, uint32_t* word, int clear) {
+  using namespace hipo;
+  clear_error();
+  HIPO_REQUIRE(word != nullptr, "batchnorm_noalloc_error: null word pointer");
+  *word = 0;
+  HIPO_REQUIRE(device >= 0 && device < kScratchDevices,
+               "batchnorm_noalloc_error: device %d out of range", device);
+  void* ptr = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[device];
+  }
+  if (ptr == nullptr) return 0;  // the entry point never ran on this device
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) cur = -1;
+  hipError_t e = hipSetDevice(device);
+  unsigned char* err = static_cast<unsigned char*>(ptr) + kBnErrorWordOffset;
+  // Every kernel that may set the word has finished before it is read.
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(word, err, sizeof(uint32_t), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && clear && *word != 0) {
+    const uint32_t zero = 0;
+    e = hipMemcpy(err, &zero, sizeof(uint32_t), hipMemcpyHostToDevice);
+  }
+  if (cur >= 0) (void)hipSetDevice(cur);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    set_error("batchnorm_noalloc_error: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  return 0;
 }

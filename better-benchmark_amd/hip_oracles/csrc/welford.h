@@ -56,6 +56,7 @@ __device__ __forceinline__ Welford wave_welford(Welford w) {
 //   [16, 16 + fused_slot_bytes)  its exchange slots
 //   [.., + split_bytes)          Welford partials of the split-K path
 constexpr size_t kBnCtlBytes = 16;
+constexpr size_t kBnErrorWordOffset = 8;  // ctl[2]: sticky error word of the single-pass path
 int64_t bn_fused_groups(int64_t n, int64_t hw);   // workgroups per channel
 size_t bn_fused_slot_bytes(int64_t n, int64_t c, int64_t hw);
 

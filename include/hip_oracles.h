@@ -311,6 +311,18 @@ int hipo_batchnorm_train_fwd_f32_noalloc(const float* x, const float* gamma,
                                          hipStream_t stream);
 
 /*
+ * The sticky error word of the allocation-free path's static scratch array
+ * on `device`: nonzero once an exchange wait of the single-pass kernel
+ * timed out there (that call's outputs and running statistics are then
+ * NaN).  *word = 0 if hipo_batchnorm_train_fwd_f32_noalloc never ran on the
+ * device.  Waits for the device's work to finish (a host query, not a launch:
+ * never call it under stream capture); with `clear`, a nonzero word is reset
+ * to zero.  No counterpart in the reference: the fault channel of the
+ * allocation-free entry point, whose workspace the caller cannot inspect.
+ */
+int hipo_batchnorm_noalloc_error(int device, uint32_t* word, int clear);
+
+/*
  * Flat stream copy (a measurement yardstick, not an oracle): reads
  * read_bytes from src and writes write_bytes to dst in one launch with the
  * oracle kernels' access style (16-byte non-temporal accesses, 1 KiB per
@@ -402,52 +414,6 @@ int hipo_gelu_erf_bwd_colsum_bf16(const uint16_t* grad, const uint16_t* x, uint1
                                   float* colsum, int64_t rows, int64_t cols,
                                   void* workspace, size_t workspace_bytes,
                                   hipStream_t stream);
-
-/*
- * Storage-order casts between bf16 and fp32 over n elements:
- *   bf16 -> fp32 exact;  fp32 -> bf16 rounded to nearest, ties to even
- *   (NaN stays NaN).
- * Element i of x's storage becomes element i of y's, so a dense tensor of
- * any layout (contiguous, channels-last, ...) is cast by passing its data
- * pointer and numel, with y allocated with the same strides.  Any
- * alignment (16-byte aligned pointers take the vector path).
- * Replaces the Triton bodies of oracle_forward in
- * repros/canonical/pointwise_04d85912d998/oracle.py:18-34 (bf16 -> fp32),
- * repros/canonical/pointwise_ccd411f2a45d/oracle.py:23-39 (fp32 -> bf16) and
- * repros/canonical/pointwise_8bb40810003c/oracle.py:102-119 (fp32 -> bf16,
- * the two returned views taken in Python).
- */
-int hipo_cast_bf16_to_f32(const uint16_t* x, float* y, int64_t n, hipStream_t stream);
-int hipo_cast_f32_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t stream);
-
-/* BatchNorm inference affine with its epilogue, bf16 in and out, in the
- * graph's op order with no contraction:
- *   t = bf16(((x - mean[c]) * inv[c]) * weight[c] + bias[c]), the four ops in
- *   fp64 and the result cast through fp32 (as the graph's fp64 evaluation,
- *   the numerics anchor), inv[c] = 1 / sqrt(var[c] + eps) in fp32
- * then, when x2 is non-null, t = bf16(t + t2) with t2 the same affine of x2
- * under (mean2, var2, weight2, bias2); when residual is non-null,
- * t = bf16(t + residual); then act 0 (none), 1 (ReLU) or 2 (ReLU6 = clamp
- * to [0, 6]); NaN stays NaN.  x, x2, residual and y are dense [n, c, hw]
- * tensors of one layout: contiguous NCHW (channels_last = 0) or
- * channels-last (1; element (n, c, p) stored at (n * hw + p) * c + c).
- * The per-channel parameters are bf16 [c], c <= 4096, n * c * hw < 2^31.
- * Any alignment (16-byte aligned tensors take the vector paths).
- * Replaces the Triton bodies of oracle_forward in
- * repros/canonical/pointwise_7899d74e0838/oracle.py:241-293 (ReLU, eps 1e-3),
- * repros/canonical/pointwise_818c3aa59952/oracle.py:106-138 (none),
- * repros/canonical/pointwise_e6ddc8e897ec/oracle.py:142-174 (residual),
- * repros/canonical/pointwise_9595e73ff43b/oracle.py:107-127 (ReLU6),
- * repros/canonical/pointwise_81485f33f5b9/oracle.py:156-202 (residual +
- * ReLU) and repros/canonical/pointwise_2c331ef4f17f/oracle.py:305-306 (two
- * affines + ReLU).
- */
-int hipo_bn_infer_act_bf16(const uint16_t* x, const uint16_t* mean, const uint16_t* var,
-                           const uint16_t* weight, const uint16_t* bias, const uint16_t* x2,
-                           const uint16_t* mean2, const uint16_t* var2, const uint16_t* weight2,
-                           const uint16_t* bias2, const uint16_t* residual, uint16_t* y,
-                           int64_t n, int64_t c, int64_t hw, int channels_last, float eps,
-                           int act, hipStream_t stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

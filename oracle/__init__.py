@@ -51,9 +51,6 @@ _SIGS = {
     "ref_row_mean_bf16": (None, [_p, _p, _i64, _i64, _i, _i]),
     "ref_gelu_erf_grad_f32": (None, [_p, _p, _i64, _i]),
     "ref_gelu_erf_bwd_colsum_bf16": (None, [_p] * 4 + [_i64, _i64, _i]),
-    "ref_cast_bf16_to_f32": (None, [_p, _p, _i64, _i]),
-    "ref_cast_f32_to_bf16": (None, [_p, _p, _i64, _i]),
-    "ref_bn_infer_act_bf16": (None, [_p] * 12 + [_i64, _i64, _i64, _i, ctypes.c_float, _i, _i]),
 }
 
 _ACTS = {None: 0, "none": 0, "relu": 1, "silu": 2}
@@ -303,54 +300,3 @@ def gelu_erf_bwd_colsum(grad, x, threads=None):
     load().ref_gelu_erf_bwd_colsum_bf16(grad.data_ptr(), x.data_ptr(), y.data_ptr(),
                                         colsum.data_ptr(), rows, cols, _th(threads))
     return y, colsum
-
-
-def cast_storage(x, dtype, threads=None):
-    """x cast bf16 <-> fp32 element by element in storage order, keeping
-    x's shape and strides: bf16 -> fp32 exact, fp32 -> bf16 to nearest
-    even."""
-    pairs = {(torch.bfloat16, torch.float32): "ref_cast_bf16_to_f32",
-             (torch.float32, torch.bfloat16): "ref_cast_f32_to_bf16"}
-    assert (x.dtype, dtype) in pairs, (x.dtype, dtype)
-    x = x.detach().to("cpu")
-    y = torch.empty_strided(tuple(x.shape), tuple(x.stride()), dtype=dtype)
-    getattr(load(), pairs[(x.dtype, dtype)])(x.data_ptr(), y.data_ptr(), x.numel(),
-                                             _th(threads))
-    return y
-
-
-BN_ACTS = {"none": 0, "relu": 1, "relu6": 2}
-
-
-def bn_infer_act(x, mean, var, weight, bias, *, eps, act="none", residual=None, second=None,
-                 threads=None):
-    """BatchNorm inference affine + epilogue of a bf16 [N, C, H, W] tensor
-    (contiguous or channels-last): bf16(((x - mean) * inv) * weight + bias)
-    with inv = 1 / sqrt(var + eps) in fp32 and the four ops in fp64, + the same affine of second[0]
-    under second[1:] (rounded to bf16), + residual (rounded to bf16), then
-    act "none" / "relu" / "relu6".  The result keeps x's strides."""
-    x = x.detach().to("cpu")
-    n, c, h, w = x.shape
-    if x.is_contiguous():
-        layout = 0
-    else:
-        assert x.is_contiguous(memory_format=torch.channels_last), x.stride()
-        layout = 1
-
-    def cpu(t):
-        t = t.detach().to("cpu")
-        assert t.stride() == x.stride() or t.dim() == 1, (t.stride(), x.stride())
-        return t.contiguous() if t.dim() == 1 else t
-
-    params = [cpu(t) for t in (mean, var, weight, bias)]
-    x2, p2 = None, [None] * 4
-    if second is not None:
-        x2 = cpu(second[0])
-        p2 = [cpu(t) for t in second[1:]]
-    res = cpu(residual) if residual is not None else None
-    y = torch.empty_strided(tuple(x.shape), tuple(x.stride()), dtype=torch.bfloat16)
-    ptr = lambda t: t.data_ptr() if t is not None else None  # noqa: E731
-    load().ref_bn_infer_act_bf16(ptr(x), *[ptr(t) for t in params], ptr(x2),
-                                 *[ptr(t) for t in p2], ptr(res), ptr(y), n, c, h * w, layout,
-                                 float(eps), BN_ACTS[act], _th(threads))
-    return y

@@ -25,8 +25,6 @@
  *   bf16 BN + SiLU + pad (NHWC)   repros/canonical/var_mean_ceb5c315290a/repro.py:27-58
  *   bf16 BN + ReLU + mean (NCHW)  repros/canonical/var_mean_mean_19ffdb35cc67/repro.py:23-54
  *   GELU(erf) bwd + column sum    repros/canonical/sum_139a3020e8bf/repro.py:24-48
- *   bf16 <-> fp32 casts           repros/canonical/pointwise_04d85912d998/repro.py:24-27 (and
- *                                 pointwise_ccd411f2a45d, pointwise_8bb40810003c)
  * (paths relative to the reference tree).  Every rounding that the eager
  * graph performs on a bf16 tensor is reproduced (float arithmetic, then
  * round-to-nearest-even to bf16); reductions and transcendental functions
@@ -559,74 +557,4 @@ void ref_gelu_erf_bwd_colsum_bf16(const uint16_t* g, const uint16_t* x, uint16_t
     colsum[c] = bf16_to_f32(f64_to_bf16(s));
   }
   free(part);
-}
-
-/* Storage-order casts (repros/canonical/pointwise_04d85912d998/repro.py:24-27,
- * pointwise_ccd411f2a45d/repro.py:24-27, pointwise_8bb40810003c/repro.py:24-29):
- * bf16 -> fp32 exact; fp32 -> bf16 to nearest even (NaN stays NaN). */
-void ref_cast_bf16_to_f32(const uint16_t* x, float* y, int64_t n, int threads) {
-#pragma omp parallel for num_threads(threads) schedule(static)
-  for (int64_t i = 0; i < n; ++i) y[i] = bf16_to_f32(x[i]);
-}
-
-void ref_cast_f32_to_bf16(const float* x, uint16_t* y, int64_t n, int threads) {
-#pragma omp parallel for num_threads(threads) schedule(static)
-  for (int64_t i = 0; i < n; ++i) y[i] = f32_to_bf16(x[i]);
-}
-
-/* BatchNorm inference affine + epilogue (reference repros
- * pointwise_7899d74e0838 / 818c3aa59952 / e6ddc8e897ec / 9595e73ff43b /
- * 81485f33f5b9 / 2c331ef4f17f, repro.py:24-47 / 24-45 / 24-46 / 24-50 /
- * 24-47 / 24-66): per channel inv = reciprocal(sqrt(f32(var) + eps)) * 1 in
- * fp32 (IEEE), per element bf16(f32(((x - mean) * inv) * w + b)) with the
- * four ops in fp64; then + the second affine (rounded to bf16), +
- * residual (rounded to bf16), then relu (act 1) or clamp to [0, 6] (act 2),
- * NaN kept and -0 -> +0.  Walks logical (n, c, p) and addresses storage from
- * the layout: NCHW offset (n * C + c) * HW + p, channels-last
- * (n * HW + p) * C + c. */
-static inline float bn_inv(uint16_t v, float eps) {
-  volatile float s = sqrtf(bf16_to_f32(v) + eps);
-  volatile float inv = 1.0f / s;
-  return inv * 1.0f;
-}
-
-/* The element ops of the graph's fp64 evaluation (the reference harness's
- * numerics anchor, oracle_harness.py:1511-1530): var is cast to fp32 in
- * the graph, so inv stays fp32; sub, mul, mul, add run in fp64; the bf16
- * cast of the fp64 result goes through fp32. */
-static inline float bn_affine_bf16(uint16_t xv, uint16_t m, float inv, uint16_t w, uint16_t b) {
-  volatile double sub = (double)bf16_to_f32(xv) - (double)bf16_to_f32(m);
-  volatile double mul1 = sub * (double)inv;
-  volatile double mul2 = mul1 * (double)bf16_to_f32(w);
-  volatile double add1 = mul2 + (double)bf16_to_f32(b);
-  return round_bf16((float)add1);
-}
-
-void ref_bn_infer_act_bf16(const uint16_t* x, const uint16_t* mean, const uint16_t* var,
-                           const uint16_t* w, const uint16_t* b, const uint16_t* x2,
-                           const uint16_t* mean2, const uint16_t* var2, const uint16_t* w2,
-                           const uint16_t* b2, const uint16_t* res, uint16_t* y, int64_t n,
-                           int64_t c, int64_t hw, int channels_last, float eps, int act,
-                           int threads) {
-#pragma omp parallel for collapse(2) num_threads(threads) schedule(static)
-  for (int64_t in = 0; in < n; ++in)
-    for (int64_t ic = 0; ic < c; ++ic) {
-      const float inv = bn_inv(var[ic], eps);
-      const float inv2 = x2 ? bn_inv(var2[ic], eps) : 0.0f;
-      for (int64_t p = 0; p < hw; ++p) {
-        const int64_t o = channels_last ? (in * hw + p) * c + ic : (in * c + ic) * hw + p;
-        float t = bn_affine_bf16(x[o], mean[ic], inv, w[ic], b[ic]);
-        if (x2) {
-          volatile float s2 = t + bn_affine_bf16(x2[o], mean2[ic], inv2, w2[ic], b2[ic]);
-          t = round_bf16(s2);
-        }
-        if (res) {
-          volatile float s3 = t + bf16_to_f32(res[o]);
-          t = round_bf16(s3);
-        }
-        if (act == 1 && !isnan(t)) t = t > 0.0f ? t : 0.0f;
-        if (act == 2 && !isnan(t)) t = t > 6.0f ? 6.0f : (t > 0.0f ? t : 0.0f);
-        y[o] = f32_to_bf16(t);
-      }
-    }
 }

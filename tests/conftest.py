@@ -68,15 +68,6 @@ VARIANT_IDS = [
     "amax_sum_fa4cc85fe5ad",
 ] + list(LN_FAMILY_OUTPUTS) + list(RMS_FAMILY_OUTPUTS) + [
     "sum_139a3020e8bf",
-    "pointwise_04d85912d998",
-    "pointwise_ccd411f2a45d",
-    "pointwise_8bb40810003c",
-    "pointwise_7899d74e0838",
-    "pointwise_818c3aa59952",
-    "pointwise_e6ddc8e897ec",
-    "pointwise_9595e73ff43b",
-    "pointwise_81485f33f5b9",
-    "pointwise_2c331ef4f17f",
 ]
 
 

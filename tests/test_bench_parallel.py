@@ -54,8 +54,7 @@ def test_find_and_expand_the_canonical_dirs():
     # ragged); the corpus families carry the reference's points
     assert len(tasks) == (3 * len(REPRO_IDS) + 16 + 1 + 1 + 1 + 2 + 1 + 6 + 2 + 1 + 2
                           + 13 + 5 + 1 + 16 + 9 + 5 + 5
-                          + 1 + 2 + 2 + 2 + 1 + 1 + 1 + 2 + 2 + 1 + 15 + 469 + 455 + 84
-                          + 121 + 52 + 24 + 22 + 21 + 23)
+                          + 1 + 2 + 2 + 2 + 1 + 1 + 1 + 2 + 2 + 1 + 15)
     assert all("::SHAPE::" in t for t in tasks)
     from repro_harness import load_shape_configs
     for d in dirs:

@@ -127,73 +127,6 @@ def test_plain_softmax_family_repro():
     assert torch.equal(y, torch.softmax(x.float(), -1).to(bf))
 
 
-def test_cast_family_repros():
-    """The three cast families: eager's preserve-format convert_element_type
-    (strides kept), and the fp32 -> bf16 weight returned as its transpose and
-    itself, both views of one tensor."""
-    g = torch.Generator().manual_seed(22)
-    x = torch.randn(4, 6, 3, 3, generator=g).to(memory_format=torch.channels_last)
-    y = get_repro_instance(CANONICAL / "pointwise_04d85912d998")(x.to(bf))
-    assert y.dtype == torch.float32 and y.stride() == x.stride() and torch.equal(y, x.to(bf).float())
-    y = get_repro_instance(CANONICAL / "pointwise_ccd411f2a45d")(x)
-    assert y.dtype == bf and y.stride() == x.stride() and torch.equal(y, x.to(bf))
-    w = torch.randn(5, 7, generator=g)
-    wt, w2 = get_repro_instance(CANONICAL / "pointwise_8bb40810003c")(w)
-    assert wt.shape == (7, 5) and w2.shape == (5, 7) and wt.data_ptr() == w2.data_ptr()
-    assert torch.equal(w2, w.to(bf)) and w2.is_contiguous()
-
-
-
-def test_bn_infer_family_repros():
-    """The six BN-inference family graphs: within bf16 roundings of
-    torch.nn.functional.batch_norm in eval mode (then the epilogue), and bit
-    for bit the C oracle, in both layouts."""
-    import oracle as ref
-    g = torch.Generator().manual_seed(24)
-    c = 12
-    fams = {"pointwise_7899d74e0838": (1e-3, "relu", None),
-            "pointwise_818c3aa59952": (1e-5, "none", None),
-            "pointwise_e6ddc8e897ec": (1e-5, "none", "residual"),
-            "pointwise_9595e73ff43b": (1e-5, "relu6", None),
-            "pointwise_81485f33f5b9": (1e-5, "relu", "residual"),
-            "pointwise_2c331ef4f17f": (1e-5, "relu", "dual")}
-
-    def params():
-        return [torch.randn(c, generator=g).to(bf), (torch.rand(c, generator=g) + 0.1).to(bf),
-                torch.randn(c, generator=g).to(bf), torch.randn(c, generator=g).to(bf)]
-
-    def textbook(x, mean, var, w, b, eps):
-        return torch.nn.functional.batch_norm(x.float(), mean.float(), var.float(), w.float(),
-                                              b.float(), training=False, eps=eps)
-
-    for fmt in (torch.contiguous_format, torch.channels_last):
-        for rid, (eps, act, kind) in fams.items():
-            x = (2 * torch.randn(3, c, 5, 4, generator=g)).to(bf).to(memory_format=fmt)
-            x2 = (2 * torch.randn(3, c, 5, 4, generator=g)).to(bf).to(memory_format=fmt)
-            p, p2 = params(), params()
-            inputs = [p[0], x, *p[1:]]
-            want = textbook(x, *p, eps)
-            kw = {}
-            if kind == "residual":
-                inputs.append(x2)
-                want = want + x2.float()
-                kw["residual"] = x2
-            if kind == "dual":
-                inputs += [p2[0], x2, *p2[1:]]
-                want = want + textbook(x2, *p2, eps)
-                kw["second"] = (x2, *p2)
-            want = want.clamp(0, 6) if act == "relu6" else (want.relu() if act == "relu" else want)
-            y = get_repro_instance(CANONICAL / rid)(*inputs)
-            assert y.dtype == bf and y.stride() == x.stride(), rid
-            # two or three bf16 roundings, the sum's taken at its operands' scale
-            tol = 2 ** -6 * (1 + want.abs() + x2.float().abs())
-            assert ((y.float() - want).abs() <= tol).all(), rid
-            # the oracle takes the element ops in fp64 (as the graph's fp64
-            # evaluation), the fp32 graph rounds each: one bf16 ulp apart at most
-            o = ref.bn_infer_act(x, *p, eps=eps, act=act, **kw).float()
-            mag = torch.maximum(y.float().abs(), o.abs()).clamp_min(2.0 ** -126)
-            assert ((y.float() - o).abs() <= torch.exp2(torch.floor(torch.log2(mag)) - 7)).all()
-
 def test_gelu_bwd_family_repro():
     """GELU(erf) backward + column sum: y against ATen's own gelu_backward
     (fp32, within a bf16 rounding), its transpose a view of y, the column sum

@@ -78,3 +78,33 @@ def test_noalloc_rejects_shapes_beyond_the_scratch_array(rocm_device):
                                                   1, stream)
     assert rc == 1000  # HIPO_EINVAL
     assert "scratch array" in lib.hipo_last_error().decode()
+
+
+def test_noalloc_forced_timeout_is_reported(rocm_device, monkeypatch):
+    """Failure injection from the host on the allocation-free path
+    (HIPO_TEST_FORCE_BN_TIMEOUT: every exchange wait looks for a tag no
+    workgroup publishes, gives up after a few polls, and the kernel exits
+    normally): the outputs and running statistics are NaN, the sticky error
+    word in the static scratch array is reported by device_faults() (read
+    through hipo_batchnorm_noalloc_error) and cleared, and the next call
+    without injection matches the workspace entry point again."""
+    import hip_oracles
+    lib = hip_oracles.load_library()
+    shape = SHAPES[0]  # the single-pass kernel with its cross-workgroup exchange
+    _run(lib, rocm_device, shape, 5, noalloc=True)  # the array is set up
+    hip_oracles.device_faults()  # start clean
+    monkeypatch.setenv("HIPO_TEST_FORCE_BN_TIMEOUT", "1")
+    out = _run(lib, rocm_device, shape, 5, noalloc=True)
+    for name, t in zip(("y", "save_mean", "save_invstd", "running_mean", "running_var"), out):
+        assert torch.isnan(t).all(), f"{name} not poisoned after a timed-out exchange"
+    faults = hip_oracles.device_faults()
+    assert len(faults) == 1 and "noalloc" in faults[0] and "timed out" in faults[0], faults
+    assert hip_oracles.device_faults() == [], "the error word was not cleared"
+    monkeypatch.delenv("HIPO_TEST_FORCE_BN_TIMEOUT")
+    got = _run(lib, rocm_device, shape, 6, noalloc=True)
+    want = _run(lib, rocm_device, shape, 6, noalloc=False)
+    for name, a, b in zip(("y", "save_mean", "save_invstd", "running_mean", "running_var"),
+                          got, want):
+        assert torch.equal(a, b), f"after the injected timeout: {name}"
+    assert hip_oracles.device_faults() == []
+
