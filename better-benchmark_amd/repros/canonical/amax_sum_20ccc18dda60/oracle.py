@@ -1,4 +1,10 @@
-"""
+"""Gap diagnosis (classification: NEW_PATTERN): this oracle computes softmax(scores + bias) over 256-wide rows with 16 lanes per row holding it in registers (four rows per wave instruction, segmented DPP reductions, the group's bias row read from cache) and reads the scores once, whereas Inductor emits triton_red_fused_add_convert_element_type_div_exp_prepare_softmax_online_sub_view_0, a looped reduction that walks each row twice -- an online max / sum pass and an output pass that reloads scores and bias and evaluates exp again; Inductor cannot do this today because for this shape its heuristics pick a non-persistent reduction and have no several-rows-per-wave layout for short rows; the fix is NEW_PATTERN: a short-row softmax template (several rows per wave, the row in registers, one exp per element).
+
+Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
+flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
+38831ee4, oracle 55.83 us, Inductor 120.06 us (ratio 2.15, GOOD); over the dir's 1
+points: 1 GOOD.
+
 MI355X oracle for amax_sum_20ccc18dda60: softmax(scores + bias) with the
 bias [G, 1, Q, K] shared by the heads of each group (TrOCR attention).
 
@@ -10,12 +16,8 @@ Replaces the Triton body of the reference's
 repros/canonical/amax_sum_20ccc18dda60/oracle.py:63
 (_broadcast_add_softmax_kernel, :12).
 """
-import sys
-from pathlib import Path
-
-sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
-import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl, oracle_main  # noqa: E402
+import hip_oracles
+from oracle_harness import oracle_impl, oracle_main
 
 
 @oracle_impl(hardware="MI355X", point="38831ee4", description="bias softmax, rows in registers")

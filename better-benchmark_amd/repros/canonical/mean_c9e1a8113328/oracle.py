@@ -1,4 +1,10 @@
-"""
+"""Gap diagnosis (classification: BANDWIDTH_BOUND): this oracle reduces a channels-last image over its H * W positions with every workgroup instruction reading whole contiguous position rows (all channels), fp32 sums per 8-channel group per thread and a fixed-order LDS merge, whereas Inductor emits triton_red_fused_mean_0, a looped reduction with one output per (image, channel) that walks the positions with channel-strided evict_first loads; Inductor cannot do this today because its reduction codegen keeps the reduced axis as the loop axis and does not re-tile a non-innermost reduction so that loads run along the contiguous channel axis; the fix is BANDWIDTH_BOUND: a column-reduction template for channels-last spatial means.
+
+Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
+flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
+2150fa2c, oracle 64.51 us, Inductor 65.43 us (ratio 1.014, AT_FLOOR); over the dir's 16
+points: 11 AT_FLOOR, 4 GOOD, 1 BAD_ORACLE.
+
 MI355X oracle for mean_c9e1a8113328: spatial mean of a channels-last bf16
 tensor over H, W (keepdim).
 
@@ -10,12 +16,8 @@ adds the slices in order).  Algorithmic bytes: 2 N H W C + 2 N C.
 Replaces the Triton body of the reference's
 repros/canonical/mean_c9e1a8113328/oracle.py:95 (_spatial_mean_cl_kernel, :11).
 """
-import sys
-from pathlib import Path
-
-sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
-import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl, oracle_main  # noqa: E402
+import hip_oracles
+from oracle_harness import oracle_impl, oracle_main
 
 _POINTS = ("69db7514", "280fa7d2", "2645a53e", "4ca56f88", "d1686c77", "333b11d0",
            "547c8164", "f0a667e3", "44f1e75f", "4784273d", "3cf84b69", "2150fa2c",

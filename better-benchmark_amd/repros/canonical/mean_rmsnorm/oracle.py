@@ -1,4 +1,10 @@
-"""
+"""Gap diagnosis (classification: BANDWIDTH_BOUND): this oracle reads x once: four waves hold each 4096-element row in registers through the fp32 sum of squares and the scaling, with non-temporal loads and stores, whereas Inductor emits triton_red_fused_add_convert_element_type_mean_mul_pow_rsqrt_0, a looped reduction whose first loop accumulates x^2 with evict_last loads and whose second loop reloads x (evict_first) and gamma to write y; Inductor cannot do this today because for rows this wide it picks a looped (non-persistent) reduction, which must walk the row twice -- the second time from cache -- instead of keeping it in registers across the statistics and the epilogue (the re-read hits in cache, so one cached launch sees the two kernels at about the same time, and a sustained stream separates them); the fix is BANDWIDTH_BOUND: a multi-wave persistent row reduction for rows of a few thousand elements that keeps the row in registers from the statistics to the epilogue, with non-temporal streams.
+
+Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
+flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
+0390a437, oracle 52.27 us, Inductor 51.47 us (ratio 0.985, AT_FLOOR); over the dir's 3
+points: 3 AT_FLOOR.
+
 MI355X oracle for mean_rmsnorm: y = x * rsqrt(mean(x^2) + eps) * gamma, rstd.
 
 Kernel: hipo_rmsnorm_bf16 -- the row in registers (4 waves per row at
@@ -8,12 +14,8 @@ bytes: 4 R C + 2 C + 4 R.
 Replaces the Triton body of the reference's
 repros/canonical/mean_4462ce967d63/oracle.py:65.
 """
-import sys
-from pathlib import Path
-
-sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
-import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl, oracle_main  # noqa: E402
+import hip_oracles
+from oracle_harness import oracle_impl, oracle_main
 
 EPS = 1e-05  # the graph constant of repro.py
 

@@ -1,4 +1,10 @@
-"""
+"""Gap diagnosis (classification: ALGEBRAIC_ELIMINATION): this oracle evaluates the decomposed tanh GELU as x * sigmoid(2u) -- for bf16, the correctly rounded result of every input (an fp32 exp2 / rcp form shown exact over the whole domain, an exact table below x = -4); for fp32, x / (1 + e^-2u) with an extended-precision exp and an IEEE division -- streamed as 8 KiB per wave with non-temporal accesses, whereas Inductor emits triton_poi_fused_add_mul_pow_tanh_view_0, a flat pointwise kernel that evaluates 0.5 x (1 + libdevice.tanh(u)) per element, whose 1 + tanh cancels in the negative tail; Inductor cannot do this today because it lowers aten.tanh literally and does not rewrite 0.5 x (1 + tanh(u)) into the algebraically equal, cheaper and cancellation-free x * sigmoid(2u); the fix is ALGEBRAIC_ELIMINATION: that rewrite in the pointwise lowering.
+
+Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
+flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
+8f687505, oracle 68.35 us, Inductor 65.87 us (ratio 0.964, AT_FLOOR); over the dir's 6
+points: 4 GOOD, 2 AT_FLOOR.
+
 MI355X oracle for pointwise_2d969ac9ad59: tanh GELU of a contiguous bf16 or
 fp32 activation, returned in the second view's shape.
 
@@ -12,12 +18,8 @@ an IEEE division (the same function, without 1 + tanh(u)'s cancellation).  Flat 
 Replaces the Triton body of the reference's
 repros/canonical/pointwise_2d969ac9ad59/oracle.py:44-62 (_tanh_gelu_kernel, :12).
 """
-import sys
-from pathlib import Path
-
-sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
-import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl, oracle_main  # noqa: E402
+import hip_oracles
+from oracle_harness import oracle_impl, oracle_main
 
 _POINTS = ("cd47785e", "92efc45e", "d05618d1", "7b14189f", "5cd82a46", "8f687505")
 

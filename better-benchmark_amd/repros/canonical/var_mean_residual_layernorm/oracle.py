@@ -1,4 +1,10 @@
-"""
+"""Gap diagnosis (classification: BANDWIDTH_BOUND): this oracle computes h = bf16(x + residual), the exact fp32 row statistics of h and y in one pass with each 4096-element row held in registers by two waves (gamma and beta staged in LDS, non-temporal 16-byte streams), whereas Inductor emits triton_red_fused_add_convert_element_type_mul_rsqrt_sub_var_mean_0, a looped reduction that stores h and merges Welford triples in its first R0_BLOCK loop and reloads h from its own output in a second loop to normalise; Inductor cannot do this today because for rows this wide it picks a looped (non-persistent) reduction, which must walk the row twice -- the second time from cache -- instead of keeping it in registers across the statistics and the epilogue; the fix is BANDWIDTH_BOUND: a multi-wave persistent row reduction for rows of a few thousand elements that keeps the row in registers from the statistics to the epilogue, with non-temporal streams.
+
+Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
+flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
+fe9bbcba, oracle 94.47 us, Inductor 106.79 us (ratio 1.13, NUMERICS_OPTOUT_ACCEPTED);
+over the dir's 3 points: 3 NUMERICS_OPTOUT_ACCEPTED.
+
 MI355X oracle for var_mean_residual_layernorm:
 h = x + residual; y = LayerNorm(h) * gamma + beta; mean, rstd (fp32).
 
@@ -10,12 +16,8 @@ Replaces the Triton body of the reference's
 repros/canonical/var_mean_80e7ff4dee7f/oracle.py:122 (without its
 anchor-clamp of the output).
 """
-import sys
-from pathlib import Path
-
-sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
-import hip_oracles  # noqa: E402
-from oracle_harness import oracle_impl, oracle_main  # noqa: E402
+import hip_oracles
+from oracle_harness import oracle_impl, oracle_main
 
 EPS = 1e-05  # the graph constant of repro.py
 

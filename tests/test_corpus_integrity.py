@@ -100,3 +100,34 @@ def test_generated_inputs_keep_point_layouts(rid):
                     torch.empty(spec["shape"], device="meta",
                                 memory_format=torch.channels_last).stride()) and math.prod(t.shape[1:2]) > 1:
                 assert t.is_contiguous(memory_format=torch.channels_last)
+
+
+# The reference's oracle-file contract (scripts/ORACLE_FORMAT.md:27, 64-72):
+# the file opens with a one-sentence gap diagnosis whose classification is
+# one of seven, naming what the oracle does, what Inductor does instead, why
+# Inductor cannot do it today and the fix; and it does no sys.path surgery
+# (the package comes from the environment -- PYTHONPATH here).
+GAP_CLASSES = ("SCHEDULER_FUSION", "SCATTER_REDUCE", "COOPERATIVE_SPLIT_K",
+               "ALGEBRAIC_ELIMINATION", "RECOMPUTE_FUSION", "BANDWIDTH_BOUND", "NEW_PATTERN")
+
+
+@pytest.mark.parametrize("rid", REPRO_IDS + VARIANT_IDS)
+def test_oracle_file_format(rid):
+    import re
+    src = (CANONICAL / rid / "oracle.py").read_text()
+    first = src.splitlines()[0]
+    m = re.match(r'"""Gap diagnosis \(classification: ([A-Z_]+)\): (.*)$', first)
+    assert m, f"{rid}: oracle.py must open with the gap-diagnosis docstring, got {first[:80]!r}"
+    cls, sentence = m.groups()
+    assert cls in GAP_CLASSES, f"{rid}: classification {cls} is not one of {GAP_CLASSES}"
+    assert sentence.startswith("this oracle ") and ", whereas Inductor " in sentence, rid
+    assert "; Inductor cannot do this today because " in sentence, rid
+    assert f"; the fix is {cls}: " in sentence, rid
+    doc = ast.get_docstring(ast.parse(src))
+    assert doc and doc.startswith("Gap diagnosis"), rid
+    tree = ast.parse(src)
+    for node in ast.walk(tree):
+        if isinstance(node, ast.Attribute) and node.attr == "path" and \
+                isinstance(node.value, ast.Name) and node.value.id == "sys":
+            pytest.fail(f"{rid}: oracle.py touches sys.path (line {node.lineno})")
+    assert "sys.path" not in src, f"{rid}: oracle.py mentions sys.path"
