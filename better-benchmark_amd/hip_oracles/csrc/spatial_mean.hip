@@ -140,6 +140,7 @@ struct SpatialPlan {
 // Channel blocks of 64 groups (1 KiB of each row), or of 32 (512 bytes),
 // when the row divides into them and images x blocks give at least 256
 // workgroups: no position split, so no partial sums and no second kernel.
+// 64-group blocks are tried first, except for small images (below).
 // The workgroup takes R rows per instruction, the smallest power of two
 // that covers the image's positions in four rounds of kUnroll loads per
 // thread, at most 512 threads.
@@ -156,7 +157,13 @@ constexpr int kChannelBlock = 64;
 SpatialPlan spatial_plan(int64_t n, int64_t p, int64_t c) {
   SpatialPlan plan;
   if (c % 8 != 0 || c / 8 > kMaxThreads || n <= 0 || p <= 0) return plan;
-  for (const int gb : {kChannelBlock, kChannelBlock / 2}) {
+  // Small images (at most 128 positions) take 32-group blocks first: twice
+  // the workgroups for the same bytes ([128, 1536, 9, 9] 8.53 -> 8.03 us,
+  // [128, 1536, 8, 8] 6.81 -> 6.60, [128, 1536, 6, 6] 5.68 -> 5.52 in the
+  // steady loop; larger images unchanged).
+  const int first = p <= 128 ? kChannelBlock / 2 : kChannelBlock;
+  const int gbs[2] = {first, kChannelBlock + kChannelBlock / 2 - first};
+  for (const int gb : gbs) {
     if ((c / 8) % gb != 0 || n * (c / 8 / gb) < 256) continue;
     int64_t r = 1;
     while (r * kUnroll * 4 < p && gb * r * 2 <= 512) r *= 2;
