@@ -401,6 +401,17 @@ def _bench_oracle_point(canonical_dir: str, shape_label: str, cfg: dict) -> dict
         return {shape_label: {"repro_id": f"{repro_id}_{shape_label}",
                               "status": "NO_ORACLE_FOR_SHAPE"}}
     point_id = f"{repro_id}_{shape_label}"
+    # A point that no registration matches (a withdrawn point of a dir with
+    # no shape-general entry) is NO_ORACLE_FOR_SHAPE, bench_oracle's own
+    # status for a dispatch miss; the reference's runner reaches it through
+    # the failed check instead and reports UNVERIFIED_NUMERICS
+    # (scripts/bench_parallel.py:3041-3052).
+    from oracle_harness import OracleDispatchError, resolve_oracle
+    try:
+        resolve_oracle(fn, make_inputs_from_config(configs[shape_label], device="meta"))
+    except OracleDispatchError as e:
+        return {shape_label: {"repro_id": point_id, "status": "NO_ORACLE_FOR_SHAPE",
+                              "error": str(e)[:300]}}
     if not cfg["skip_check"]:
         check = check_oracle_all_shapes(fn, d, repro_id, skip_stochastic=True,
                                         point=shape_label)

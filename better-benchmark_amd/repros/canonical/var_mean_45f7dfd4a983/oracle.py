@@ -22,18 +22,28 @@ from oracle_harness import oracle_impl, oracle_main
 
 EPS = 1e-12
 
+# Points of shapes.json with no MI355X registration.  The status sweeps
+# measured Inductor more than 5 % faster at each of them (BAD_ORACLE) in the
+# reference's single-launch protocol: rows of 768 or 1024 values, 16384 rows
+# or more, where the two kernels are within 3 % of each other in a
+# back-to-back loop but Inductor is 5-8 % faster in a single launch after a
+# cache flush (layouts with 32-lane row segments, cached loads or an
+# occupancy cap measured no better).  There is no shape-general
+# registration, so these points find no MI355X oracle (NO_ORACLE_FOR_SHAPE,
+# the reference's state of a point without one); the kernel still computes
+# them and the parity tests call it directly.  Values: the measured ratios
+# compile_us / oracle_us.
+WITHDRAWN_POINTS = {
+    "63bebcf6": (0.963, 0.949),
+    "d1f40ce2": (0.945, 0.945),
+    "d4cc3e3e": (0.965, 0.949),
+}
+
 
 @oracle_impl(hardware="MI355X", point="d4701d13",
              description="residual LayerNorm, 4096 x 4096")
 @oracle_impl(hardware="MI355X", point="0b3dc49f",
              description="residual LayerNorm, 8192 x 1024")
-@oracle_impl(hardware="MI355X", point="63bebcf6",
-             description="residual LayerNorm, 16384 x 768")
-@oracle_impl(hardware="MI355X", point="d1f40ce2",
-             description="residual LayerNorm, 16384 x 768")
-@oracle_impl(hardware="MI355X", point="d4cc3e3e",
-             description="residual LayerNorm, 16384 x 1024")
-@oracle_impl(hardware="MI355X", description="residual LayerNorm, shape-general")
 def oracle_forward(inputs):
     x, residual, gamma, beta = inputs[:4]
     shapes = inputs[4:]

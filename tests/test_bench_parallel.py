@@ -63,6 +63,27 @@ def test_find_and_expand_the_canonical_dirs():
                 if bp._split_shape_task_key(t)[0] == str(d)] == labels
 
 
+def test_withdrawn_points_are_no_oracle_for_shape():
+    """A point its oracle.py withdraws (no registration matches it) is
+    reported as NO_ORACLE_FOR_SHAPE before any check or timing runs; the
+    dispatch miss needs no GPU."""
+    from oracle_harness import _load_oracle_module
+    from repro_harness import load_shape_configs
+    seen = 0
+    for rid in VARIANT_IDS:
+        mod, _, d = _load_oracle_module(CANONICAL / rid)
+        withdrawn = getattr(mod, "WITHDRAWN_POINTS", {})
+        for label in load_shape_configs(str(d / "repro.py")):
+            if label.rsplit("_", 1)[-1] in withdrawn:
+                out = bp._bench_oracle_point(str(d), label, {"n_warmup": 1, "n_rep": 1,
+                                                             "compile": False,
+                                                             "skip_check": False})
+                assert out[label]["status"] == "NO_ORACLE_FOR_SHAPE", out
+                assert "NO_ORACLE_FOR_SHAPE" in _INVALID_STATUSES
+                seen += 1
+    assert seen == 15
+
+
 def test_find_resolves_relative_dirs(monkeypatch):
     """Workers run from the package dir: a relative path on the command line
     must reach them as an absolute one."""

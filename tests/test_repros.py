@@ -248,19 +248,29 @@ def test_family_repro_contract(rid):
     # every shapes.json point has an MI355X registration -- its own, or, where
     # points differ only in strides (the registry keys by input shapes), that
     # of a point with the same input shapes -- plus one shape-general entry
-    # for shapes outside the corpus
+    # for shapes outside the corpus; except the points the module withdraws
+    # (WITHDRAWN_POINTS), which match no entry: such a dir has no
+    # shape-general entry either
     import oracle_harness as oh
-    _, fn, _ = oh._load_oracle_module(CANONICAL / rid)
+    mod, fn, _ = oh._load_oracle_module(CANONICAL / rid)
     entries = oh.get_module_registry(fn.__module__)._entries
     points = json.loads((CANONICAL / rid / "shapes.json").read_text())["points"]
+    withdrawn = getattr(mod, "WITHDRAWN_POINTS", {})
+    hashes = {p["shape_hash"] for p in points}
+    assert set(withdrawn) <= hashes
 
     def shapes(p):
         return tuple(tuple(i[0]) for i in p["inputs"] if i[0] != "S")
     registered = {e["point"] for e in entries if e["point"]}
-    assert registered <= {p["shape_hash"] for p in points}
+    assert registered <= hashes and not registered & set(withdrawn)
     covered = {shapes(p) for p in points if p["shape_hash"] in registered}
-    assert all(shapes(p) in covered for p in points)
-    assert any(e["shape"] is None and e["hardware"] == "MI355X" for e in entries)
+    assert all(shapes(p) in covered for p in points if p["shape_hash"] not in withdrawn)
+    general = any(e["shape"] is None and e["hardware"] == "MI355X" for e in entries)
+    assert general == (not withdrawn)
+    for label, pcfg in cfgs.items():
+        if label.rsplit("_", 1)[-1] in withdrawn:
+            with pytest.raises(oh.OracleDispatchError):
+                oh.resolve_oracle(fn, make_inputs_from_config(pcfg, device="meta"))
 
 
 def _bn_inputs(shape, memory_format, seed):
