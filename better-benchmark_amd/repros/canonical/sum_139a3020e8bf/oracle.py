@@ -21,6 +21,17 @@ repros/canonical/sum_139a3020e8bf/oracle.py:101.
 import hip_oracles
 from oracle_harness import oracle_impl, oracle_main
 
+# Points of shapes.json with no MI355X registration: [128, 3072] (0.8 MB),
+# one launch of 48 workgroups at the graph-replay floor, where the oracle
+# holds 15.0-15.1 us and Inductor's re-tuned kernels took 14.3-16.7 us
+# across the status sweeps (BAD_ORACLE in two of three).  There is no
+# shape-general registration, so the point finds no MI355X oracle
+# (NO_ORACLE_FOR_SHAPE); the kernel still computes it and the parity tests
+# call it directly.  Values: the measured ratios compile_us / oracle_us.
+WITHDRAWN_POINTS = {
+    "67c7a377": (1.115, 0.952, 0.944),
+}
+
 
 @oracle_impl(hardware="MI355X", point="8572c66c",
              description="GELU(erf) bwd + column sum, 25216 x 3072")
@@ -32,8 +43,6 @@ from oracle_harness import oracle_impl, oracle_main
              description="GELU(erf) bwd + column sum, 175360 x 3072")
 @oracle_impl(hardware="MI355X", point="c064ba70",
              description="GELU(erf) bwd + column sum, 32768 x 3072")
-@oracle_impl(hardware="MI355X", point="67c7a377",
-             description="GELU(erf) bwd + column sum, 128 x 3072")
 @oracle_impl(hardware="MI355X", point="8951d544",
              description="GELU(erf) bwd + column sum, 8192 x 4096")
 @oracle_impl(hardware="MI355X", point="a448a1c6",
@@ -52,7 +61,6 @@ from oracle_harness import oracle_impl, oracle_main
              description="GELU(erf) bwd + column sum, 16384 x 4096")
 @oracle_impl(hardware="MI355X", point="7c4310e0",
              description="GELU(erf) bwd + column sum, 4096 x 4096")
-@oracle_impl(hardware="MI355X", description="GELU(erf) bwd + column sum, shape-general")
 def oracle_forward(inputs):
     grad, x, _shape0, _shape1, shape2, shape3 = inputs
     rows, cols = int(shape2[0]), int(shape2[1])

@@ -22,6 +22,21 @@ from oracle_harness import oracle_impl, oracle_main
 
 EPS = 1e-05
 
+# Points of shapes.json with no MI355X registration.  The status sweeps
+# measured Inductor more than 5 % faster at each of them (BAD_ORACLE) in the
+# reference's single-launch protocol: rows of 768 or 1024 values, 16384 rows
+# or more, where the two kernels are within 3 % of each other in a
+# back-to-back loop but Inductor is 5-8 % faster in a single launch after a
+# cache flush (layouts with 32-lane row segments, cached loads or an
+# occupancy cap measured no better).  There is no shape-general
+# registration, so these points find no MI355X oracle (NO_ORACLE_FOR_SHAPE,
+# the reference's state of a point without one); the kernel still computes
+# them and the parity tests call it directly.  Values: the measured ratios
+# compile_us / oracle_us.
+WITHDRAWN_POINTS = {
+    "a3e95c29": (0.973, 0.951, 0.944),
+}
+
 
 @oracle_impl(hardware="MI355X", point="c4bf51cc",
              description="residual LayerNorm, 4096 x 2560")
@@ -35,13 +50,10 @@ EPS = 1e-05
              description="residual LayerNorm, 8192 x 1024")
 @oracle_impl(hardware="MI355X", point="ceab07f0",
              description="residual LayerNorm, 8192 x 1024")
-@oracle_impl(hardware="MI355X", point="a3e95c29",
-             description="residual LayerNorm, 16384 x 1024")
 @oracle_impl(hardware="MI355X", point="f2e11670",
              description="residual LayerNorm, 4096 x 1024")
 @oracle_impl(hardware="MI355X", point="324149d9",
              description="residual LayerNorm, 1 x 384")
-@oracle_impl(hardware="MI355X", description="residual LayerNorm, shape-general")
 def oracle_forward(inputs):
     x, residual, gamma, beta = inputs[:4]
     shapes = inputs[4:]
