@@ -102,8 +102,8 @@ int hipo_scaled_masked_softmax_bf16(const uint16_t* x, const uint16_t* mask,
  * repros/canonical/var_mean_80e7ff4dee7f/oracle.py:122
  * (_residual_layernorm_kernel, same file :51), and of the residual-LayerNorm
  * families var_mean_0ada225c0a04, var_mean_96edf0542ecd,
- * var_mean_ee167627f636, var_mean_f4578c128d74, var_mean_b19e82f2a47b,
- * var_mean_393456b916a6 and var_mean_45f7dfd4a983 (oracle.py, oracle_forward).
+ * var_mean_f4578c128d74, var_mean_b19e82f2a47b, var_mean_393456b916a6 and
+ * var_mean_45f7dfd4a983 (oracle.py, oracle_forward).
  */
 int hipo_residual_layernorm_bf16(const uint16_t* x, const uint16_t* residual,
                                  const uint16_t* gamma, const uint16_t* beta,

@@ -29,7 +29,6 @@ REPRO_IDS = [
 LN_FAMILY_OUTPUTS = {
     "var_mean_0ada225c0a04": "y2",
     "var_mean_96edf0542ecd": "y2",
-    "var_mean_ee167627f636": "y2",
     "var_mean_f4578c128d74": "h_y2",
     "var_mean_b19e82f2a47b": "h_y2x3",
     "var_mean_393456b916a6": "y3_y2x3",

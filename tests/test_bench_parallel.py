@@ -53,7 +53,7 @@ def test_find_and_expand_the_canonical_dirs():
     # three shapes.json points per BASELINE repro (BASELINE size + two
     # ragged); the corpus families carry the reference's points
     assert len(tasks) == (3 * len(REPRO_IDS) + 16 + 1 + 1 + 1 + 2 + 1 + 6 + 2 + 1 + 2
-                          + 13 + 5 + 1 + 16 + 9 + 5 + 5
+                          + 13 + 5 + 16 + 9 + 5 + 5
                           + 1 + 2 + 2 + 2 + 1 + 1 + 1 + 2 + 2 + 1 + 15)
     assert all("::SHAPE::" in t for t in tasks)
     from repro_harness import load_shape_configs
@@ -81,7 +81,7 @@ def test_withdrawn_points_are_no_oracle_for_shape():
                 assert out[label]["status"] == "NO_ORACLE_FOR_SHAPE", out
                 assert "NO_ORACLE_FOR_SHAPE" in _INVALID_STATUSES
                 seen += 1
-    assert seen == 18
+    assert seen == 21
 
 
 def test_find_resolves_relative_dirs(monkeypatch):
