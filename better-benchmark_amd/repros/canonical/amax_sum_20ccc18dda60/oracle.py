@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-38831ee4, oracle 55.83 us, Inductor 120.06 us (ratio 2.15, GOOD); over the dir's 1
-points: 1 GOOD.
+38831ee4, oracle 56.67 us, Inductor 119.26 us (ratio 2.104, GOOD); over the dir's 1
+registered points: 1 GOOD.
 
 MI355X oracle for amax_sum_20ccc18dda60: softmax(scores + bias) with the
 bias [G, 1, Q, K] shared by the heads of each group (TrOCR attention).

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-134a1d74, oracle 255.73 us, Inductor 299.04 us (ratio 1.169, GOOD); over the dir's 3
-points: 2 AT_FLOOR, 1 GOOD.
+134a1d74, oracle 262.65 us, Inductor 296.28 us (ratio 1.128, GOOD); over the dir's 3
+registered points: 2 AT_FLOOR, 1 GOOD.
 
 MI355X oracle for amax_sum_scaled_masked_softmax:
 softmax(scores * 0.125 + mask, -1), bf16 in/out, fp32 max and sum.

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-40057a60, oracle 15.44 us, Inductor 14.56 us (ratio 0.943, NUMERICS_OPTOUT_ACCEPTED);
-over the dir's 1 points: 1 NUMERICS_OPTOUT_ACCEPTED.
+40057a60, oracle 15.28 us, Inductor 14.64 us (ratio 0.958, NUMERICS_OPTOUT_ACCEPTED);
+over the dir's 1 registered points: 1 NUMERICS_OPTOUT_ACCEPTED.
 
 MI355X oracle for mean_4462ce967d63: residual add + T5 RMSNorm (HF op
 order, eps 1e-6) + output scale.

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-40057a60, oracle 15.32 us, Inductor 14.76 us (ratio 0.963, AT_FLOOR); over the dir's 1
-points: 1 AT_FLOOR.
+40057a60, oracle 15.88 us, Inductor 15.76 us (ratio 0.992, AT_FLOOR); over the dir's 1
+registered points: 1 AT_FLOOR.
 
 MI355X oracle for mean_4dace6865eee: residual add + RMSNorm over the last
 dim (eps 1e-06), returning y and 12 views of y.

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-111af936, oracle 15.64 us, Inductor 15.68 us (ratio 1.003, AT_FLOOR); over the dir's 2
-points: 2 AT_FLOOR.
+111af936, oracle 15.68 us, Inductor 15.72 us (ratio 1.003, AT_FLOOR); over the dir's 2
+registered points: 2 AT_FLOOR.
 
 MI355X oracle for mean_db9733790220: residual add + RMSNorm over the last
 dim (eps 1e-06), returning y.

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-533b2091, oracle 15.8 us, Inductor 15.88 us (ratio 1.005, AT_FLOOR); over the dir's 1
-points: 1 AT_FLOOR.
+533b2091, oracle 15.72 us, Inductor 15.8 us (ratio 1.005, AT_FLOOR); over the dir's 1
+registered points: 1 AT_FLOOR.
 
 MI355X oracle for mean_f21cc667fe83: residual add + RMSNorm over the last
 dim (eps 1e-05), returning the bf16 sum h and 1 view of y.

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-8d22dcbf, oracle 75.27 us, Inductor 93.51 us (ratio 1.242, GOOD); over the dir's 3
-points: 2 AT_FLOOR, 1 GOOD.
+8d22dcbf, oracle 76.03 us, Inductor 93.47 us (ratio 1.229, GOOD); over the dir's 3
+registered points: 2 AT_FLOOR, 1 GOOD.
 
 MI355X oracle for pointwise_bias_gelu_tanh_nhwc:
 gelu_tanh(x + bias[None, :, None, None]) written channels-last (bf16).

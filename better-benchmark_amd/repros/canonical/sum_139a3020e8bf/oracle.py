@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-3f451298, oracle 570.0 us, Inductor 761.9 us (ratio 1.337, GOOD); over the dir's 15
-points: 14 GOOD, 1 AT_FLOOR.
+3f451298, oracle 565.65 us, Inductor 762.79 us (ratio 1.349, GOOD); over the dir's 14
+registered points: 14 GOOD; 1 points withdrawn (WITHDRAWN_POINTS).
 
 MI355X oracle for sum_139a3020e8bf: the gradient through an erf GELU, y = bf16(grad *
 GELU'(x)), returned with its transpose view, and its column sum (the bias

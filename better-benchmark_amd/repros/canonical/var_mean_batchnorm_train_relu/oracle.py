@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-ce16d05d, oracle 153.58 us, Inductor 204.41 us (ratio 1.331, GOOD); over the dir's 3
-points: 2 AT_FLOOR, 1 GOOD.
+ce16d05d, oracle 161.3 us, Inductor 205.94 us (ratio 1.277, GOOD); over the dir's 3
+registered points: 2 AT_FLOOR, 1 GOOD.
 
 MI355X oracle for var_mean_batchnorm_train_relu: BatchNorm training forward
 + ReLU, save_mean / save_invstd, running statistics updated in place.
