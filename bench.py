@@ -28,8 +28,9 @@ roofline.flat_copy_us = a non-temporal flat copy (hipo_flat_copy) of the
                     / kernel_us
 configs[].pattern_copy_us = where a flat copy does not share the kernel's
                     access pattern, the copy that does (config 4a: two
-                    streams in, two out), same loop; vs_pattern_copy =
-                    pattern_copy_us / steady_us
+                    streams in, two out; config 5: the single-pass
+                    BatchNorm's register-held slabs without the exchange),
+                    same loop; vs_pattern_copy = pattern_copy_us / steady_us
 cpu_baseline      = the eager repro (ATen) on the host CPU, os.cpu_count()
                     threads, warmup 1 + min of 5 (BASELINE.md's method); the
                     CPU oracle (oracle/hipo_ref.c) time rides along.
@@ -389,7 +390,9 @@ def _steady_callable(fn, sets, steps, label):
 def pattern_copy_steady(rid, cpu_inputs, steps: int = 128):
     """The copy that shares a config's access pattern, where a flat copy does
     not, in the steady-state loop: config 4a, a 2-in / 2-out copy of x and
-    residual's bytes (hipo_flat_copy2).  (name, us) or None."""
+    residual's bytes (hipo_flat_copy2); config 5, x copied with the
+    single-pass BatchNorm kernel's own slabs, rounds and register holding
+    but no exchange (hipo_hold_copy_f32).  (name, us) or None."""
     import torch
     import hip_oracles
     if rid == "var_mean_residual_layernorm":
@@ -402,6 +405,17 @@ def pattern_copy_steady(rid, cpu_inputs, steps: int = 128):
         del bufs
         torch.cuda.empty_cache()
         return "2-in/2-out copy (hipo_flat_copy2)", us
+    if rid == "var_mean_batchnorm_train_relu":
+        x = cpu_inputs[0]
+        nb = x.numel() * x.element_size()
+        sets = max(2, math.ceil((1 << 30) / (2 * nb)))
+        src = [x.to("cuda") for _ in range(sets)]
+        dst = [torch.empty_like(t) for t in src]
+        us = _steady_callable(lambda k: hip_oracles.hold_copy(src[k], out=dst[k]), sets, steps,
+                              "hold_copy")
+        del src, dst
+        torch.cuda.empty_cache()
+        return "hold copy (hipo_hold_copy_f32: the kernel's single-read pattern, no exchange)", us
     return None
 
 

@@ -22,7 +22,7 @@ import torch  # imported before the .so so the process has one HIP runtime
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libhip_oracles.so"
 HEADER_PATH = PKG_DIR.parents[1] / "include" / "hip_oracles.h"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _c_i64 = ctypes.c_int64
 _c_ptr = ctypes.c_void_p
@@ -71,6 +71,7 @@ _SIGNATURES = {
                                                     ctypes.c_int]),
     "hipo_flat_copy": (ctypes.c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
     "hipo_flat_copy2": (ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr]),
+    "hipo_hold_copy_f32": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr]),
     "hipo_gelu_tanh_bf16": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "hipo_gelu_tanh_f32": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "hipo_transpose_last2": (
@@ -567,6 +568,24 @@ def flat_copy2(src0: torch.Tensor, src1: torch.Tensor, dst0: torch.Tensor,
                                    _stream(dev)), "flat_copy2")
 
 
+def hold_copy(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Measurement yardstick: y = x for an fp32 NCHW [N, C, H, W] tensor with
+    the single-pass BatchNorm kernel's access pattern (slabs held in
+    registers from their loads to their stores, no exchange, no arithmetic
+    on the values)."""
+    lib = load_library()
+    dev = _require_rocm(x)
+    _require(x.dtype == torch.float32 and x.dim() == 4 and x.is_contiguous(),
+             "hold_copy: a contiguous fp32 [N, C, H, W] tensor required")
+    y = torch.empty_like(x) if out is None else out
+    _require(y.shape == x.shape and y.dtype == x.dtype and y.is_contiguous(),
+             "hold_copy: out must match x")
+    n, c, h, w = x.shape
+    with torch.cuda.device(dev):
+        _check(lib.hipo_hold_copy_f32(_ptr(x), _ptr(y), n, c, h * w, _stream(dev)), "hold_copy")
+    return y
+
+
 _BN_ACTS = {None: 0, "none": 0, "relu": 1, "silu": 2}
 
 
@@ -709,5 +728,6 @@ __all__ = [
     "batchnorm_cached_workspace", "batchnorm_error_flag", "BN_ERROR_WORD_OFFSET",
     "HipOraclesDeviceFault", "device_faults", "raise_on_device_faults", "flat_copy",
     "flat_copy2",
+    "hold_copy",
     "gelu_erf_bwd_colsum",
 ]

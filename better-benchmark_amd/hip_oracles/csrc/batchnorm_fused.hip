@@ -88,6 +88,7 @@ struct FusedArgs {
   float eps;
   uint32_t spin_limit;
   uint32_t wait_tag_skew;  // 0; 1 only under failure injection (see launch)
+  uint32_t copy;           // 1: the hold-copy yardstick (no exchange, y = x)
 };
 
 __device__ __forceinline__ uint32_t opaque(uint32_t v) {
@@ -325,6 +326,13 @@ __device__ __forceinline__ void finish_channel(float* coef, const FusedArgs& a,
   }
 }
 
+// a.copy (the hold-copy yardstick, hipo_hold_copy_f32; uniform): the same
+// slabs, rounds, register buffers, loads, per-thread statistics (which wait
+// for each round's loads), barriers and stores, with no exchange between
+// workgroups: the exchange wave sets the coefficients to alpha = 1, shift =
+// -0, so the stored fma(x, 1, -0) is x itself (signed zeros included; a
+// signalling NaN comes out quiet).  A runtime flag, not a template
+// parameter, so the data waves run the kernel's own code.
 template <int V, bool FULL, bool RELU>
 __global__ __launch_bounds__(kThreads) void bn_train_fused(
     const f32x4_t* __restrict__ x, f32x4_t* __restrict__ y, FusedArgs a,
@@ -335,7 +343,7 @@ __global__ __launch_bounds__(kThreads) void bn_train_fused(
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
-  if (tid == kDataThreads)
+  if (!a.copy && tid == kDataThreads)
     epoch_s = __hip_atomic_load(a.ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   block_sync();
   const uint32_t epoch = epoch_s;
@@ -347,7 +355,18 @@ __global__ __launch_bounds__(kThreads) void bn_train_fused(
   const int nr = j < g.C ? min(g.rounds, (g.C - j + g.R - 1) / g.R) : 0;
   auto chan = [&](int r) { return r * g.R + j; };
 
-  if (nr > 0 && wave == kDataWaves) {
+  if (a.copy && nr > 0 && wave == kDataWaves) {
+    // ---- the exchange wave's barriers, nothing exchanged
+    if (lane == 0) {
+      coef[0] = 1.0f;
+      coef[1] = -0.0f;
+    }
+    block_sync();
+    for (int r = 0; r < nr; ++r) {
+      block_sync();
+      if (r + 1 < nr) block_sync();
+    }
+  } else if (nr > 0 && wave == kDataWaves) {
     // ---- exchange wave
     ChannelParams cp{0.f, 0.f, 0.f, 0.f};
     if (lane < nr) {
@@ -419,7 +438,7 @@ __global__ __launch_bounds__(kThreads) void bn_train_fused(
 #undef HIPO_BN_ROUND
 #undef HIPO_BN_LAST
   }
-  if (tid == kDataThreads) {
+  if (!a.copy && tid == kDataThreads) {
     // The last workgroup out resets the completion count and opens the next
     // epoch; every workgroup has read this launch's epoch by then.
     const uint32_t done =
@@ -451,17 +470,22 @@ const Variant kVariants[] = {
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
 // Whether one workgroup of each instantiation fits on a CU, per device.
-bool resident(int device, int variant, bool relu) {
+// kind: 0 plain (also the hold copy), 1 ReLU.
+FusedKernel variant_kernel(int variant, int kind) {
+  const Variant& vt = kVariants[variant];
+  return kind == 1 ? vt.relu : vt.plain;
+}
+
+bool resident(int device, int variant, int kind) {
   static std::mutex mu;
-  static std::vector<int8_t> cache;  // [device][variant][relu]: -1 unknown
+  static std::vector<int8_t> cache;  // [device][variant][kind]: -1 unknown
   std::lock_guard<std::mutex> lock(mu);
-  const size_t idx = (static_cast<size_t>(device) * kNumVariants + variant) * 2 + relu;
+  const size_t idx = (static_cast<size_t>(device) * kNumVariants + variant) * 2 + kind;
   if (cache.size() <= idx) cache.resize(idx + 1, -1);
   if (cache[idx] < 0) {
-    const Variant& vt = kVariants[variant];
     int blocks = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &blocks, reinterpret_cast<const void*>(relu ? vt.relu : vt.plain), kThreads, 0);
+        &blocks, reinterpret_cast<const void*>(variant_kernel(variant, kind)), kThreads, 0);
     cache[idx] = (e == hipSuccess && blocks >= 1) ? 1 : 0;
     if (e != hipSuccess) (void)hipGetLastError();
   }
@@ -495,26 +519,26 @@ size_t bn_fused_slot_bytes(int64_t n, int64_t c, int64_t hw) {
   return static_cast<size_t>(c * g * 3) * sizeof(uint64_t);
 }
 
-int bn_fused_launch(const float* x, const float* gamma, const float* beta,
-                    float* running_mean, float* running_var, float* y,
-                    float* save_mean, float* save_invstd, int64_t n, int64_t c,
-                    int64_t hw, float momentum, float eps, int relu,
-                    void* workspace, hipStream_t stream) {
-  if (hw % 4 != 0 || !aligned16(x) || !aligned16(y) || !aligned16(workspace))
-    return -1;
+namespace {
+
+// Slabs, rounds and instantiation of the single-pass geometry for x / y
+// [n, c, hw] fp32; false when the shape or the device falls outside it.
+bool fused_plan(const float* x, const float* y, int64_t n, int64_t c, int64_t hw, int kind,
+                FusedGeom& g, int& variant, int64_t& grid) {
+  if (hw % 4 != 0 || !aligned16(x) || !aligned16(y)) return false;
   const int64_t F = hw / 4;
   const int64_t nf = n * F;
-  if (n * c * hw * 4 >= (int64_t{1} << 32) || nf >= (int64_t{1} << 31)) return -1;
+  if (n * c * hw * 4 >= (int64_t{1} << 32) || nf >= (int64_t{1} << 31)) return false;
   const DeviceInfo* dev = device_info();
-  if (!dev) return -1;
+  if (!dev) return false;
   const int64_t G = bn_fused_groups(n, hw);
-  if (G < 1 || G > 64 || G > dev->cu_count) return -1;
+  if (G < 1 || G > 64 || G > dev->cu_count) return false;
   const int64_t R = std::min<int64_t>(c, dev->cu_count / G);
   const int64_t rounds = (c + R - 1) / R;
-  if (rounds > 64) return -1;
+  if (rounds > 64) return false;
   const int64_t S = (nf + G - 1) / G;
   const int64_t per_thread = (S + kDataThreads - 1) / kDataThreads;
-  int variant = -1;
+  variant = -1;
   if (S == int64_t{kFullV} * kDataThreads && G * S == nf) {
     variant = 0;
   } else {
@@ -525,9 +549,7 @@ int bn_fused_launch(const float* x, const float* gamma, const float* beta,
       }
     }
   }
-  if (variant < 0 || !resident(dev->device, variant, relu != 0)) return -1;
-
-  FusedGeom g;
+  if (variant < 0 || !resident(dev->device, variant, kind)) return false;
   g.C = static_cast<int>(c);
   g.F = static_cast<int>(F);
   g.G = static_cast<int>(G);
@@ -536,6 +558,22 @@ int bn_fused_launch(const float* x, const float* gamma, const float* beta,
   g.NF = static_cast<uint32_t>(nf);
   g.S = static_cast<uint32_t>(S);
   division_magic(static_cast<uint32_t>(F), g.magic, g.shift);
+  grid = R * G;
+  return true;
+}
+
+}  // namespace
+
+int bn_fused_launch(const float* x, const float* gamma, const float* beta,
+                    float* running_mean, float* running_var, float* y,
+                    float* save_mean, float* save_invstd, int64_t n, int64_t c,
+                    int64_t hw, float momentum, float eps, int relu,
+                    void* workspace, hipStream_t stream) {
+  if (!aligned16(workspace)) return -1;
+  FusedGeom g;
+  int variant = -1;
+  int64_t grid = 0;
+  if (!fused_plan(x, y, n, c, hw, relu ? 1 : 0, g, variant, grid)) return -1;
 
   char* ws = static_cast<char*>(workspace);
   FusedArgs a;
@@ -557,13 +595,39 @@ int bn_fused_launch(const float* x, const float* gamma, const float* beta,
   const bool force_timeout = getenv("HIPO_TEST_FORCE_BN_TIMEOUT") != nullptr;
   a.spin_limit = force_timeout ? 8u : kSpinLimit;
   a.wait_tag_skew = force_timeout ? 1u : 0u;
+  a.copy = 0;
 
-  const Variant& vt = kVariants[variant];
-  const FusedKernel kernel = relu ? vt.relu : vt.plain;
-  const dim3 grid(static_cast<unsigned>(R * G));
-  kernel<<<grid, dim3(kThreads), 0, stream>>>(
+  const FusedKernel kernel = variant_kernel(variant, relu ? 1 : 0);
+  kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream>>>(
       reinterpret_cast<const f32x4_t*>(x), reinterpret_cast<f32x4_t*>(y), a, g);
   return check_launch("batchnorm_train_fwd_f32 (single pass)");
 }
 
+int bn_hold_copy_launch(const float* x, float* y, int64_t n, int64_t c, int64_t hw,
+                        hipStream_t stream) {
+  FusedGeom g;
+  int variant = -1;
+  int64_t grid = 0;
+  if (!fused_plan(x, y, n, c, hw, 0, g, variant, grid)) return -1;
+  FusedArgs a{};  // the copy reads no parameters and exchanges nothing
+  a.copy = 1;
+  variant_kernel(variant, 0)<<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream>>>(
+      reinterpret_cast<const f32x4_t*>(x), reinterpret_cast<f32x4_t*>(y), a, g);
+  return check_launch("hold_copy_f32");
+}
+
 }  // namespace hipo
+
+extern "C" int hipo_hold_copy_f32(const float* x, float* y, int64_t n, int64_t c, int64_t hw,
+                                  hipStream_t stream) {
+  using namespace hipo;
+  clear_error();
+  HIPO_REQUIRE(n > 0 && c > 0 && hw > 0, "hold_copy: sizes must be positive");
+  HIPO_REQUIRE(x && y, "hold_copy: null pointer");
+  const int rc = bn_hold_copy_launch(x, y, n, c, hw, stream);
+  HIPO_REQUIRE(rc >= 0,
+               "hold_copy: [%lld, %lld, %lld] is outside the single-pass BatchNorm geometry "
+               "(H*W a multiple of 4, 16-byte aligned, at most 64 slabs and 64 rounds)",
+               (long long)n, (long long)c, (long long)hw);
+  return rc;
+}

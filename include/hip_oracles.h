@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define HIPO_ABI_VERSION 3
+#define HIPO_ABI_VERSION 4
 #define HIPO_EINVAL 1000
 
 /* ABI version of the loaded library (HIPO_ABI_VERSION at build time). */
@@ -348,6 +348,21 @@ int hipo_flat_copy(const void* src, int64_t read_bytes, void* dst,
  */
 int hipo_flat_copy2(const void* src0, const void* src1, void* dst0, void* dst1,
                     int64_t bytes, hipStream_t stream);
+
+/*
+ * Yardstick for the single-pass BatchNorm (hipo_batchnorm_train_fwd_f32's
+ * fused kernel): y = x for fp32 [n, c, hw] NCHW, with that kernel's exact
+ * access pattern -- the same slabs and rounds, each workgroup holding its
+ * slab in registers from its loads to its stores, the same per-thread
+ * statistics (they wait for each round's loads) and barriers -- but no
+ * exchange between workgroups and no normalisation.  Its time is the
+ * ceiling of that pattern.  Applies where the fused kernel does (hw a
+ * multiple of 4, x and y 16-byte aligned, at most 64 slabs per channel and
+ * 64 rounds); other shapes are rejected.  No counterpart in the reference;
+ * used only to price a kernel's access pattern.
+ */
+int hipo_hold_copy_f32(const float* x, float* y, int64_t n, int64_t c, int64_t hw,
+                       hipStream_t stream);
 
 
 /*

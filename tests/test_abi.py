@@ -33,7 +33,7 @@ def test_exported_names_match_header():
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.hipo_abi_version() == hip_oracles.ABI_VERSION == 3
+    assert lib.hipo_abi_version() == hip_oracles.ABI_VERSION == 4
     assert lib.hipo_last_error() == b""
 
 
@@ -162,6 +162,21 @@ def test_yardstick_argument_checks(lib):
     q = ctypes.c_void_p(base + 4)
     assert lib.hipo_flat_copy2(p, q, p, p, 1024, None) != 0
     assert "aligned" in lib.hipo_last_error().decode()
+
+
+def test_hold_copy_argument_checks(lib):
+    """The BatchNorm hold-copy yardstick rejects, on the host, sizes that are
+    not positive, null pointers and shapes outside the single-pass geometry
+    (H*W not a multiple of 4) before any device call."""
+    import ctypes
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = ctypes.c_void_p((ctypes.addressof(buf) + 15) // 16 * 16)
+    assert lib.hipo_hold_copy_f32(p, p, 0, 4, 4, None) != 0
+    assert "positive" in lib.hipo_last_error().decode()
+    assert lib.hipo_hold_copy_f32(None, p, 2, 4, 4, None) != 0
+    assert "null" in lib.hipo_last_error().decode()
+    assert lib.hipo_hold_copy_f32(p, p, 2, 4, 49, None) != 0
+    assert "geometry" in lib.hipo_last_error().decode()
 
 
 def test_gelu_bwd_workspace_bytes(lib):

@@ -1545,3 +1545,27 @@ def test_yardstick_copies_are_copies(rocm_device):
     torch.cuda.synchronize()
     for s_, d_ in zip(srcs, dsts):
         assert torch.equal(s_.view(torch.int16), d_.view(torch.int16))
+
+
+def test_hold_copy_is_a_copy(rocm_device):
+    """hipo_hold_copy_f32 (the single-pass BatchNorm kernel's pattern without
+    its exchange) returns x bit for bit -- signed zeros and infinities
+    included, NaN as NaN -- with exact 28-float4 slabs (config 5's shape),
+    masked slabs over several rounds, and a channel count that leaves the
+    last round short."""
+    import hip_oracles
+    for shape in [(128, 256, 56, 56), (100, 200, 30, 30), (16, 300, 28, 28)]:
+        print(f"[hold_copy] {shape}", flush=True)
+        g = torch.Generator().manual_seed(sum(shape))
+        x = torch.randn(*shape, generator=g)
+        flat = x.view(-1)
+        flat[:: 1 << 16] = -0.0
+        flat[7:: 1 << 17] = float("inf")
+        flat[11:: 1 << 17] = float("-inf")
+        flat[13:: 1 << 18] = float("nan")
+        xd = x.to(rocm_device)
+        y = hip_oracles.hold_copy(xd).cpu()
+        nan = torch.isnan(x)
+        assert torch.equal(torch.isnan(y), nan), shape
+        assert torch.equal(y.view(torch.int32)[~nan], x.view(torch.int32)[~nan]), shape
+        del xd, y
