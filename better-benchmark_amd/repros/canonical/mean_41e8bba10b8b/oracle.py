@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-841ed042, oracle 13.68 us, Inductor 13.96 us (ratio 1.02, AT_FLOOR); over the dir's 1
+841ed042, oracle 14.04 us, Inductor 14.24 us (ratio 1.014, AT_FLOOR); over the dir's 1
 registered points: 1 AT_FLOOR.
 
 MI355X oracle for mean_41e8bba10b8b: residual add + RMSNorm over the last

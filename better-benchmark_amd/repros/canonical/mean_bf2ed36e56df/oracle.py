@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-40057a60, oracle 17.0 us, Inductor 16.68 us (ratio 0.981, AT_FLOOR); over the dir's 2
+40057a60, oracle 16.96 us, Inductor 17.16 us (ratio 1.012, AT_FLOOR); over the dir's 2
 registered points: 2 AT_FLOOR.
 
 MI355X oracle for mean_bf2ed36e56df: residual add + RMSNorm over the last

@@ -42,3 +42,23 @@ def test_bench_json_line_contract():
     cb = line["cpu_baseline"]
     assert cb["kind"] in ("port", "reference") and cb["cores"] >= 1 and cb["value"] > 0
     assert cb["unit"] == "GB/s" and cb["sample"]
+
+
+@pytest.mark.gpu
+def test_pattern_copies_of_configs_4a_and_5():
+    """The per-config pattern yardsticks: config 4a's two-in/two-out copy and
+    config 5's hold copy time positive, the other configs have none."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+    from conftest import CANONICAL
+    from repro_harness import load_shape_configs, make_inputs_from_config
+    for rid in ("var_mean_residual_layernorm", "var_mean_batchnorm_train_relu", "mean_rmsnorm"):
+        print(f"[pattern] {rid}", flush=True)
+        cfg = next(iter(load_shape_configs(str(CANONICAL / rid / "repro.py")).values()))
+        cpu_inputs = make_inputs_from_config(cfg, device="cpu")
+        got = bench.pattern_copy_steady(rid, cpu_inputs, steps=8)
+        if rid == "mean_rmsnorm":
+            assert got is None
+        else:
+            name, us = got
+            assert name and us > 0, got
