@@ -12,36 +12,18 @@ Kernel: hipo_spatial_mean_nhwc_bf16 -- per image a column reduction of the
 [H*W, C] block: each workgroup instruction reads whole contiguous rows, every
 thread keeps fp32 sums for one 8-channel group, partial sums meet in LDS in a
 fixed order (and, when positions are split for parallelism, a second pass
-adds the slices in order).  Algorithmic bytes: 2 N H W C + 2 N C.
+adds the slices in order); images of at most 192 positions take one wave per
+(image, 64-channel block) with every position in flight at once and an
+xor-shuffle combine (no LDS).  Algorithmic bytes: 2 N H W C + 2 N C.
 Replaces the Triton body of the reference's
 repros/canonical/mean_c9e1a8113328/oracle.py:95 (_spatial_mean_cl_kernel, :11).
 """
 import hip_oracles
 from oracle_harness import oracle_impl, oracle_main
 
-_POINTS = ("280fa7d2", "2645a53e", "4ca56f88", "547c8164",
-           "f0a667e3", "4784273d", "3cf84b69", "2150fa2c", "d3381898", "473b7062",
-           "630d0797")
-
-# Points of shapes.json with no MI355X registration: the 6x6, 7x7, 8x8, 9x9
-# and 12x12 images of 1536 channels.  Back to back, Inductor's reduction is
-# faster (6x6: 4.76 against 5.50 us, 7x7: 5.73 against 6.36 us, 9x9: 7.08
-# against 8.05 us) or equal (8x8: 6.49 against 6.54 us); 16-, 32- and
-# 64-group channel blocks, one round of loads and wave-shuffle combines
-# reached 5.20, 5.83, 6.48 and 8.10 us at best; single launches measured
-# BAD_ORACLE at each of them at least once (12x12: 0.939 in the last of five
-# status sweeps, 0.954-0.987 before).  There is no shape-general
-# registration, so these points find no MI355X oracle (NO_ORACLE_FOR_SHAPE);
-# the kernel still computes them and the parity tests call it directly.
-# Values: the lowest single-launch ratio compile_us / oracle_us, then the
-# back-to-back ratio where measured.
-WITHDRAWN_POINTS = {
-    "d1686c77": (0.906, 0.865),
-    "6b68d184": (0.915, 0.901),
-    "69db7514": (0.941, 0.992),
-    "44f1e75f": (0.900, 0.879),
-    "333b11d0": (0.939,),
-}
+_POINTS = ("69db7514", "280fa7d2", "2645a53e", "4ca56f88", "d1686c77", "333b11d0",
+           "547c8164", "f0a667e3", "44f1e75f", "4784273d", "3cf84b69", "2150fa2c",
+           "6b68d184", "d3381898", "473b7062", "630d0797")
 
 
 def oracle_forward(inputs):
@@ -52,6 +34,8 @@ def oracle_forward(inputs):
 for _point in _POINTS:
     oracle_forward = oracle_impl(hardware="MI355X", point=_point,
                                  description="channels-last spatial mean")(oracle_forward)
+oracle_forward = oracle_impl(hardware="MI355X",
+                             description="channels-last spatial mean, shape-general")(oracle_forward)
 
 
 if __name__ == "__main__":

@@ -1023,14 +1023,17 @@ def test_masked_softmax_broadcast_mask_rows(rocm_device):
 
 def test_spatial_mean_layouts(rocm_device):
     """Vector path (one slice and several; channel blocks of 64 groups when
-    images x blocks fill the chip), C not a multiple of 8 and C / 8 above
-    1024 (scalar kernel), one position, non-power-of-two group counts,
-    keepdim off."""
+    images x blocks fill the chip), the small-image kernel (one wave per
+    image and 64-channel block, 1 to 24 positions per lane), C not a
+    multiple of 8 and C / 8 above 1024 (scalar kernel), one position,
+    non-power-of-two group counts, keepdim off."""
     import hip_oracles
     bf = torch.bfloat16
     for n, c, h, w in [(2, 96, 7, 7), (1, 240, 33, 33), (3, 20, 5, 5), (1, 8, 1, 1),
                        (1, 8192, 2, 2), (2, 8200, 3, 3), (4, 1536, 6, 6), (1, 256, 72, 72),
-                       (256, 64, 2, 3), (1, 24, 300, 7), (128, 1024, 5, 5), (100, 1536, 7, 7)]:
+                       (256, 64, 2, 3), (1, 24, 300, 7), (128, 1024, 5, 5), (100, 1536, 7, 7),
+                       (128, 1536, 6, 6), (64, 512, 12, 12), (32, 1024, 16, 12), (600, 64, 1, 1),
+                       (512, 128, 3, 3), (1024, 64, 9, 10)]:
         what = f"spatial_mean n={n} c={c} {h}x{w}"
         print(f"[edges] {what}", flush=True)
         g = torch.Generator().manual_seed(n * c + h * w)
