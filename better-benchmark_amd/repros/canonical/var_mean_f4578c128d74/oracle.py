@@ -33,7 +33,11 @@ EPS = 1e-06
 # the reference's state of a point without one); the kernel still computes
 # them and the parity tests call it directly.  Values: the measured ratios
 # compile_us / oracle_us.
+# [131072, 144] (rows of 144 values, no row-class relation to the above):
+# the oracle held 36.7-37.1 us in seven sweeps while Inductor's re-tuned
+# kernel took 34.6-38.2 us; its fastest beats the oracle's fastest by 5.8 %.
 WITHDRAWN_POINTS = {
+    "d8c968d2": (1.017, 1.019, 1.03, 1.014, 1.013, 0.997, 0.938),
     "155170ab": (0.956, 0.989, 0.977, 0.961),
     "9801ab6a": (0.927, 0.959),
     "63bebcf6": (0.980, 0.993, 0.993, 0.981),
@@ -47,8 +51,6 @@ WITHDRAWN_POINTS = {
              description="residual LayerNorm, 8192 x 240")
 @oracle_impl(hardware="MI355X", point="f049abfe",
              description="residual LayerNorm, 32768 x 192")
-@oracle_impl(hardware="MI355X", point="d8c968d2",
-             description="residual LayerNorm, 131072 x 144")
 @oracle_impl(hardware="MI355X", point="c4bf51cc",
              description="residual LayerNorm, 4096 x 2560")
 @oracle_impl(hardware="MI355X", point="7f824027",

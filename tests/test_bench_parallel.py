@@ -81,7 +81,7 @@ def test_withdrawn_points_are_no_oracle_for_shape():
                 assert out[label]["status"] == "NO_ORACLE_FOR_SHAPE", out
                 assert "NO_ORACLE_FOR_SHAPE" in _INVALID_STATUSES
                 seen += 1
-    assert seen == 17
+    assert seen == 18
 
 
 def test_find_resolves_relative_dirs(monkeypatch):
