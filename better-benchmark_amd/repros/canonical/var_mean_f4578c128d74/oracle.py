@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-d8c968d2, oracle 37.08 us, Inductor 36.95 us (ratio 0.997, AT_FLOOR); over the dir's 12
-registered points: 10 AT_FLOOR, 2 GOOD; 4 points withdrawn (WITHDRAWN_POINTS).
+c4bf51cc, oracle 28.0 us, Inductor 29.04 us (ratio 1.037, AT_FLOOR); over the dir's 11
+registered points: 9 AT_FLOOR, 2 GOOD; 5 points withdrawn (WITHDRAWN_POINTS).
 
 MI355X oracle for var_mean_f4578c128d74: residual add + LayerNorm over the
 last dim (eps 1e-06), returning the bf16 sum h and y.
