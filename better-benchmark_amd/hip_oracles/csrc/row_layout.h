@@ -186,7 +186,8 @@ struct RowPlan {
 
 inline bool row_plan(int64_t cols, RowPlan& plan) {
   // About 2 groups (2 KiB) per wave of each streamed tensor, 8 waves per
-  // workgroup.  (One group per wave for the two streams of LayerNorm was
+  // workgroup.  (RMSNorm at [16384, 4096], back to back: 4 waves per row x
+  // 2 groups 45.2-45.4 us, 2 x 4 46.9-47.3, 1 x 8 50.0-50.2.)  (One group per wave for the two streams of LayerNorm was
   // faster with outputs reused across launches, slower in the steady loop
   // where every step writes fresh output buffers: 91.7-92.3 against
   // 89.7-89.9 us at [16384, 4096].)

@@ -566,7 +566,9 @@ void launch_seg_plan(const SegPlan& sp, int64_t rows, hipStream_t stream, const 
 // Shape of residual_layernorm_k at 4096 columns: waves per row, row slots
 // per workgroup, rows per slot, gamma / beta staged in LDS.  Rows per slot,
 // measured at [16384, 4096], one process: 1 row 90.2-90.8 us, 2 rows 93.4
-// us, 4 rows 100.6-102.8 us.
+// us, 4 rows 100.6-102.8 us.  Waves per row x slots, back to back (flat
+// copy 83.1-83.4 us): 2 x 2 89.4-90.1 us, 2 x 4 89.4-89.5, 4 x 1 90.8-90.9,
+// 1 x 2 94.5, 1 x 4 94.0 (94.5 with gamma / beta from the cache).
 constexpr int kLnWaves = 2;
 constexpr int kLnSlots = 2;
 constexpr int kLayerNormRowsPerWave = 1;
