@@ -34,22 +34,86 @@ constexpr int kMaxThreads = 1024;
 
 enum { kActNone = 0, kActRelu = 1, kActSilu = 2 };
 
-// act(bf16(((x - mean) * rstd) * gamma + beta)), fp32 ops in the eager order
-// (no contraction).  SiLU is t / (1 + exp(-t)) as eager, with the
-// extended-precision exp_f32 and an IEEE division; callers round the result
-// to bf16 (eager's activation output) before storing or summing it.  (A
-// correctly rounded bf16 SiLU table staged in LDS, like the GELU kernels',
-// measured 2-5 % slower in the channels-last epilogue.)
+// SiLU(t) = t / (1 + e^-t) of a bf16 value t, in fp32; callers round it to
+// bf16.  That rounding gives the correctly rounded SiLU of every bf16 t,
+// and -0 where e^-t overflows fp32 (t < -88.72), as eager's expf does.
+//
+// Common inputs (t > -87): t * rcp(1 + 2^(t * -log2 e)), with the hardware
+// exp2 (v_exp_f32) and reciprocal (v_rcp_f32) -- 3 VALU and 2 transcendental
+// instructions where the accurate form below takes ~18.  Over all bf16
+// t > -87 this rounds to the correctly rounded SiLU except at t = 5.9375,
+// whose exact SiLU lies 1.18 fp32 ulps below the bf16 midpoint 5.921875 and
+// which one select patches (to 5.90625).  The GPU tests run all 65536 bf16
+// inputs through the kernels and compare bit for bit with mpmath; the GPU's
+// exp2 and rcp are deterministic and the domain is finite, so that is the
+// proof.  At -88.5 <= t <= -87.5 the reciprocal's result is an fp32
+// denormal, which the hardware reciprocal flushes to zero.
+//
+// Rare inputs (t <= -87, NaN): the accurate form, the extended-precision
+// exp_f32 and an IEEE division, correctly rounded there too.
+constexpr float kSiluNegLog2e = -1.4426950408889634f;
+constexpr float kSiluFastMin = -87.0f;
+
+__device__ __forceinline__ float silu_fast(float t) {
+  const float y = t * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(t * kSiluNegLog2e));
+  return t == 5.9375f ? 5.90625f : y;
+}
+
+__device__ __forceinline__ float silu_accurate(float t) {
+  return t / (1.f + exp_f32(exp_domain(-t)));
+}
+
+__device__ __forceinline__ float silu_of_bf16(float t) {
+  return __builtin_expect(t > kSiluFastMin, 1) ? silu_fast(t) : silu_accurate(t);
+}
+
+// bf16(((x - mean) * rstd) * gamma + beta), fp32 ops in the eager order (no
+// contraction): the activation's input.
+__device__ __forceinline__ float bn_affine(float x, float mean, float rstd, float g, float b) {
+  const float y = __fmul_rn(__fsub_rn(x, mean), rstd);
+  return round_bf16(__fadd_rn(__fmul_rn(y, g), b));
+}
+
+// act(bn_affine(...)); callers round the result to bf16 (eager's activation
+// output) before storing or summing it.  (A correctly rounded bf16 SiLU
+// table staged in LDS, like the GELU kernels', measured 2-5 % slower in the
+// channels-last epilogue than the accurate form silu_of_bf16 uses for rare
+// inputs.)
 __device__ __forceinline__ float bn_act(float x, float mean, float rstd, float g, float b,
                                         int act) {
-  float y = __fmul_rn(__fsub_rn(x, mean), rstd);
-  y = round_bf16(__fadd_rn(__fmul_rn(y, g), b));
+  float y = bn_affine(x, mean, rstd, g, b);
   if (act == kActRelu) {
     y = y < 0.f ? 0.f : y;
   } else if (act == kActSilu) {
-    y = y / (1.f + exp_f32(exp_domain(-y)));
+    y = silu_of_bf16(y);
   }
   return y;
+}
+
+// The activation of 8 values with the activation known at compile time, so
+// the 8 evaluations interleave: SiLU takes the fast form for all 8 and
+// redoes them with silu_of_bf16 only when one of them is rare (t <= -87 or
+// NaN; the comparison is false for NaN).
+template <int ACT>
+__device__ __forceinline__ void bn_act_x8(float (&y)[8]) {
+  if constexpr (ACT == kActRelu) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = y[e] < 0.f ? 0.f : y[e];
+  } else if constexpr (ACT == kActSilu) {
+    float s[8];
+    bool rare = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s[e] = silu_fast(y[e]);
+      rare |= !(y[e] > kSiluFastMin);
+    }
+    if (__builtin_expect(rare, 0)) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s[e] = silu_of_bf16(y[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = s[e];
+  }
 }
 
 // Chan's pairwise merge of (count, mean, M2) partials: (n, mean, m2) <-
@@ -164,11 +228,12 @@ __global__ __launch_bounds__(kMaxThreads) void bn_nhwc_partial(
 // normalised, activated x row (n, ho, wo) when ho < H and wo < W, else zeros.
 // Workgroup b writes rows [b*R*kApplyUnroll, (b+1)*R*kApplyUnroll).
 constexpr int kApplyUnroll = 4;
+template <int ACT>
 __global__ __launch_bounds__(kMaxThreads) void bn_nhwc_apply_pad(
     const uint16_t* __restrict__ x, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
     const float* __restrict__ beta, uint16_t* __restrict__ out, uint32_t rows_out, uint32_t H,
-    uint32_t W, uint32_t Ho, uint32_t Wo, DivMagic image_div, DivMagic row_div, int G, int act) {
+    uint32_t W, uint32_t Ho, uint32_t Wo, DivMagic image_div, DivMagic row_div, int G) {
   const int T = blockDim.x;
   const int t = threadIdx.x;
   const int g = t % G;
@@ -206,15 +271,13 @@ __global__ __launch_bounds__(kMaxThreads) void bn_nhwc_apply_pad(
     if (o >= rows_out) continue;
     float f[8];
     unpack8(v[u], f);
+    // Padding: act(0) = 0 for every activation, so the select goes first.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = inside[u] ? bn_affine(f[e], m[e], rs[e], ga[e], be[e]) : 0.f;
+    bn_act_x8<ACT>(f);
     u32x4_t w;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const float a = inside[u] ? bn_act(f[2 * d], m[2 * d], rs[2 * d], ga[2 * d], be[2 * d], act) : 0.f;
-      const float b = inside[u] ? bn_act(f[2 * d + 1], m[2 * d + 1], rs[2 * d + 1], ga[2 * d + 1],
-                                         be[2 * d + 1], act)
-                                : 0.f;
-      w[d] = pack_bf16x2(a, b);
-    }
+    for (int d = 0; d < 4; ++d) w[d] = pack_bf16x2(f[2 * d], f[2 * d + 1]);
     __builtin_nontemporal_store(w, ov + static_cast<int64_t>(o) * G64);
   }
 }
@@ -727,11 +790,14 @@ extern "C" int hipo_batchnorm_nhwc_act_pad_bf16(
     const int G = static_cast<int>(c / 8);
     const int64_t rows_per_block = static_cast<int64_t>(plan.threads / G) * kApplyUnroll;
     const int64_t blocks = (rows_out + rows_per_block - 1) / rows_per_block;
-    bn_nhwc_apply_pad<<<dim3(static_cast<unsigned>(blocks)), dim3(plan.threads), 0, stream>>>(
+    auto kernel = act == kActSilu   ? bn_nhwc_apply_pad<kActSilu>
+                  : act == kActRelu ? bn_nhwc_apply_pad<kActRelu>
+                                    : bn_nhwc_apply_pad<kActNone>;
+    kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(plan.threads), 0, stream>>>(
         x, save_mean, save_rstd, gamma, beta, out, static_cast<uint32_t>(rows_out),
         static_cast<uint32_t>(h), static_cast<uint32_t>(w), static_cast<uint32_t>(Ho),
         static_cast<uint32_t>(Wo), div_magic(static_cast<uint32_t>(Ho * Wo)),
-        div_magic(static_cast<uint32_t>(Wo)), G, act);
+        div_magic(static_cast<uint32_t>(Wo)), G);
   } else {
     const int64_t total = rows_out * c;
     HIPO_REQUIRE((total + 255) / 256 <= 0x7fffffff, "%s: too large", what);

@@ -1159,6 +1159,86 @@ def test_batchnorm_bf16_closed_forms(rocm_device):
         assert_close(d[3], torch.full((c,), 0.9), F32_TOL, layout + " running_var")
 
 
+def _exact_silu_bf16_bits():
+    """The correctly rounded bf16 SiLU(t) = t / (1 + e^-t) of every bf16 bit
+    pattern t, by mpmath at 96 bits, as a list of result bits (None for NaN
+    results); -0 where e^-t overflows fp32 (t < -ln(FLT_MAX)), as eager's
+    expf makes it."""
+    from conftest import PKG
+    spec = importlib.util.spec_from_file_location(
+        "gen_gelu_table", PKG / "hip_oracles" / "gen_gelu_table.py")
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    mp = gen.mpmath
+    overflow = -mp.log(mp.ldexp(mp.mpf(2) ** 24 - 1, 104))  # -ln(FLT_MAX)
+    want = []
+    for tb in range(65536):
+        mag = tb & 0x7FFF
+        if mag > 0x7F80 or tb == 0xFF80:   # NaN in, or -inf * 0
+            want.append(None)
+        elif tb == 0x7F80:
+            want.append(0x7F80)
+        elif mag == 0:
+            want.append(tb)
+        else:
+            t = gen.bf16_value(tb)
+            want.append(0x8000 if t < overflow else gen.to_bf16(t / (1 + mp.exp(-t))))
+    return want
+
+
+def test_batchnorm_silu_every_bf16_input(rocm_device):
+    """Bit for bit, over all 65536 bf16 t: the BatchNorm kernels' SiLU is
+    the correctly rounded SiLU (mpmath), through the channels-last vector
+    and scalar epilogues and both NCHW act+mean kernels.  One element per
+    channel (n = h = w = 1) makes the normalised value 0, so the activation
+    input is bf16(0 * gamma + beta) = beta exactly (-0 becomes +0): beta
+    carries the 65536 patterns.  The kernels evaluate t > -87 with the
+    hardware exp2 and reciprocal, so this comparison over the whole domain
+    is what proves that evaluation correctly rounded."""
+    import hip_oracles
+    pytest.importorskip("mpmath")
+    want = _exact_silu_bf16_bits()
+    ts = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+
+    def run(layout, lo, c):
+        beta = ts[lo:lo + c].contiguous()
+        x = torch.zeros(1, c, 1, 1, dtype=torch.bfloat16)
+        if layout == "nhwc":
+            x = x.contiguous(memory_format=torch.channels_last)
+        d = [t.to(rocm_device) for t in (x, torch.ones(c), beta, torch.zeros(c), torch.ones(c))]
+        if layout == "nhwc":
+            _, _, out = hip_oracles.batchnorm_nhwc_act_pad(
+                *d, momentum=0.1, eps=1e-3, var_scale=1.0, act="silu", pad_bottom=0, pad_right=0)
+        else:
+            _, _, out = hip_oracles.batchnorm_nchw_act_mean(
+                *d, momentum=0.1, eps=1e-3, var_scale=1.0, act="silu")
+        return out.cpu().reshape(-1).view(torch.int16).tolist()
+
+    # (layout, what, channel chunk): 8192 channels take the channels-last
+    # vector path, 65536 its scalar path; 65536 the NCHW planes kernel,
+    # 65533 + 3 (not a multiple of 8) its small-hw kernel.
+    plans = (("nhwc", "vector", [8192] * 8), ("nhwc", "scalar", [65536]),
+             ("nchw", "planes", [65536]), ("nchw", "small_hw", [65533, 3]))
+    for layout, what, chunks in plans:
+        print(f"[bn-silu] every bf16 input, {layout} {what}", flush=True)
+        got, lo = [], 0
+        for c in chunks:
+            got += run(layout, lo, c)
+            lo += c
+        bad = []
+        for tb, gv in enumerate(got):
+            w = want[0 if tb == 0x8000 else tb]
+            gv &= 0xFFFF
+            if layout == "nchw" and w == 0x8000:
+                w = 0   # a mean of -0 starts from +0
+            if w is None:
+                if not (gv & 0x7F80 == 0x7F80 and gv & 0x7F):
+                    bad.append((hex(tb), hex(gv), "NaN"))
+            elif gv != w:
+                bad.append((hex(tb), hex(gv), hex(w)))
+        assert not bad, f"{layout} {what}: {len(bad)} inputs differ, first {bad[:8]}"
+
+
 def test_batchnorm_closed_forms_and_edges(rocm_device):
     import hip_oracles
     import oracle as ref
