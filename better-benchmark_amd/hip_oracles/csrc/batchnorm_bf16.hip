@@ -140,7 +140,11 @@ __device__ __forceinline__ void unpack8(const u32x4_t v, float (&f)[8]) {
 // ---------------------------------------------------------------------------
 // Channels-last: x is [M, C] rows (M = N*H*W), G = C / 8 groups of 16 bytes.
 // A workgroup of T threads (T a multiple of G) covers T / G whole rows per
-// access instruction; thread t owns group t % G.
+// access instruction; thread t owns group t % G.  x is read twice (the
+// statistics pass, then the epilogue) with ordinary cached loads, and the
+// epilogue walks the rows in reverse: it starts on the rows the statistics
+// pass read last, the likeliest to be still in the 256 MB Infinity Cache
+// (all of x when it fits there).
 // ---------------------------------------------------------------------------
 
 // Workgroup s reduces rows [s*L, min(M, (s+1)*L)): sums of (x - shift) and
@@ -176,7 +180,7 @@ __global__ __launch_bounds__(kMaxThreads) void bn_nhwc_partial(
       // Rows past the slice re-read its first row and count as the shift
       // (a zero deviation).
       const int64_t pu = p + static_cast<int64_t>(u) * R;
-      v[u] = __builtin_nontemporal_load(xv + (pu < p1 ? pu : p0) * G64);
+      v[u] = xv[(pu < p1 ? pu : p0) * G64];
       if (pu >= p1) v[u] = shv;
     }
 #pragma unroll
@@ -226,7 +230,8 @@ __global__ __launch_bounds__(kMaxThreads) void bn_nhwc_partial(
 
 // Output row o = (n, ho, wo) of the padded [N, Ho, Wo, C] tensor: the
 // normalised, activated x row (n, ho, wo) when ho < H and wo < W, else zeros.
-// Workgroup b writes rows [b*R*kApplyUnroll, (b+1)*R*kApplyUnroll).
+// Workgroup b writes rows [b'*R*kApplyUnroll, (b'+1)*R*kApplyUnroll),
+// b' = gridDim.x - 1 - b (reverse order, see above).
 constexpr int kApplyUnroll = 4;
 template <int ACT>
 __global__ __launch_bounds__(kMaxThreads) void bn_nhwc_apply_pad(
@@ -249,7 +254,7 @@ __global__ __launch_bounds__(kMaxThreads) void bn_nhwc_apply_pad(
   }
   const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x) + g;
   u32x4_t* ov = reinterpret_cast<u32x4_t*>(out) + g;
-  const uint32_t o0 = blockIdx.x * static_cast<uint32_t>(R * kApplyUnroll) + r;
+  const uint32_t o0 = (gridDim.x - 1 - blockIdx.x) * static_cast<uint32_t>(R * kApplyUnroll) + r;
   const int64_t G64 = G;
   u32x4_t v[kApplyUnroll];
   bool inside[kApplyUnroll];
@@ -263,7 +268,7 @@ __global__ __launch_bounds__(kMaxThreads) void bn_nhwc_apply_pad(
     inside[u] = o < rows_out && ho < H && wo < W;
     // Padding and rows past the end read row 0 (in bounds) and store zeros.
     const int64_t src = inside[u] ? (static_cast<int64_t>(img) * H + ho) * W + wo : 0;
-    v[u] = __builtin_nontemporal_load(xv + src * G64);
+    v[u] = xv[src * G64];
   }
 #pragma unroll
   for (int u = 0; u < kApplyUnroll; ++u) {
@@ -708,7 +713,12 @@ int64_t gcd64(int64_t a, int64_t b) {
 // or cached loads: 21-27 / 55-64 us.  Whole call (three launches, graph
 // loop): 44.0 / 160.2 us as planned; 128- or 64-row slices with up to 1024
 // or 2048 of them 71-100 / 167-184 us; 2 or 1 rows per thread in the
-// epilogue instead of kApplyUnroll = 4: 44.1-51.2 / 168.6-203.5 us.
+// epilogue instead of kApplyUnroll = 4: 44.1-51.2 / 168.6-203.5 us.  With
+// the SiLU fast form, one call after a 1 GiB cache flush (the runner's
+// protocol), [128, 240, 28, 28] / [128, 96, 112, 112]: 47.2 / 161-163 us
+// with 960-thread workgroups and non-temporal loads; 42.5 / 162.5 with 480
+// threads (G * R above); 38.4 / 161.5 with 480 threads, cached loads and
+// the reversed epilogue (shipped); 256-row slices on top: 40.7 / 162.6.
 struct NhwcPlan {
   int threads = 0;
   int64_t slice_len = 0;
@@ -724,7 +734,16 @@ NhwcPlan nhwc_plan(int64_t M, int64_t C, bool vec_ok) {
   if (vec_ok && C % 8 == 0 && C / 8 <= kMaxThreads) {
     const int64_t G = C / 8;
     const int64_t lcm = G / gcd64(G, kWave) * kWave;
-    plan.threads = static_cast<int>(lcm <= kMaxThreads ? lcm * std::max<int64_t>(1, 512 / lcm) : G);
+    if (lcm <= 512) {
+      plan.threads = static_cast<int>(lcm * (512 / lcm));
+    } else {
+      // Whole waves would take lcm threads (960 for C = 240): one such
+      // workgroup per CU at the kernels' register use.  G * R threads with
+      // a partial last wave fit two or three per CU instead.
+      int64_t R = 1;
+      while (G * R * 2 <= 512) R *= 2;
+      plan.threads = static_cast<int>(G * R);
+    }
   }
   const int64_t want = (M + kNhwcMaxSlices - 1) / kNhwcMaxSlices;
   plan.slice_len = (want + kNhwcSliceStep - 1) / kNhwcSliceStep * kNhwcSliceStep;

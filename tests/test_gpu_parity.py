@@ -1081,6 +1081,8 @@ BN_NHWC_CASES = [  # n, c, h, w, pad_bottom, pad_right, act
     (3, 240, 28, 28, 1, 1, "silu"), (2, 96, 9, 9, 0, 0, "relu"), (1, 8, 3, 3, 2, 3, None),
     (2, 20, 5, 5, 1, 1, "silu"), (4, 8192, 2, 2, 1, 0, "relu"), (2, 8200, 2, 2, 0, 1, None),
     (16, 64, 40, 40, 1, 1, "silu"), (5, 24, 17, 3, 0, 2, "silu"),
+    # lcm(C / 8, 64) > 512: workgroups of C / 8 * R threads, a partial last wave
+    (2, 136, 9, 9, 1, 1, "silu"), (3, 288, 7, 7, 0, 1, "relu"), (4, 240, 5, 6, 1, 0, None),
 ]
 
 
