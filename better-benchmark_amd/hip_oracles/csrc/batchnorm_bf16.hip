@@ -20,9 +20,11 @@
 //   2. a per-channel merge of the slices in fp64 (a fixed order) that writes
 //      save_mean, save_rstd and the running statistics -- its own launch for
 //      channels-last; folded into the epilogue's workgroups for NCHW, whose
-//      64 channels each workgroup merges itself;
+//      channels each workgroup merges itself;
 //   3. the normalise + activation pass (padded store / spatial mean).
-// HBM-bound: x is read twice and the output written once.
+// HBM-bound: x is read twice and the output written once.  NCHW shapes whose
+// channels fit a workgroup's registers (N * HW <= 8192, HW <= 64) take one
+// launch instead (bn_nchw_channels): x read once, no workspace.
 #include <algorithm>
 
 #include "hipo_common.h"
@@ -616,6 +618,174 @@ __global__ __launch_bounds__(kPlaneWaves * kWave) void bn_nchw_planes(
 }
 
 // ---------------------------------------------------------------------------
+// NCHW with all of a channel's N x HW values held in registers (C a multiple
+// of kChanCh, x and out aligned to a word of kChanCh values, HW <= 64, N * HW
+// <= kChanLoads * kChanThreads, ceil(N / kImgStep) * HWB / 8 <=
+// kChanMaxVals): one launch, x read once, no workspace.  A workgroup owns
+// channels c0 .. c0 + kChanCh - 1; for image n their planes are one
+// contiguous run of kChanCh * HW values (HW words), so the workgroup stages
+// its N * HW words in LDS ([N][kChanCh][HW] values), all of a thread's
+// loads in flight at once.  kChanParts waves share a channel c and split its
+// images: wave (ch, part) takes n = kImgStep s + 8 part + r (step s), lane
+// 8 r + k the elements k, k + 8, ... of plane (n, c).  From the registers:
+//   mean: shift = x[0, c, 0]; per lane the sum of (x - shift) in fp32, per
+//     wave in fp64 (a fixed order), the channel's waves added in order
+//     through LDS: mean = shift + S1 / (N HW);
+//   M2: the sum of (x - mean_f)^2 (mean_f = fp32(mean)) the same way, less
+//     N HW (mean - mean_f)^2;
+//   save_mean, save_rstd and the running statistics as the merges elsewhere;
+//   out[n, c] = bf16(sum_hw act(bn(x[n, c, hw])) / HW): per step a plane's
+//     sum over its 8 lanes (sum8), staged in LDS so that each image's
+//     kChanCh outputs leave as one word.
+// ---------------------------------------------------------------------------
+// Measured at [128, 1024, 7, 7] (ReLU), kernel alone: 4 channels x 4 waves,
+// 8-byte words: 11.3 us, 10.6 with the XCD-aware order below (shipped);
+// 2 channels x 8 waves, 4-byte words: 16.5 us.  The two-launch planes path
+// took 7.5 + 5.8 us there.
+constexpr int kChanCh = 4;          // channels per workgroup
+typedef u32x2_t chan_word_t;        // kChanCh bf16 values
+constexpr int kChanParts = 4;       // waves per channel
+constexpr int kChanThreads = kChanCh * kChanParts * kWave;
+constexpr int kImgStep = kChanParts * 8;  // images per step of a channel's waves
+constexpr int kChanLoads = 8;       // words per thread
+constexpr int kChanMaxVals = 32;    // values per lane
+constexpr int kChanMaxHw = 64;
+constexpr int64_t kChanMaxWords = int64_t{kChanLoads} * kChanThreads;  // N * HW
+
+template <int HWB, int ACT>
+__global__ __launch_bounds__(kChanThreads) void bn_nchw_channels(
+    const uint16_t* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float* __restrict__ running_mean,
+    float* __restrict__ running_var, float* __restrict__ save_mean,
+    float* __restrict__ save_rstd, uint16_t* __restrict__ out, int N, int C, int HW,
+    DivMagic by_hw, float momentum, float eps, float var_scale) {
+  constexpr int kT = HWB / 8;                // values per lane per plane
+  constexpr int kSteps = kChanMaxVals / kT;  // planes per lane: N <= kImgStep kSteps
+  extern __shared__ __align__(16) uint16_t chan_stage[];
+  __shared__ double red[2][kChanCh][kChanParts];
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int w = t >> 6;
+  const int ch = w % kChanCh;
+  const int part = w / kChanCh;
+  const int r = lane >> 3;
+  const int k = lane & 7;
+  // XCD-aware order: workgroup ids go round-robin over the 8 XCDs; each XCD
+  // takes a contiguous range of channel groups, so the cache lines shared by
+  // neighbouring groups' runs are fetched into one L2.
+  const int nb = static_cast<int>(gridDim.x);
+  const int bid = static_cast<int>(blockIdx.x);
+  const int grp = nb % 8 == 0 ? (bid % 8) * (nb / 8) + bid / 8 : bid;
+  const int c0 = grp * kChanCh;
+  const int c = c0 + ch;
+  const int words = N * HW;
+  const chan_word_t* xw = reinterpret_cast<const chan_word_t*>(x);
+  const float g = gamma[c], b = beta[c];
+  chan_word_t v[kChanLoads];
+#pragma unroll
+  for (int q = 0; q < kChanLoads; ++q) {
+    const int i0 = t + q * kChanThreads;
+    const int i = i0 < words ? i0 : words - 1;  // in bounds; stored only if i0 < words
+    const int n = static_cast<int>(div_by(static_cast<uint32_t>(i), by_hw));
+    // Word i - n HW of image n's run, which starts at value (n C + c0) HW,
+    // a multiple of kChanCh.
+    v[q] = xw[(static_cast<int64_t>(n) * C + c0) * HW / kChanCh + (i - n * HW)];
+  }
+  chan_word_t* sw = reinterpret_cast<chan_word_t*>(chan_stage);
+#pragma unroll
+  for (int q = 0; q < kChanLoads; ++q) {
+    const int i = t + q * kChanThreads;
+    if (i < words) sw[i] = v[q];
+  }
+  __syncthreads();
+
+  // This lane's values: val[s][u] = x[n_s, c, k + 8u], valid where
+  // n_s < N and k + 8u < HW (zero elsewhere).  The LDS reads are
+  // unconditional (indices clamped into the staged values), so they all
+  // issue before the first is used.
+  const uint16_t* pl = chan_stage + ch * HW;
+  const int stride = kChanCh * HW;
+  float val[kSteps][kT];
+  bool img_ok[kSteps];
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const int n = kImgStep * s + 8 * part + r;
+    img_ok[s] = n < N;
+    const uint16_t* p = pl + (img_ok[s] ? n : 0) * stride;
+#pragma unroll
+    for (int u = 0; u < kT; ++u) {
+      const int j = k + 8 * u;
+      val[s][u] = bf16_to_f32(p[j < HW ? j : HW - 1]);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s)
+#pragma unroll
+    for (int u = 0; u < kT; ++u) val[s][u] = img_ok[s] && k + 8 * u < HW ? val[s][u] : 0.f;
+  const float shift = bf16_to_f32(pl[0]);
+  float s1 = 0.f;
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s)
+#pragma unroll
+    for (int u = 0; u < kT; ++u)
+      s1 += img_ok[s] && k + 8 * u < HW ? val[s][u] - shift : 0.f;
+  const double w1 = wave_sum(static_cast<double>(s1));
+  if (lane == 0) red[0][ch][part] = w1;
+  __syncthreads();
+  const double cnt = static_cast<double>(N) * HW;
+  double t1 = red[0][ch][0];
+#pragma unroll
+  for (int q = 1; q < kChanParts; ++q) t1 += red[0][ch][q];
+  const double mean = static_cast<double>(shift) + t1 / cnt;
+  const float mf = static_cast<float>(mean);
+  float s2 = 0.f;
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s)
+#pragma unroll
+    for (int u = 0; u < kT; ++u) {
+      const float d = val[s][u] - mf;
+      s2 = img_ok[s] && k + 8 * u < HW ? __builtin_fmaf(d, d, s2) : s2;
+    }
+  const double w2 = wave_sum(static_cast<double>(s2));
+  if (lane == 0) red[1][ch][part] = w2;
+  __syncthreads();
+  double t2 = red[1][ch][0];
+#pragma unroll
+  for (int q = 1; q < kChanParts; ++q) t2 += red[1][ch][q];
+  const double dm = mean - static_cast<double>(mf);
+  const double m2 = t2 - cnt * dm * dm;
+  const float var_f = static_cast<float>(std::max(0.0, m2) / cnt);
+  const float rc = 1.0f / __builtin_sqrtf(__fadd_rn(var_f, eps));
+  if (part == 0 && lane == 0) {
+    save_mean[c] = mf;
+    save_rstd[c] = rc;
+    const float keep = 1.0f - momentum;
+    running_mean[c] = __fadd_rn(__fmul_rn(mf, momentum), __fmul_rn(running_mean[c], keep));
+    running_var[c] = __fadd_rn(__fmul_rn(__fmul_rn(var_f, var_scale), momentum),
+                               __fmul_rn(running_var[c], keep));
+  }
+  // The staged x is no longer read (every wave passed the barriers above
+  // after its last read of it): the outputs go there, [N][kChanCh].
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    if (kImgStep * s >= N) break;  // wave-uniform
+    float sum = 0.f;
+#pragma unroll
+    for (int u = 0; u < kT; ++u)
+      sum += k + 8 * u < HW ? round_bf16(bn_act(val[s][u], mf, rc, g, b, ACT)) : 0.f;
+    sum = sum8(sum);
+    const int n = kImgStep * s + 8 * part + r;
+    if (k == 0 && img_ok[s])
+      chan_stage[n * kChanCh + ch] =
+          static_cast<uint16_t>(pack_bf16x2(sum / static_cast<float>(HW), 0.f) & 0xffffu);
+  }
+  __syncthreads();
+  chan_word_t* ow = reinterpret_cast<chan_word_t*>(out);
+  for (int n = t; n < N; n += kChanThreads)
+    ow[(static_cast<int64_t>(n) * C + c0) / kChanCh] = sw[n];
+}
+
+// ---------------------------------------------------------------------------
 // Per-channel merge.  The workspace is channel-major: part[c * S + s] is
 // slice s of channel c, which holds (min(units, (s+1)*per) - s*per) * mult
 // values with mean m_s and M2_s.  In fp64, about the shift K = m_0:
@@ -852,6 +1022,38 @@ extern "C" int hipo_batchnorm_nchw_act_mean_bf16(
                "%s: workspace of %zu bytes (16-byte aligned), need %zu", what, workspace_bytes,
                need);
   HIPO_REQUIRE(slices <= 65535, "%s: too many images", what);
+  const bool word_aligned = reinterpret_cast<uintptr_t>(x) % sizeof(chan_word_t) == 0 &&
+                            reinterpret_cast<uintptr_t>(out) % sizeof(chan_word_t) == 0;
+  if (c % kChanCh == 0 && word_aligned && hw <= kChanMaxHw && n * hw <= kChanMaxWords) {
+    const int hwb = hw <= 8 ? 8 : hw <= 16 ? 16 : hw <= 32 ? 32 : 64;
+    if ((n + kImgStep - 1) / kImgStep * (hwb / 8) <= kChanMaxVals) {
+      const int ni = static_cast<int>(n), ci = static_cast<int>(c), hi = static_cast<int>(hw);
+      const DivMagic by_hw = div_magic(static_cast<uint32_t>(hw));
+      const size_t lds = static_cast<size_t>(n * hw) * sizeof(chan_word_t);
+      const dim3 grid(static_cast<unsigned>(c / kChanCh));
+      const dim3 block(kChanThreads);
+#define HIPO_CHANNELS(B_)                                                                        \
+  do {                                                                                           \
+    auto kernel = act == kActSilu   ? bn_nchw_channels<B_, kActSilu>                             \
+                  : act == kActRelu ? bn_nchw_channels<B_, kActRelu>                             \
+                                    : bn_nchw_channels<B_, kActNone>;                            \
+    kernel<<<grid, block, lds, stream>>>(x, gamma, beta, running_mean, running_var, save_mean,   \
+                                         save_rstd, out, ni, ci, hi, by_hw, momentum, eps,       \
+                                         var_scale);                                             \
+  } while (0)
+      if (hwb == 8) {
+        HIPO_CHANNELS(8);
+      } else if (hwb == 16) {
+        HIPO_CHANNELS(16);
+      } else if (hwb == 32) {
+        HIPO_CHANNELS(32);
+      } else {
+        HIPO_CHANNELS(64);
+      }
+#undef HIPO_CHANNELS
+      return check_launch(what);
+    }
+  }
   float2* part = static_cast<float2*>(workspace);
   const NchwMerge none{};
   const NchwMerge mg{part, slices, running_mean, running_var, save_mean, save_rstd,

@@ -58,6 +58,9 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 inline bool aligned16(const void* p) {
   return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 }
+inline bool aligned8(const void* p) {
+  return reinterpret_cast<uintptr_t>(p) % 8 == 0;
+}
 
 // bf16 bits held in the low / high half of a 32-bit word -> fp32 (exact).
 __device__ __forceinline__ float bf16lo(uint32_t w) {
@@ -155,6 +158,23 @@ __device__ __forceinline__ float wave_sum(float v) {
   float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
   float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
   return (a + b) + (c + d);
+}
+
+// The same fixed-order full-wave sum in fp64.
+__device__ __forceinline__ double wave_sum(double v) {
+  v += dpp<kDppQuadXor1>(v);
+  v += dpp<kDppQuadXor2>(v);
+  v += dpp<kDppRowRor4>(v);
+  v += dpp<kDppRowRor8>(v);
+  auto lane_value = [&](int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b)), l));
+    const uint32_t hi = static_cast<uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b >> 32)), l));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+  };
+  return (lane_value(0) + lane_value(16)) + (lane_value(32) + lane_value(48));
 }
 
 // Full-wave max; every lane receives the same value (all lanes active).

@@ -1110,6 +1110,11 @@ def test_batchnorm_nhwc_act_pad(n, c, h, w, pb, pr, act, rocm_device):
 BN_NCHW_CASES = [  # n, c, h, w, act
     (5, 72, 7, 7, "relu"), (3, 20, 7, 7, "relu"), (4, 16, 10, 10, "silu"), (2, 64, 1, 1, None),
     (9, 128, 3, 5, "relu"), (8, 1024, 7, 7, "relu"), (2, 16, 12, 12, "relu"),
+    # one launch, a channel's values in registers (C % 4 == 0, HW <= 64,
+    # N * HW <= 8192, ceil(N / 32) * ceil8(HW) / 8 <= 32)
+    (64, 32, 7, 7, "relu"), (40, 16, 9, 9, "relu"), (128, 64, 8, 8, None), (32, 12, 3, 3, "relu"),
+    (128, 1024, 7, 7, "relu"), (1024, 8, 2, 4, "relu"), (257, 8, 4, 4, "silu"),
+    (33, 8, 16, 16, "relu"), (40, 24, 9, 10, "relu"),
 ]
 
 
@@ -1191,10 +1196,11 @@ def _exact_silu_bf16_bits():
 def test_batchnorm_silu_every_bf16_input(rocm_device):
     """Bit for bit, over all 65536 bf16 t: the BatchNorm kernels' SiLU is
     the correctly rounded SiLU (mpmath), through the channels-last vector
-    and scalar epilogues and both NCHW act+mean kernels.  One element per
-    channel (n = h = w = 1) makes the normalised value 0, so the activation
-    input is bf16(0 * gamma + beta) = beta exactly (-0 becomes +0): beta
-    carries the 65536 patterns.  The kernels evaluate t > -87 with the
+    and scalar epilogues and the three NCHW act+mean kernels.  An all-zero
+    x (h = w = 1) makes every channel's variance 0 and its normalised
+    values 0, so the activation input is bf16(0 * gamma + beta) = beta
+    exactly (-0 becomes +0): beta carries the 65536 patterns.  The kernels
+    evaluate t > -87 with the
     hardware exp2 and reciprocal, so this comparison over the whole domain
     is what proves that evaluation correctly rounded."""
     import hip_oracles
@@ -1202,9 +1208,9 @@ def test_batchnorm_silu_every_bf16_input(rocm_device):
     want = _exact_silu_bf16_bits()
     ts = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
 
-    def run(layout, lo, c):
+    def run(layout, lo, c, images=1, hw=1):
         beta = ts[lo:lo + c].contiguous()
-        x = torch.zeros(1, c, 1, 1, dtype=torch.bfloat16)
+        x = torch.zeros(images, c, hw, 1, dtype=torch.bfloat16)
         if layout == "nhwc":
             x = x.contiguous(memory_format=torch.channels_last)
         d = [t.to(rocm_device) for t in (x, torch.ones(c), beta, torch.zeros(c), torch.ones(c))]
@@ -1214,18 +1220,24 @@ def test_batchnorm_silu_every_bf16_input(rocm_device):
         else:
             _, _, out = hip_oracles.batchnorm_nchw_act_mean(
                 *d, momentum=0.1, eps=1e-3, var_scale=1.0, act="silu")
-        return out.cpu().reshape(-1).view(torch.int16).tolist()
+            # x is all zeros, so every image's row is the same, bit for bit
+            bits = out.view(torch.int16)
+            assert bool((bits == bits[:1]).all())
+        return out.cpu()[0].reshape(-1).view(torch.int16).tolist()
 
-    # (layout, what, channel chunk): 8192 channels take the channels-last
-    # vector path, 65536 its scalar path; 65536 the NCHW planes kernel,
-    # 65533 + 3 (not a multiple of 8) its small-hw kernel.
-    plans = (("nhwc", "vector", [8192] * 8), ("nhwc", "scalar", [65536]),
-             ("nchw", "planes", [65536]), ("nchw", "small_hw", [65533, 3]))
-    for layout, what, chunks in plans:
+    # (layout, what, channel chunk, images, hw): 8192 channels take the
+    # channels-last vector path, 65536 its scalar path; NCHW with HW = 1 the
+    # register-held channels kernel, HW = 65 the planes kernel (a mean of
+    # 65 equal values: exact unless the sum overflows, so |SiLU| >= 2^120 is
+    # left out there), 65533 + 3 (not a multiple of 4) the small-hw kernel.
+    plans = (("nhwc", "vector", [8192] * 8, 1, 1), ("nhwc", "scalar", [65536], 1, 1),
+             ("nchw", "channels", [8192] * 8, 32, 1), ("nchw", "planes", [65536], 1, 65),
+             ("nchw", "small_hw", [65533, 3], 1, 1))
+    for layout, what, chunks, images, hw in plans:
         print(f"[bn-silu] every bf16 input, {layout} {what}", flush=True)
         got, lo = [], 0
         for c in chunks:
-            got += run(layout, lo, c)
+            got += run(layout, lo, c, images, hw)
             lo += c
         bad = []
         for tb, gv in enumerate(got):
@@ -1233,6 +1245,8 @@ def test_batchnorm_silu_every_bf16_input(rocm_device):
             gv &= 0xFFFF
             if layout == "nchw" and w == 0x8000:
                 w = 0   # a mean of -0 starts from +0
+            if hw > 1 and w is not None and (w & 0x7FFF) >= 0x7B80:
+                continue  # |SiLU| >= 2^120: the sum of 65 copies can overflow
             if w is None:
                 if not (gv & 0x7F80 == 0x7F80 and gv & 0x7F):
                     bad.append((hex(tb), hex(gv), "NaN"))
