@@ -250,7 +250,15 @@ __global__ __launch_bounds__(kFinishThreads) void colsum_finish(const double* __
   constexpr int kSlices = kFinishThreads / kCols;
   const int l = threadIdx.x % kCols;
   const int j = threadIdx.x / kCols;
-  const int c = static_cast<int>(blockIdx.x) * kCols + l;
+  // XCD-aware order: workgroup ids go round-robin over the 8 XCDs; each XCD
+  // takes a contiguous range of column groups, so the partial rows' cache
+  // lines, which kCols-column groups share, are fetched into one L2.  (After
+  // a cache flush, [175360, 3072] / [25216, 3072]: 569 -> 557 / 97.6 -> 94.4
+  // us for the whole call.)
+  const int nb = static_cast<int>(gridDim.x);
+  const int bid = static_cast<int>(blockIdx.x);
+  const int grp = nb % 8 == 0 ? (bid % 8) * (nb / 8) + bid / 8 : bid;
+  const int c = grp * kCols + l;
   const bool ok = c < cols;
   const int cc = ok ? c : cols - 1;
   double s = 0.0;
