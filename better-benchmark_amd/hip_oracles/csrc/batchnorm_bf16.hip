@@ -628,11 +628,13 @@ __global__ __launch_bounds__(kPlaneWaves * kWave) void bn_nchw_planes(
 // loads in flight at once.  kChanParts waves share a channel c and split its
 // images: wave (ch, part) takes n = kImgStep s + 8 part + r (step s), lane
 // 8 r + k the elements k, k + 8, ... of plane (n, c).  From the registers:
-//   mean: shift = x[0, c, 0]; per lane the sum of (x - shift) in fp32, per
-//     wave in fp64 (a fixed order), the channel's waves added in order
-//     through LDS: mean = shift + S1 / (N HW);
-//   M2: the sum of (x - mean_f)^2 (mean_f = fp32(mean)) the same way, less
-//     N HW (mean - mean_f)^2;
+//   one pass about shift = x[0, c, 0] (a value of the channel, so the
+//     deviations stay of the order of its spread): per lane the sums of
+//     d = x - shift and d^2 in fp32, per wave in fp32 (a fixed order), the
+//     channel's waves added in order in fp64 through LDS: with n = N HW,
+//     mean = shift + S1 / n, M2 = S2 - S1^2 / n (one barrier; the exact
+//     two-pass form, mean first and then the squares about it, took a
+//     second barrier and 0.5 us more at [128, 1024, 7, 7]);
 //   save_mean, save_rstd and the running statistics as the merges elsewhere;
 //   out[n, c] = bf16(sum_hw act(bn(x[n, c, hw])) / HW): per step a plane's
 //     sum over its 8 lanes (sum8), staged in LDS so that each image's
@@ -723,37 +725,34 @@ __global__ __launch_bounds__(kChanThreads) void bn_nchw_channels(
 #pragma unroll
     for (int u = 0; u < kT; ++u) val[s][u] = img_ok[s] && k + 8 * u < HW ? val[s][u] : 0.f;
   const float shift = bf16_to_f32(pl[0]);
-  float s1 = 0.f;
-#pragma unroll
-  for (int s = 0; s < kSteps; ++s)
-#pragma unroll
-    for (int u = 0; u < kT; ++u)
-      s1 += img_ok[s] && k + 8 * u < HW ? val[s][u] - shift : 0.f;
-  const double w1 = wave_sum(static_cast<double>(s1));
-  if (lane == 0) red[0][ch][part] = w1;
-  __syncthreads();
-  const double cnt = static_cast<double>(N) * HW;
-  double t1 = red[0][ch][0];
-#pragma unroll
-  for (int q = 1; q < kChanParts; ++q) t1 += red[0][ch][q];
-  const double mean = static_cast<double>(shift) + t1 / cnt;
-  const float mf = static_cast<float>(mean);
-  float s2 = 0.f;
+  float s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s)
 #pragma unroll
     for (int u = 0; u < kT; ++u) {
-      const float d = val[s][u] - mf;
-      s2 = img_ok[s] && k + 8 * u < HW ? __builtin_fmaf(d, d, s2) : s2;
+      const bool ok = img_ok[s] && k + 8 * u < HW;
+      const float d = val[s][u] - shift;
+      s1 += ok ? d : 0.f;
+      s2 = ok ? __builtin_fmaf(d, d, s2) : s2;
     }
-  const double w2 = wave_sum(static_cast<double>(s2));
-  if (lane == 0) red[1][ch][part] = w2;
+  const double w1 = static_cast<double>(wave_sum(s1));
+  const double w2 = static_cast<double>(wave_sum(s2));
+  if (lane == 0) {
+    red[0][ch][part] = w1;
+    red[1][ch][part] = w2;
+  }
   __syncthreads();
-  double t2 = red[1][ch][0];
+  const double cnt = static_cast<double>(N) * HW;
+  double t1 = red[0][ch][0], t2 = red[1][ch][0];
 #pragma unroll
-  for (int q = 1; q < kChanParts; ++q) t2 += red[1][ch][q];
-  const double dm = mean - static_cast<double>(mf);
-  const double m2 = t2 - cnt * dm * dm;
+  for (int q = 1; q < kChanParts; ++q) {
+    t1 += red[0][ch][q];
+    t2 += red[1][ch][q];
+  }
+  const double dmean = t1 / cnt;
+  const double mean = static_cast<double>(shift) + dmean;
+  const float mf = static_cast<float>(mean);
+  const double m2 = t2 - t1 * dmean;
   const float var_f = static_cast<float>(std::max(0.0, m2) / cnt);
   const float rc = 1.0f / __builtin_sqrtf(__fadd_rn(var_f, eps));
   if (part == 0 && lane == 0) {

@@ -1136,6 +1136,30 @@ def test_batchnorm_nchw_act_mean(n, c, h, w, act, rocm_device):
     assert_close(out, wy.mean((2, 3)), BF16_TOL, "spatial mean")
 
 
+def test_batchnorm_nchw_misaligned_x_takes_the_general_kernel(rocm_device):
+    """x 2 bytes off a 16-byte boundary: neither the register-held channels
+    kernel (8-byte words) nor the planes kernel (16-byte vectors) applies,
+    and the lane-per-channel kernel gives the same statistics and means as
+    the aligned call at the same shape (which takes the channels kernel)."""
+    import hip_oracles
+    n, c, h, w = 64, 32, 7, 7
+    x, (gm, bt, rm, rv) = _bn_bf16_inputs(n, c, h, w, 77, False)
+    buf = torch.empty(x.numel() + 8, dtype=torch.bfloat16, device=rocm_device)
+    xm = buf[1:1 + x.numel()].view(n, c, h, w)
+    xm.copy_(x.to(rocm_device))
+    assert xm.data_ptr() % 8 == 2
+    got = []
+    for xd in (xm, x.to(rocm_device)):
+        d = [t.to(rocm_device) for t in (gm, bt, rm, rv)]
+        got.append(hip_oracles.batchnorm_nchw_act_mean(
+            xd, d[0], d[1], d[2], d[3], momentum=0.1, eps=1e-5, var_scale=1.5, act="relu"))
+    wm, wr, wy, _, _ = _bn_bf16_ref(x, gm, bt, rm, rv, 1e-5, 0.1, 1.5, "relu")
+    for (mean, rstd, out), what in zip(got, ("misaligned", "aligned")):
+        assert_close(mean, wm, F32_TOL, what + " save_mean")
+        assert_close(rstd, wr, (1e-5, 1e-5 * max(1.0, float(wr.abs().max()))), what + " save_rstd")
+        assert_close(out, wy.mean((2, 3)), BF16_TOL, what + " spatial mean")
+
+
 def test_batchnorm_bf16_closed_forms(rocm_device):
     """A constant channel: mean = the constant, var = 0, rstd = 1/sqrt(eps),
     y = act(bf16(beta)); running_var decays by 1 - momentum."""
