@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-40057a60, oracle 16.84 us, Inductor 16.4 us (ratio 0.974, AT_FLOOR); over the dir's 2
+40057a60, oracle 16.88 us, Inductor 17.52 us (ratio 1.038, AT_FLOOR); over the dir's 2
 registered points: 2 AT_FLOOR.
 
 MI355X oracle for mean_8818e35b12aa: residual add + RMSNorm over the last

@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-c4bf51cc, oracle 27.92 us, Inductor 29.16 us (ratio 1.044, AT_FLOOR); over the dir's 8
+c4bf51cc, oracle 27.8 us, Inductor 29.6 us (ratio 1.065, GOOD); over the dir's 8
 registered points: 5 GOOD, 3 AT_FLOOR; 1 points withdrawn (WITHDRAWN_POINTS).
 
 MI355X oracle for var_mean_b19e82f2a47b: residual add + LayerNorm over the
