@@ -32,7 +32,9 @@ configs[].pattern_copy_us = where a flat copy does not share the kernel's
                     BatchNorm's register-held slabs without the exchange),
                     same loop; vs_pattern_copy = pattern_copy_us / steady_us
 cpu_baseline      = the eager repro (ATen) on the host CPU, os.cpu_count()
-                    threads, warmup 1 + min of 5 (BASELINE.md's method); the
+                    threads, warmup 1 + min of 5 runs (the min-of-runs
+                    CPU timing of the reference's _do_bench,
+                    oracle_harness.py:1718, with fewer runs); the
                     CPU oracle (oracle/hipo_ref.c) time rides along.
 configs           = every BASELINE config: the same steady-state loop and
                     flat copy; the compiled repro (torch.compile, Inductor)
@@ -140,8 +142,9 @@ def c_oracle_time(rid, cpu_inputs, budget_s: float = 5.0) -> dict:
 
 
 def cpu_baseline(rid, cpu_inputs, nbytes) -> dict:
-    """The eager repro on the host CPU (os.cpu_count() threads,
-    warmup 1 + min of 5 perf_counter runs), expressed in the metric's unit
+    """The eager repro on the host CPU (os.cpu_count() threads, warmup 1 + min
+    of 5 perf_counter runs: the min-of-runs CPU timing of the reference's
+    _do_bench, oracle_harness.py:1718, with fewer runs), expressed in the metric's unit
     over the same algorithmic bytes; the CPU oracle's time rides along."""
     import oracle_harness as oh
     _, _, d = oh._load_oracle_module(CANONICAL / rid)
