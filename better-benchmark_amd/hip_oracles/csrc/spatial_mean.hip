@@ -201,6 +201,7 @@ struct SpatialPlan {
 };
 
 // Channel blocks of 64 groups (1 KiB of each row), or of 32 (512 bytes),
+// or of 16 (256 bytes),
 // when the row divides into them and images x blocks give at least 256
 // workgroups: no position split, so no partial sums and no second kernel.
 // 64-group blocks are tried first, except for small images (below).
@@ -214,7 +215,7 @@ struct SpatialPlan {
 // of a fixed 8 rows, [128, 1536, 6, 6] 15.4 -> 15.1 us and [128, 512, 24,
 // 24] (32-group blocks instead of slices) 25.1 -> 23.7 us (graph replays);
 // one round (R up to 16 rows, 1024 threads) was 4-6 % slower, cached loads
-// and 16- or 8-group blocks no faster.
+// and 16- or 8-group blocks no faster where 64-group blocks apply.
 constexpr int kChannelBlock = 64;
 
 SpatialPlan spatial_plan(int64_t n, int64_t p, int64_t c) {
@@ -224,8 +225,14 @@ SpatialPlan spatial_plan(int64_t n, int64_t p, int64_t c) {
   // the workgroups for the same bytes ([128, 1536, 9, 9] 8.53 -> 8.03 us,
   // [128, 1536, 8, 8] 6.81 -> 6.60, [128, 1536, 6, 6] 5.68 -> 5.52 in the
   // steady loop; larger images unchanged).
+  // Then 16-group blocks (256 bytes of each row), where the wider blocks
+  // give too few workgroups: C = 256 at 128 images takes 256 workgroups
+  // with no position slices and no finishing kernel ([128, 256, 72, 72]
+  // 57.9 -> 56.1 us after a cache flush, 55.2 -> 53.0 back to back;
+  // [128, 256, 56, 56] 37.8 -> 36.4 / 34.7 -> 33.4; [128, 256, 48, 48] and
+  // [128, 256, 64, 64] 1-3 % faster).
   const int first = p <= 128 ? kChannelBlock / 2 : kChannelBlock;
-  const int gbs[2] = {first, kChannelBlock + kChannelBlock / 2 - first};
+  const int gbs[3] = {first, kChannelBlock + kChannelBlock / 2 - first, kChannelBlock / 4};
   for (const int gb : gbs) {
     if ((c / 8) % gb != 0 || n * (c / 8 / gb) < 256) continue;
     int64_t r = 1;

@@ -1022,8 +1022,8 @@ def test_masked_softmax_broadcast_mask_rows(rocm_device):
 
 
 def test_spatial_mean_layouts(rocm_device):
-    """Vector path (one slice and several; channel blocks of 64 groups when
-    images x blocks fill the chip), the small-image kernel (one wave per
+    """Vector path (one slice and several; channel blocks of 64, 32 or 16
+    groups when images x blocks fill the chip), the small-image kernel (one wave per
     image and 64-channel block, 1 to 24 positions per lane), C not a
     multiple of 8 and C / 8 above 1024 (scalar kernel), one position,
     non-power-of-two group counts, keepdim off."""
@@ -1033,7 +1033,9 @@ def test_spatial_mean_layouts(rocm_device):
                        (1, 8192, 2, 2), (2, 8200, 3, 3), (4, 1536, 6, 6), (1, 256, 72, 72),
                        (256, 64, 2, 3), (1, 24, 300, 7), (128, 1024, 5, 5), (100, 1536, 7, 7),
                        (128, 1536, 6, 6), (64, 512, 12, 12), (32, 1024, 16, 12), (600, 64, 1, 1),
-                       (512, 128, 3, 3), (1024, 64, 9, 10)]:
+                       (512, 128, 3, 3), (1024, 64, 9, 10),
+                       # 16-group channel blocks: C = 256, 128 or more images
+                       (128, 256, 20, 20), (129, 256, 13, 15), (256, 128, 14, 14)]:
         what = f"spatial_mean n={n} c={c} {h}x{w}"
         print(f"[edges] {what}", flush=True)
         g = torch.Generator().manual_seed(n * c + h * w)
