@@ -190,7 +190,10 @@ inline bool row_plan(int64_t cols, RowPlan& plan) {
   // 2 groups 45.2-45.4 us, 2 x 4 46.9-47.3, 1 x 8 50.0-50.2.)  (One group per wave for the two streams of LayerNorm was
   // faster with outputs reused across launches, slower in the steady loop
   // where every step writes fresh output buffers: 91.7-92.3 against
-  // 89.7-89.9 us at [16384, 4096].)
+  // 89.7-89.9 us at [16384, 4096].)  (LayerNorm rows of 2560: 5 waves x 1
+  // group, no idle lanes, against this plan's 3 x 2: y only [4096, 2560]
+  // 15.5 against 14.3 us and [2048, 2560] 9.4 against 7.5 back to back; h
+  // and y [4096, 2560] 17.3 against 18.2.)
   const int64_t per_wave = 2 * kRowSweep;
   const int64_t w = std::min<int64_t>(kRowMaxWaves, (cols + per_wave - 1) / per_wave);
   plan.waves_per_row = static_cast<int>(std::max<int64_t>(1, w));
