@@ -15,7 +15,7 @@
 // With one position slice per image the result is written as bf16 directly;
 // with S > 1 slices (more workgroups than images alone give) each slice
 // writes fp32 partials and a second kernel adds the S slices of a channel in
-// a fixed order.  Small images (at most 192 positions, C a multiple of 64,
+// a fixed order.  Small images (at most 224 positions, C a multiple of 64,
 // enough images) take spatial_mean_small_waves instead: one wave per (image,
 // 64-channel block), every position in flight.  Deterministic.
 // HBM-bound: algorithmic bytes = 2 N P C (read) + 2 N C (write).
@@ -105,9 +105,11 @@ __global__ __launch_bounds__(kMaxThreads) void spatial_mean_nhwc_partial(
 // kernel's time first): 6x6 5.47 -> 4.56 us, 7x7 6.33 -> 5.28, 8x8 6.63 ->
 // 5.96, 9x9 8.06 -> 7.16, 12x12 12.36 -> 10.90 (Inductor 4.78, 5.29, 6.48,
 // 7.58, 12.17); blocks of 128 or 256 channels (16 or 32 lanes per row)
-// were slower (4.85 / 5.50 us at 6x6).
+// were slower (4.85 / 5.50 us at 6x6).  Up to 224 positions (28 loads per
+// lane): [128, 1536, 14, 14] 15.3 -> 13.8 us back to back (18.3 -> 16.8
+// after a cache flush), [64, 1536, 14, 15] 10.5 -> 9.0.
 constexpr int kSmallGroups = 8;    // 16-byte groups per wave block (64 channels)
-constexpr int kSmallMaxLoads = 24;  // positions per lane: P <= 192
+constexpr int kSmallMaxLoads = 28;  // positions per lane: P <= 224
 
 template <int L>
 __global__ __launch_bounds__(256) void spatial_mean_small_waves(
@@ -263,7 +265,7 @@ SpatialPlan spatial_plan(int64_t n, int64_t p, int64_t c) {
 }
 
 // The small-image kernel's loads per lane (ceil(P / 8)), or 0 where it
-// does not apply: C a multiple of 64, P <= 192, and at least 512 waves (two
+// does not apply: C a multiple of 64, P <= 224, and at least 512 waves (two
 // per CU) of (image, 64-channel block).
 int spatial_small_loads(int64_t n, int64_t p, int64_t c) {
   if (c % (8 * kSmallGroups) != 0 || p <= 0 || n <= 0) return 0;
@@ -294,7 +296,8 @@ void launch_small_waves(int loads, const uint16_t* x, uint16_t* out, int64_t n, 
     case 15: case 16: HIPO_SMW(16); break;
     case 17: case 18: HIPO_SMW(18); break;
     case 19: case 20: HIPO_SMW(20); break;
-    default: HIPO_SMW(24); break;
+    case 21: case 22: case 23: case 24: HIPO_SMW(24); break;
+    default: HIPO_SMW(28); break;
   }
 #undef HIPO_SMW
 }

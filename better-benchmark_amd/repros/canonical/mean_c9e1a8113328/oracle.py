@@ -12,7 +12,7 @@ Kernel: hipo_spatial_mean_nhwc_bf16 -- per image a column reduction of the
 [H*W, C] block: each workgroup instruction reads whole contiguous rows, every
 thread keeps fp32 sums for one 8-channel group, partial sums meet in LDS in a
 fixed order (and, when positions are split for parallelism, a second pass
-adds the slices in order); images of at most 192 positions take one wave per
+adds the slices in order); images of at most 224 positions take one wave per
 (image, 64-channel block) with every position in flight at once and an
 xor-shuffle combine (no LDS).  Algorithmic bytes: 2 N H W C + 2 N C.
 Replaces the Triton body of the reference's

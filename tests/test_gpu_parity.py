@@ -1024,7 +1024,7 @@ def test_masked_softmax_broadcast_mask_rows(rocm_device):
 def test_spatial_mean_layouts(rocm_device):
     """Vector path (one slice and several; channel blocks of 64, 32 or 16
     groups when images x blocks fill the chip), the small-image kernel (one wave per
-    image and 64-channel block, 1 to 24 positions per lane), C not a
+    image and 64-channel block, 1 to 28 positions per lane), C not a
     multiple of 8 and C / 8 above 1024 (scalar kernel), one position,
     non-power-of-two group counts, keepdim off."""
     import hip_oracles
@@ -1034,8 +1034,10 @@ def test_spatial_mean_layouts(rocm_device):
                        (256, 64, 2, 3), (1, 24, 300, 7), (128, 1024, 5, 5), (100, 1536, 7, 7),
                        (128, 1536, 6, 6), (64, 512, 12, 12), (32, 1024, 16, 12), (600, 64, 1, 1),
                        (512, 128, 3, 3), (1024, 64, 9, 10),
-                       # 16-group channel blocks: C = 256, 128 or more images
-                       (128, 256, 20, 20), (129, 256, 13, 15), (256, 128, 14, 14)]:
+                       # 16-group channel blocks: C = 256 or 128, 128 or more images
+                       (128, 256, 20, 20), (130, 256, 15, 16), (256, 128, 16, 15),
+                       # the small-image kernel at 193..224 positions (25..28 loads)
+                       (256, 128, 14, 14), (129, 256, 13, 15), (64, 512, 14, 16)]:
         what = f"spatial_mean n={n} c={c} {h}x{w}"
         print(f"[edges] {what}", flush=True)
         g = torch.Generator().manual_seed(n * c + h * w)
