@@ -54,7 +54,7 @@ def test_abi_version_and_error_string(lib):
     (lambda l: l.hipo_scaled_bias_softmax_bf16(1, 1, 1, 6, 4, 8, 8, -8, 3, 1.0, None),
      b"mask_batch_stride"),
     (lambda l: l.hipo_spatial_mean_nhwc_bf16(1, 1, 2, 0, 8, None, 0, None), b"spatial"),
-    (lambda l: l.hipo_spatial_mean_nhwc_bf16(16, 16, 128, 4096, 256, None, 0, None), b"workspace"),
+    (lambda l: l.hipo_spatial_mean_nhwc_bf16(16, 16, 64, 4096, 256, None, 0, None), b"workspace"),
     (lambda l: l.hipo_batchnorm_train_fwd_f32(1, 1, 1, 1, 1, 1, 1, 1, 2, 4, 9, 0.1, 1e-5, 1,
                                               1, 0, None), b"workspace"),
     (lambda l: l.hipo_batchnorm_train_fwd_f32(None, 1, 1, 1, 1, 1, 1, 1, 2, 4, 9, 0.1, 1e-5, 1,
@@ -116,8 +116,10 @@ def test_spatial_mean_workspace_bytes(lib):
     # one slice per image when there are enough images or few positions
     assert lib.hipo_spatial_mean_workspace_bytes(128, 36, 1536) == 0
     assert lib.hipo_spatial_mean_workspace_bytes(0, 64, 8) == 0
-    # [128, 256, 64, 64]: two position slices -> fp32 partials [128, 2, 256]
-    assert lib.hipo_spatial_mean_workspace_bytes(128, 4096, 256) == 128 * 2 * 256 * 4
+    # [128, 256, 64, 64]: 16-group channel blocks, 256 workgroups, no slices
+    assert lib.hipo_spatial_mean_workspace_bytes(128, 4096, 256) == 0
+    # [64, 256, 64, 64]: four position slices -> fp32 partials [64, 4, 256]
+    assert lib.hipo_spatial_mean_workspace_bytes(64, 4096, 256) == 64 * 4 * 256 * 4
     # C not a multiple of 8: the scalar kernel, no workspace
     assert lib.hipo_spatial_mean_workspace_bytes(4, 4096, 100) == 0
 
