@@ -333,7 +333,13 @@ BwdPlan bwd_plan(int64_t rows, int64_t cols) {
   } else {
     p.threads = 1024;
     if (p.col_blocks <= 2) {
+      // Long blocks, halved while they would leave most CUs idle (fewer
+      // than 192 workgroups): [8192, 768] 23.5 -> 13.6 us back to back with
+      // 64-row blocks (256 workgroups) instead of 256-row ones (64); at
+      // [25216, 768] and [32768, 1024] (198 and 256 workgroups of 256 rows)
+      // shorter blocks were 1-8 % slower.
       rpb = 256;
+      while (rpb > 32 && (rows + rpb - 1) / rpb * p.col_blocks < 192) rpb /= 2;
     } else {
       const int64_t lo = p.col_blocks <= 8 ? 64 : 32;
       rpb = rows * p.col_blocks / 2048;

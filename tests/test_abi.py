@@ -184,7 +184,8 @@ def test_hold_copy_argument_checks(lib):
 def test_gelu_bwd_workspace_bytes(lib):
     """fp64 column partials, one row per row block: none up to 256 rows (one
     launch); 8-row blocks up to 1024 rows; 256-row blocks for one or two
-    512-column blocks; rows * blocks / 2048 rows held to [64, 128] (up to 8
+    512-column blocks, halved (to 32 at least) while they give fewer than
+    192 workgroups; rows * blocks / 2048 rows held to [64, 128] (up to 8
     column blocks) or [32, 128]."""
     assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(25216, 3072) == 346 * 3072 * 8
     assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(175360, 3072) == 1370 * 3072 * 8
@@ -194,6 +195,12 @@ def test_gelu_bwd_workspace_bytes(lib):
     assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(256, 16) == 0
     assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(257, 3072) == 33 * 3072 * 8
     assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(1000, 16) == 125 * 16 * 8
+    # two column blocks, 8192 rows: 64-row blocks (128 x 2 = 256 workgroups)
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(8192, 768) == 128 * 768 * 8
+    # 25216 rows: 256-row blocks already give 99 x 2 = 198 workgroups
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(25216, 768) == 99 * 768 * 8
+    # 2048 rows of one column block: halved down to the 32-row floor
+    assert lib.hipo_gelu_erf_bwd_colsum_workspace_bytes(2048, 512) == 64 * 512 * 8
     # grid.y holds at most 65535 row blocks: longer tensors get longer blocks
     rows = 10 ** 8
     rpb = -(-rows // 65535)

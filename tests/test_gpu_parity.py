@@ -616,7 +616,7 @@ def test_gelu_erf_bwd_every_bf16_input(rocm_device):
 # 4-wave and 16-wave workgroups with a finishing pass
 GELU_BWD_SHAPES = [(1, 8), (3, 24), (15, 512), (16, 520), (17, 768), (33, 1032), (100, 3072),
                    (128, 72), (129, 3072), (256, 1040), (257, 3072), (1000, 10240), (1024, 520),
-                   (4099, 64), (5000, 1024), (200003, 16)]
+                   (4099, 64), (5000, 1024), (8192, 768), (200003, 16)]
 
 
 @pytest.mark.parametrize("rows,cols", GELU_BWD_SHAPES)
