@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-5b248c57, oracle 52.31 us, Inductor 63.43 us (ratio 1.213, GOOD); over the dir's 2
-registered points: 2 GOOD.
+5b248c57, oracle 52.75 us, Inductor 62.75 us (ratio 1.19, GOOD); over the dir's 2
+registered points: 1 AT_FLOOR, 1 GOOD.
 
 MI355X oracle for amax_sum_fa4cc85fe5ad: the plain attention softmax of T5 /
 MT5 (no bias, no scale), bf16 in and out, fp32 statistics.

@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-111af936, oracle 16.84 us, Inductor 17.32 us (ratio 1.029, AT_FLOOR); over the dir's 2
+111af936, oracle 16.88 us, Inductor 17.28 us (ratio 1.024, AT_FLOOR); over the dir's 2
 registered points: 2 AT_FLOOR.
 
 MI355X oracle for mean_c033ad4c69ca: residual add + RMSNorm over the last

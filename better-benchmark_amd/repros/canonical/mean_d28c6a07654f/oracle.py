@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-111af936, oracle 17.04 us, Inductor 17.16 us (ratio 1.007, AT_FLOOR); over the dir's 2
+111af936, oracle 16.68 us, Inductor 17.24 us (ratio 1.034, AT_FLOOR); over the dir's 2
 registered points: 2 AT_FLOOR.
 
 MI355X oracle for mean_d28c6a07654f: residual add + RMSNorm over the last

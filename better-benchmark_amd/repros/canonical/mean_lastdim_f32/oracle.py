@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-b84ae979, oracle 29.6 us, Inductor 30.68 us (ratio 1.037, AT_FLOOR); over the dir's 3
+b84ae979, oracle 29.88 us, Inductor 30.72 us (ratio 1.028, AT_FLOOR); over the dir's 3
 registered points: 3 AT_FLOOR.
 
 MI355X oracle for mean_lastdim_f32: x.mean(dim=-1) on fp32 [R, C].

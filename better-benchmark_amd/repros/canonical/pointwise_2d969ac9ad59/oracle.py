@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-8f687505, oracle 68.79 us, Inductor 67.39 us (ratio 0.98, AT_FLOOR); over the dir's 6
+8f687505, oracle 68.39 us, Inductor 66.91 us (ratio 0.978, AT_FLOOR); over the dir's 6
 registered points: 4 GOOD, 2 AT_FLOOR.
 
 MI355X oracle for pointwise_2d969ac9ad59: tanh GELU of a contiguous bf16 or

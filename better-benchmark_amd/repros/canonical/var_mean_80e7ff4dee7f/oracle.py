@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-1cea4d76, oracle 18.0 us, Inductor 17.2 us (ratio 0.956, AT_FLOOR); over the dir's 1
+1cea4d76, oracle 17.76 us, Inductor 17.36 us (ratio 0.977, AT_FLOOR); over the dir's 1
 registered points: 1 AT_FLOOR.
 
 MI355X oracle for var_mean_80e7ff4dee7f: residual add + LayerNorm, y only.

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-c4bf51cc, oracle 27.88 us, Inductor 29.4 us (ratio 1.055, GOOD); over the dir's 11
-registered points: 8 AT_FLOOR, 3 GOOD; 5 points withdrawn (WITHDRAWN_POINTS).
+c4bf51cc, oracle 27.8 us, Inductor 29.24 us (ratio 1.052, GOOD); over the dir's 11
+registered points: 9 AT_FLOOR, 2 GOOD; 5 points withdrawn (WITHDRAWN_POINTS).
 
 MI355X oracle for var_mean_f4578c128d74: residual add + LayerNorm over the
 last dim (eps 1e-06), returning the bf16 sum h and y.
