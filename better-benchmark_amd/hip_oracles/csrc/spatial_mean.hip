@@ -143,10 +143,19 @@ __global__ __launch_bounds__(256) void spatial_mean_small_waves(
       acc[2 * d + 1] += in ? bf16hi(v[k][d]) : 0.f;
     }
   }
+  // Add lanes 8, 16 and 32 apart (the same pairs as xor shuffles, so the same
+  // sums): row_ror:8 within each 16-lane row, then gfx950's permlane swaps,
+  // which hand every lane its partner's value without an LDS round trip.
+  static_assert(G == 8, "the combine adds lanes 8 apart first");
 #pragma unroll
-  for (int off = G; off < kWave; off *= 2) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], off);
+  for (int e = 0; e < 8; ++e) {
+    acc[e] += dpp<kDppRowRor8>(acc[e]);
+    const auto h = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[e]),
+                                                    __float_as_uint(acc[e]), false, false);
+    acc[e] = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+    const auto w = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[e]),
+                                                    __float_as_uint(acc[e]), false, false);
+    acc[e] = __uint_as_float(w[0]) + __uint_as_float(w[1]);
   }
   if (ok && lane < G) {
     const float inv = 1.0f / static_cast<float>(P);
