@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-38831ee4, oracle 56.75 us, Inductor 118.59 us (ratio 2.09, GOOD); over the dir's 1
+38831ee4, oracle 56.71 us, Inductor 119.35 us (ratio 2.104, GOOD); over the dir's 1
 registered points: 1 GOOD.
 
 MI355X oracle for amax_sum_20ccc18dda60: softmax(scores + bias) with the

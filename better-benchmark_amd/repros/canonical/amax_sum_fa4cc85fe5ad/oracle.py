@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-5b248c57, oracle 52.75 us, Inductor 62.75 us (ratio 1.19, GOOD); over the dir's 2
+5b248c57, oracle 53.11 us, Inductor 63.99 us (ratio 1.205, GOOD); over the dir's 2
 registered points: 1 AT_FLOOR, 1 GOOD.
 
 MI355X oracle for amax_sum_fa4cc85fe5ad: the plain attention softmax of T5 /

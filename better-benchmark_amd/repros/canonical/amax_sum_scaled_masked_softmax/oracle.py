@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-134a1d74, oracle 262.05 us, Inductor 294.25 us (ratio 1.123, GOOD); over the dir's 3
+134a1d74, oracle 262.53 us, Inductor 296.85 us (ratio 1.131, GOOD); over the dir's 3
 registered points: 2 AT_FLOOR, 1 GOOD.
 
 MI355X oracle for amax_sum_scaled_masked_softmax:

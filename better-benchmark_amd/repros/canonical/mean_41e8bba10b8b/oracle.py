@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-841ed042, oracle 13.88 us, Inductor 14.84 us (ratio 1.069, GOOD); over the dir's 1
-registered points: 1 GOOD.
+841ed042, oracle 14.08 us, Inductor 14.76 us (ratio 1.048, AT_FLOOR); over the dir's 1
+registered points: 1 AT_FLOOR.
 
 MI355X oracle for mean_41e8bba10b8b: residual add + RMSNorm over the last
 dim (eps 1e-06), returning the bf16 sum h and 2 views of y.

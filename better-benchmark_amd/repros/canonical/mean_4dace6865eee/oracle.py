@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-40057a60, oracle 15.48 us, Inductor 15.56 us (ratio 1.005, AT_FLOOR); over the dir's 1
+40057a60, oracle 15.12 us, Inductor 14.64 us (ratio 0.968, AT_FLOOR); over the dir's 1
 registered points: 1 AT_FLOOR.
 
 MI355X oracle for mean_4dace6865eee: residual add + RMSNorm over the last

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-40057a60, oracle 16.64 us, Inductor 16.28 us (ratio 0.978, AT_FLOOR); over the dir's 2
-registered points: 1 GOOD, 1 AT_FLOOR.
+40057a60, oracle 17.2 us, Inductor 16.6 us (ratio 0.965, AT_FLOOR); over the dir's 2
+registered points: 2 AT_FLOOR.
 
 MI355X oracle for mean_8818e35b12aa: residual add + RMSNorm over the last
 dim (eps 1e-06), returning the bf16 sum h and 1 view of y.

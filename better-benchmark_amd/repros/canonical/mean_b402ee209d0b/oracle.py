@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-dad91233, oracle 13.6 us, Inductor 13.52 us (ratio 0.994, AT_FLOOR); over the dir's 1
+dad91233, oracle 13.56 us, Inductor 13.64 us (ratio 1.006, AT_FLOOR); over the dir's 1
 registered points: 1 AT_FLOOR.
 
 MI355X oracle for mean_b402ee209d0b: relu(x).mean([-1, -2]) of a contiguous

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-40057a60, oracle 16.64 us, Inductor 16.88 us (ratio 1.014, AT_FLOOR); over the dir's 2
-registered points: 1 GOOD, 1 AT_FLOOR.
+40057a60, oracle 17.0 us, Inductor 16.88 us (ratio 0.993, AT_FLOOR); over the dir's 2
+registered points: 2 AT_FLOOR.
 
 MI355X oracle for mean_bf2ed36e56df: residual add + RMSNorm over the last
 dim (eps 1e-06), returning the bf16 sum h and 3 views of y.

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-111af936, oracle 16.88 us, Inductor 17.28 us (ratio 1.024, AT_FLOOR); over the dir's 2
-registered points: 2 AT_FLOOR.
+111af936, oracle 16.8 us, Inductor 18.28 us (ratio 1.088, GOOD); over the dir's 2
+registered points: 1 AT_FLOOR, 1 GOOD.
 
 MI355X oracle for mean_c033ad4c69ca: residual add + RMSNorm over the last
 dim (eps 1e-06), returning the bf16 sum h and 3 views of y.

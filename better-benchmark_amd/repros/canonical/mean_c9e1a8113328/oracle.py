@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-2150fa2c, oracle 62.43 us, Inductor 67.27 us (ratio 1.078, GOOD); over the dir's 16
-registered points: 9 AT_FLOOR, 7 GOOD.
+2150fa2c, oracle 61.63 us, Inductor 65.11 us (ratio 1.056, GOOD); over the dir's 16
+registered points: 10 AT_FLOOR, 6 GOOD.
 
 MI355X oracle for mean_c9e1a8113328: spatial mean of a channels-last bf16
 tensor over H, W (keepdim).

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-111af936, oracle 16.68 us, Inductor 17.24 us (ratio 1.034, AT_FLOOR); over the dir's 2
-registered points: 2 AT_FLOOR.
+111af936, oracle 16.92 us, Inductor 17.88 us (ratio 1.057, GOOD); over the dir's 2
+registered points: 1 AT_FLOOR, 1 GOOD.
 
 MI355X oracle for mean_d28c6a07654f: residual add + RMSNorm over the last
 dim (eps 1e-06), returning the bf16 sum h and 2 views of y.

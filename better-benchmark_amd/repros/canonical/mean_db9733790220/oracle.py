@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-111af936, oracle 15.56 us, Inductor 15.76 us (ratio 1.013, AT_FLOOR); over the dir's 2
+111af936, oracle 15.56 us, Inductor 16.24 us (ratio 1.044, AT_FLOOR); over the dir's 2
 registered points: 2 AT_FLOOR.
 
 MI355X oracle for mean_db9733790220: residual add + RMSNorm over the last

@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-841ed042, oracle 13.6 us, Inductor 13.68 us (ratio 1.006, AT_FLOOR); over the dir's 1
+841ed042, oracle 13.8 us, Inductor 14.12 us (ratio 1.023, AT_FLOOR); over the dir's 1
 registered points: 1 AT_FLOOR.
 
 MI355X oracle for mean_f08c75b5f21f: residual add + RMSNorm over the last

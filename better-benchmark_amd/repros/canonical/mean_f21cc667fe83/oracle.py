@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-533b2091, oracle 15.68 us, Inductor 15.48 us (ratio 0.987, AT_FLOOR); over the dir's 1
+533b2091, oracle 15.8 us, Inductor 15.92 us (ratio 1.008, AT_FLOOR); over the dir's 1
 registered points: 1 AT_FLOOR.
 
 MI355X oracle for mean_f21cc667fe83: residual add + RMSNorm over the last

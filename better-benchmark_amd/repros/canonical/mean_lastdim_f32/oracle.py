@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-b84ae979, oracle 29.88 us, Inductor 30.72 us (ratio 1.028, AT_FLOOR); over the dir's 3
-registered points: 3 AT_FLOOR.
+b84ae979, oracle 29.88 us, Inductor 30.04 us (ratio 1.005, AT_FLOOR); over the dir's 3
+registered points: 2 AT_FLOOR, 1 BAD_ORACLE.
 
 MI355X oracle for mean_lastdim_f32: x.mean(dim=-1) on fp32 [R, C].
 

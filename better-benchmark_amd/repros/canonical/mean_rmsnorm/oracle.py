@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-0390a437, oracle 53.35 us, Inductor 51.35 us (ratio 0.963, AT_FLOOR); over the dir's 3
+0390a437, oracle 53.35 us, Inductor 51.31 us (ratio 0.962, AT_FLOOR); over the dir's 3
 registered points: 3 AT_FLOOR.
 
 MI355X oracle for mean_rmsnorm: y = x * rsqrt(mean(x^2) + eps) * gamma, rstd.

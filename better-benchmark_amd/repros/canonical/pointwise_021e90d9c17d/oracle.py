@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-918a77e3, oracle 16.44 us, Inductor 17.52 us (ratio 1.066, GOOD); over the dir's 2
+918a77e3, oracle 16.48 us, Inductor 17.56 us (ratio 1.066, GOOD); over the dir's 2
 registered points: 2 GOOD.
 
 MI355X oracle for pointwise_021e90d9c17d: [B, heads, N, D] -> contiguous

@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-8f687505, oracle 68.39 us, Inductor 66.91 us (ratio 0.978, AT_FLOOR); over the dir's 6
-registered points: 4 GOOD, 2 AT_FLOOR.
+8f687505, oracle 68.43 us, Inductor 67.27 us (ratio 0.983, AT_FLOOR); over the dir's 6
+registered points: 5 GOOD, 1 AT_FLOOR.
 
 MI355X oracle for pointwise_2d969ac9ad59: tanh GELU of a contiguous bf16 or
 fp32 activation, returned in the second view's shape.

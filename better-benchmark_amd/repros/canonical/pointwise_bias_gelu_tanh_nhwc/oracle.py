@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-8d22dcbf, oracle 75.79 us, Inductor 92.67 us (ratio 1.223, GOOD); over the dir's 3
+8d22dcbf, oracle 76.47 us, Inductor 93.63 us (ratio 1.224, GOOD); over the dir's 3
 registered points: 2 AT_FLOOR, 1 GOOD.
 
 MI355X oracle for pointwise_bias_gelu_tanh_nhwc:

@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-3f451298, oracle 557.97 us, Inductor 759.79 us (ratio 1.362, GOOD); over the dir's 14
+3f451298, oracle 552.38 us, Inductor 759.91 us (ratio 1.376, GOOD); over the dir's 14
 registered points: 14 GOOD; 1 points withdrawn (WITHDRAWN_POINTS).
 
 MI355X oracle for sum_139a3020e8bf: the gradient through an erf GELU, y = bf16(grad *

@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-c4bf51cc, oracle 23.0 us, Inductor 27.2 us (ratio 1.183, GOOD); over the dir's 9
+c4bf51cc, oracle 23.52 us, Inductor 28.28 us (ratio 1.202, GOOD); over the dir's 9
 registered points: 6 AT_FLOOR, 3 GOOD; 4 points withdrawn (WITHDRAWN_POINTS).
 
 MI355X oracle for var_mean_0ada225c0a04: residual add + LayerNorm over the

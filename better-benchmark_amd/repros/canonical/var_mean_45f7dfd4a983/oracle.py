@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-d4701d13, oracle 28.0 us, Inductor 33.32 us (ratio 1.19, GOOD); over the dir's 2
+d4701d13, oracle 28.0 us, Inductor 32.96 us (ratio 1.177, GOOD); over the dir's 2
 registered points: 1 GOOD, 1 AT_FLOOR; 3 points withdrawn (WITHDRAWN_POINTS).
 
 MI355X oracle for var_mean_45f7dfd4a983: residual add + LayerNorm over the

@@ -2,8 +2,12 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-1cea4d76, oracle 17.76 us, Inductor 17.36 us (ratio 0.977, AT_FLOOR); over the dir's 1
-registered points: 1 AT_FLOOR.
+1cea4d76, oracle 18.24 us, Inductor 17.0 us (ratio 0.932, BAD_ORACLE); over the dir's 1
+registered points: 1 BAD_ORACLE.  The ten sweeps before measured 0.949-0.982; the
+fastest oracle run against the fastest Inductor run over all eleven gives 0.959, above
+the 0.95 below which a point is withdrawn, so it stays registered.  Back to back (inputs
+rotating through 1.2 GB) Inductor's tuned kernel is faster at this shape, 7.65 against
+8.42 us; one- or two-row workgroups and two rows per wave took 8.6-8.9 us.
 
 MI355X oracle for var_mean_80e7ff4dee7f: residual add + LayerNorm, y only.
 

@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-d4701d13, oracle 27.88 us, Inductor 32.76 us (ratio 1.175, GOOD); over the dir's 3
+d4701d13, oracle 28.08 us, Inductor 33.4 us (ratio 1.189, GOOD); over the dir's 3
 registered points: 2 GOOD, 1 AT_FLOOR; 2 points withdrawn (WITHDRAWN_POINTS).
 
 MI355X oracle for var_mean_96edf0542ecd: residual add + LayerNorm over the

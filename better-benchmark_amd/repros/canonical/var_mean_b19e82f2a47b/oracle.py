@@ -2,8 +2,8 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-c4bf51cc, oracle 28.08 us, Inductor 29.36 us (ratio 1.046, AT_FLOOR); over the dir's 8
-registered points: 4 AT_FLOOR, 4 GOOD; 1 points withdrawn (WITHDRAWN_POINTS).
+c4bf51cc, oracle 28.12 us, Inductor 29.36 us (ratio 1.044, AT_FLOOR); over the dir's 8
+registered points: 6 AT_FLOOR, 2 GOOD; 1 points withdrawn (WITHDRAWN_POINTS).
 
 MI355X oracle for var_mean_b19e82f2a47b: residual add + LayerNorm over the
 last dim (eps 1e-05), returning the bf16 sum h and three [R, C] views of y.

@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-ce16d05d, oracle 160.94 us, Inductor 206.7 us (ratio 1.284, GOOD); over the dir's 3
+ce16d05d, oracle 160.26 us, Inductor 206.42 us (ratio 1.288, GOOD); over the dir's 3
 registered points: 2 AT_FLOOR, 1 GOOD.
 
 MI355X oracle for var_mean_batchnorm_train_relu: BatchNorm training forward

@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-8026229d, oracle 163.46 us, Inductor 432.91 us (ratio 2.648, GOOD); over the dir's 2
+8026229d, oracle 163.82 us, Inductor 429.35 us (ratio 2.621, GOOD); over the dir's 2
 registered points: 2 GOOD.
 
 MI355X oracle for var_mean_ceb5c315290a: BatchNorm training forward of a

@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-c4bf51cc, oracle 27.8 us, Inductor 29.24 us (ratio 1.052, GOOD); over the dir's 11
+c4bf51cc, oracle 28.28 us, Inductor 29.6 us (ratio 1.047, AT_FLOOR); over the dir's 11
 registered points: 9 AT_FLOOR, 2 GOOD; 5 points withdrawn (WITHDRAWN_POINTS).
 
 MI355X oracle for var_mean_f4578c128d74: residual add + LayerNorm over the

@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-5b9efb9c, oracle 19.6 us, Inductor 26.24 us (ratio 1.339, GOOD); over the dir's 1
+5b9efb9c, oracle 19.76 us, Inductor 26.68 us (ratio 1.35, GOOD); over the dir's 1
 registered points: 1 GOOD.
 
 MI355X oracle for var_mean_mean_19ffdb35cc67: BatchNorm training forward of

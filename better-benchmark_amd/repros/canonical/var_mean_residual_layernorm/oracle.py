@@ -2,7 +2,7 @@
 
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
-fe9bbcba, oracle 97.87 us, Inductor 106.79 us (ratio 1.091, NUMERICS_OPTOUT_ACCEPTED);
+fe9bbcba, oracle 98.23 us, Inductor 106.71 us (ratio 1.086, NUMERICS_OPTOUT_ACCEPTED);
 over the dir's 3 registered points: 3 NUMERICS_OPTOUT_ACCEPTED.
 
 MI355X oracle for var_mean_residual_layernorm:
