@@ -81,8 +81,23 @@ __global__ __launch_bounds__(256) void row_mean_f32_scalar(
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const float* p = x + row * row_stride;
+  // Eight loads per lane in flight before any add (one at a time, every
+  // iteration waited a full memory latency); the adds keep the order
+  // i = lane, lane + 64, ... and skip what lies past the row, so the sum is
+  // the same as a one-by-one loop's.
+  constexpr int kBatch = 8;
   float acc = 0.f;
-  for (int64_t i = lane; i < cols; i += kWave) acc += p[i];
+  for (int64_t i0 = lane; i0 < cols; i0 += int64_t{kWave} * kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int64_t i = i0 + int64_t{k} * kWave;
+      v[k] = i < cols ? p[i] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+      if (i0 + int64_t{k} * kWave < cols) acc += v[k];
+  }
   const float s = wave_sum(acc);
   if (lane == 0) out[row] = s / static_cast<float>(cols);
 }

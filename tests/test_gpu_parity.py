@@ -378,6 +378,13 @@ def test_row_mean_edges(rocm_device):
     # exact small integers: sum is exact, so the mean is exact
     x = torch.randint(-8, 8, (33, 4096)).float()
     assert torch.equal(hip_oracles.row_mean(x.to(rocm_device)).cpu(), x.sum(1) / 4096)
+    # scalar path (cols % 4 != 0), eight loads per lane at a time: the same
+    # exact check at one partial batch, several batches and a ragged last one
+    for r, c in ((7, 333), (2, 63), (5, 513), (3, 4097)):
+        x = torch.randint(-8, 8, (r, c)).float()
+        assert torch.equal(hip_oracles.row_mean(x.to(rocm_device)).cpu(), x.sum(1) / c), (r, c)
+    x = torch.randn(7, 333)
+    assert_close(hip_oracles.row_mean(x.to(rocm_device)), ref.row_mean(x), F32_TOL, "7x333")
 
 
 def test_bias_gelu_edges(rocm_device):
