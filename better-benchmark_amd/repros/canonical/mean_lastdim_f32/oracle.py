@@ -3,7 +3,9 @@
 Measured on one MI355X (oracle_harness.bench_oracle: graph replay after a 1 GiB read
 flush, min over rounds; Inductor with coordinate-descent tuning): at the largest point
 b84ae979, oracle 29.88 us, Inductor 30.04 us (ratio 1.005, AT_FLOOR); over the dir's 3
-registered points: 2 AT_FLOOR, 1 BAD_ORACLE.
+registered points: 2 AT_FLOOR, 1 BAD_ORACLE.  That one, [7, 333] at 0.941, was the
+scalar kernel issuing one load at a time; with eight loads per lane in flight the
+same protocol measured 0.994 and 1.003 (12.92-13.04 us against 12.96), AT_FLOOR.
 
 MI355X oracle for mean_lastdim_f32: x.mean(dim=-1) on fp32 [R, C].
 
